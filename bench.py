@@ -1,0 +1,349 @@
+"""Benchmark of the paged-KV hot path on one MI355X.
+
+Headline (value): paged decode attention GB/s at the Llama-3-8B decode shape
+(C2: 256 sequences, context U[512, 8192], 32 q-heads / 8 kv-heads, D=128,
+bf16 KV, block_size 16).  A step is one batched decode pass over all 256
+sequences; inputs are resident in HBM before the timed region.  The same run
+also measures the chunked-prefill KV append (C3: 64 x 512 tokens at
+non-aligned offsets, bf16) and the fp8-KV decode (C5: 512 sequences, context
+U[1024, 16384]) and reports them as extra fields.
+
+Algorithmic bytes (unique bytes that must cross HBM):
+  decode  sum(ctx) * 2 * Hkv * D * elt  + Q + O + block-table entries + seq_lens
+  append  2 * T * Hkv * D * elt (read)  + the same (write) + T * 8 (int64 slots)
+The roofline object is for the dominant kernel (decode_partials): its bytes
+are the KV bytes + Q + table entries + seq_lens, divided by its mean launch
+duration from hipEvents recorded around each launch during the timed region.
+
+cpu_baseline: the CPU oracle's faithful scalar decode (oracle/zk_oracle.c,
+restating src/attention/mod.rs:64-98 over the pages) timed on this host on a
+bounded sample of the same workload (the first 64 sequences' context lengths),
+single-threaded; the OpenMP figure over all host cores is reported beside it.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBPS = 8000.0
+SEED = 20261201
+METRIC = "paged decode attn GB/s (% of HBM peak) + KV append GB/s, Llama-3-8B shape"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def paged_tables(rng, lens, bs, slack=0.10):
+    pages = [(int(L) + bs - 1) // bs for L in lens]
+    nb = int(math.ceil(sum(pages) * (1 + slack))) + 1
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = -np.ones((len(lens), max(pages)), np.int32)
+    o = 0
+    for n, p in enumerate(pages):
+        bt[n, :p] = perm[o:o + p]
+        o += p
+    return bt, nb, sum(pages)
+
+
+def timed(fn, steps, warmup, torch):
+    """Runs fn warmup times, then times exactly `steps` calls with events on the
+    current stream, bracketed by synchronize() on both sides. Returns ms/step."""
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(steps):
+        fn(i)
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def kernel_ms(lib, name):
+    import ctypes
+    n = ctypes.c_int64()
+    ms = ctypes.c_double()
+    rc = lib.zk_timing_query(name.encode(), ctypes.byref(n), ctypes.byref(ms))
+    assert rc == 0
+    return (ms.value / n.value if n.value else float("nan")), n.value
+
+
+# ---------------------------------------------------------------- C2 decode
+
+def bench_decode(args, torch, ops, lib, kv="bf16"):
+    if kv == "bf16":
+        N, lo, hi = 256, 512, 8192
+    else:
+        N, lo, hi = 512, 1024, 16384
+    H, Hkv, D, BS = 32, 8, 128, 16
+    rng = np.random.default_rng(SEED + (0 if kv == "bf16" else 5))
+    lens = rng.integers(lo, hi + 1, N)
+    bt, nb, npages = paged_tables(rng, lens, BS)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    log(f"decode {kv}: N={N} sum_ctx={int(lens.sum())} blocks={nb}")
+    q = torch.randn((N, H, D), generator=g, device=dev).to(torch.bfloat16)
+    btd = torch.from_numpy(bt).to(dev)
+    lensd = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    elt = 2 if kv == "bf16" else 1
+    ks = vs = None
+    if kv == "bf16":
+        kp = torch.randn((nb, Hkv, BS, D), generator=g, device=dev).to(torch.bfloat16)
+        vp = torch.randn((nb, Hkv, BS, D), generator=g, device=dev).to(torch.bfloat16)
+    else:
+        # quantise on append: bf16 N(0,1) K/V, per-(seq, head) amax scales
+        kp = torch.zeros((nb, Hkv, BS, D), dtype=torch.uint8, device=dev)
+        vp = torch.zeros_like(kp)
+        ks = torch.empty((N, Hkv), dtype=torch.float32, device=dev)
+        vs = torch.empty_like(ks)
+        for n0 in range(0, N, 32):
+            n1 = min(N, n0 + 32)
+            L = lens[n0:n1]
+            T = int(L.sum())
+            kx = torch.randn((T, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+            vx = torch.randn((T, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+            cu = torch.from_numpy(np.concatenate([[0], np.cumsum(L)]).astype(np.int64)).to(dev)
+            ks[n0:n1] = ops.fp8_scales(kx, cu)
+            vs[n0:n1] = ops.fp8_scales(vx, cu)
+            slots = np.concatenate([bt[n, np.arange(l) // BS].astype(np.int64) * BS + np.arange(l) % BS
+                                    for n, l in zip(range(n0, n1), L)])
+            rows = np.repeat(np.arange(n0, n1), L).astype(np.int32)
+            ops.append(kp, vp, kx, vx, torch.from_numpy(slots).to(dev), k_scales=ks, v_scales=vs,
+                       token_row=torch.from_numpy(rows).to(dev))
+            del kx, vx
+        torch.cuda.synchronize()
+    out = torch.empty_like(q)
+    ws = torch.empty(ops.decode_workspace_bytes(N, H, D, bt.shape[1], BS), dtype=torch.uint8, device=dev)
+
+    def step(_):
+        ops.paged_decode(q, kp, vp, btd, lensd, k_scales=ks, v_scales=vs, out=out, workspace=ws)
+
+    lib.zk_timing_reset()
+    lib.zk_timing_enable(1)
+    ms = timed(step, args.steps, args.warmup, torch)
+    lib.zk_timing_enable(0)
+    k_ms, k_n = kernel_ms(lib, "decode_partials")
+    r_ms, _ = kernel_ms(lib, "decode_reduce")
+    i_ms, _ = kernel_ms(lib, "decode_seq_info")
+    lib.zk_timing_reset()
+    sum_ctx = int(lens.sum())
+    kv_bytes = sum_ctx * 2 * Hkv * D * elt
+    q_bytes = N * H * D * 2
+    small = npages * 4 + N * 4 + (2 * N * Hkv * 4 if kv != "bf16" else 0)
+    alg = kv_bytes + 2 * q_bytes + small
+    alg_kernel = kv_bytes + q_bytes + small
+    gbps = alg / (ms * 1e-3) / 1e9
+    kgbps = alg_kernel / (k_ms * 1e-3) / 1e9
+    torch.cuda.synchronize()
+    res = {
+        "ms_per_step": ms, "gbps": gbps, "frac_of_peak": gbps / PEAK_HBM_GBPS,
+        "new_tokens_per_s": N / (ms * 1e-3), "context_tokens_per_s": sum_ctx / (ms * 1e-3),
+        "algorithmic_bytes": alg, "sum_ctx": sum_ctx, "num_seqs": N,
+        "kernel_ms": {"decode_partials": k_ms, "decode_reduce": r_ms, "decode_seq_info": i_ms},
+        "roofline": {"bound": "hbm", "achieved": kgbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": kgbps / PEAK_HBM_GBPS, "traffic": None,
+                     "kernel": "decode_partials", "kernel_bytes_per_launch": alg_kernel,
+                     "launches": k_n},
+    }
+    del kp, vp, q, out, ws
+    torch.cuda.empty_cache()
+    return res, lens
+
+
+# ---------------------------------------------------------------- C3 append
+
+def bench_append(args, torch, ops, lib):
+    Nseq, C, Hkv, D, BS = 64, 512, 8, 128, 16
+    R = 4  # rotating buffer sets: 4 x 256 MiB moved > 256 MB Infinity Cache
+    rng = np.random.default_rng(SEED + 1)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(SEED + 1)
+    sets = []
+    total_blocks = 0
+    tables = []
+    for r in range(R):
+        starts = rng.integers(0, 4096, Nseq)
+        starts[starts % BS == 0] += 1
+        pages = [(int(s) + C + BS - 1) // BS for s in starts]
+        tables.append((starts, pages, total_blocks))
+        total_blocks += sum(pages)
+    nb = int(total_blocks * 1.1) + 1
+    perm = rng.permutation(nb)
+    kp = torch.zeros((nb, Hkv, BS, D), dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros_like(kp)
+    T = Nseq * C
+    for starts, pages, base in tables:
+        blocks = perm[base: base + sum(pages)]
+        o = 0
+        slots = []
+        for s, p in zip(starts, pages):
+            row = blocks[o:o + p]
+            o += p
+            gpos = int(s) + np.arange(C)
+            slots.append(row[gpos // BS].astype(np.int64) * BS + gpos % BS)
+        k = torch.randn((T, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((T, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+        sets.append((k, v, torch.from_numpy(np.concatenate(slots)).to(dev)))
+    log(f"append bf16: T={T} rotating sets={R} pool blocks={nb}")
+
+    def step(i):
+        k, v, s = sets[i % R]
+        ops.append(kp, vp, k, v, s)
+
+    lib.zk_timing_reset()
+    lib.zk_timing_enable(1)
+    ms = timed(step, args.steps, args.warmup, torch)
+    lib.zk_timing_enable(0)
+    k_ms, k_n = kernel_ms(lib, "append")
+    lib.zk_timing_reset()
+    alg = 2 * (2 * T * Hkv * D * 2) + T * 8
+    gbps = alg / (ms * 1e-3) / 1e9
+    kgbps = alg / (k_ms * 1e-3) / 1e9
+    # in-repo streaming copy of the same byte count, as the attainable yardstick
+    nbytes = 2 * T * Hkv * D * 2
+    a = torch.empty(nbytes * R, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    import ctypes
+
+    def cp(i):
+        off = (i % R) * nbytes
+        lib.zk_stream_copy(ctypes.c_void_p(b.data_ptr() + off), ctypes.c_void_p(a.data_ptr() + off),
+                           nbytes, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+    cms = timed(cp, args.steps, args.warmup, torch)
+    copy_gbps = 2 * nbytes / (cms * 1e-3) / 1e9
+    res = {"ms_per_step": ms, "gbps": gbps, "frac_of_peak": gbps / PEAK_HBM_GBPS,
+           "tokens_per_s": T / (ms * 1e-3), "algorithmic_bytes": alg,
+           "stream_copy_gbps": copy_gbps, "frac_of_stream_copy": gbps / copy_gbps,
+           "roofline": {"bound": "hbm", "achieved": kgbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                        "frac": kgbps / PEAK_HBM_GBPS, "traffic": None, "kernel": "append",
+                        "launches": k_n}}
+    del sets, kp, vp, a, b
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(lens_all, sample_seqs):
+    import oracle
+    H, Hkv, D, BS = 32, 8, 128, 16
+    rng = np.random.default_rng(SEED + 2)
+    lens = [int(x) for x in lens_all[:sample_seqs]]
+    bt, nb, _ = paged_tables(rng, lens, BS)
+    kp = oracle.bf16_bits_from_f32(rng.standard_normal((nb, Hkv, BS, D), dtype=np.float32)).reshape(nb, Hkv, BS, D)
+    vp = oracle.bf16_bits_from_f32(rng.standard_normal((nb, Hkv, BS, D), dtype=np.float32)).reshape(nb, Hkv, BS, D)
+    q = oracle.f32_from_bf16_bits(oracle.bf16_bits_from_f32(
+        rng.standard_normal((len(lens), H, D), dtype=np.float32))).reshape(len(lens), H, D)
+    scale = np.float32(1 / math.sqrt(D))
+    alg = sum(lens) * 2 * Hkv * D * 2 + 2 * len(lens) * H * D * 2
+    t0 = time.perf_counter()
+    oracle.paged_decode(q, kp, vp, oracle.BF16, bt, lens, Hkv, D, BS, scale, threads=1)
+    t1 = time.perf_counter() - t0
+    cores = os.cpu_count() or 1
+    t0 = time.perf_counter()
+    oracle.paged_decode(q, kp, vp, oracle.BF16, bt, lens, Hkv, D, BS, scale, threads=cores)
+    tn = time.perf_counter() - t0
+    return {"value": alg / t1 / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"C2 decode, first {len(lens)} of the 256 context lengths (sum_ctx={sum(lens)}), "
+                      f"bf16 KV, scalar fp32 loops of oracle/zk_oracle.c, {t1:.2f} s",
+            "omp_value": alg / tn / 1e9, "omp_cores": cores, "host_cpu": cpu_model()}
+
+
+# ---------------------------------------------------------------- main
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["decode", "append", "fp8"], default=None,
+                    help="run one workload (for profiler passes)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-seqs", type=int, default=64)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the decode shards by sequence / kv-head with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    import zealot_amd
+    from zealot_amd import ops
+    lib = zealot_amd.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    result = {}
+    dec = lens = app = fp8 = None
+    if args.only in (None, "decode"):
+        dec, lens = bench_decode(args, torch, ops, lib, "bf16")
+        log(f"decode bf16: {dec['ms_per_step']:.4f} ms {dec['gbps']:.1f} GB/s")
+    if args.only in (None, "append"):
+        app = bench_append(args, torch, ops, lib)
+        log(f"append bf16: {app['ms_per_step'] * 1e3:.2f} us {app['gbps']:.1f} GB/s")
+    if args.only in (None, "fp8"):
+        fp8, _ = bench_decode(args, torch, ops, lib, "fp8")
+        log(f"decode fp8: {fp8['ms_per_step']:.4f} ms {fp8['gbps']:.1f} GB/s")
+    cpu = None
+    if args.only is None and not args.no_cpu_baseline:
+        cpu = cpu_baseline(lens, args.cpu_sample_seqs)
+        log(f"cpu baseline: {cpu['value']:.3f} GB/s (1 core), {cpu['omp_value']:.2f} GB/s ({cpu['omp_cores']} cores)")
+    head = dec if dec is not None else (app if app is not None else fp8)
+    result = {
+        "metric": METRIC,
+        "value": round(head["gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,1) bf16 Q/K/V (seeded torch/numpy generators), random non-contiguous block tables",
+        "config": {"workload": "C2 paged decode, Llama-3-8B shape: 256 seqs, ctx U[512,8192], "
+                               "32 q-heads / 8 kv-heads, head_dim 128, block_size 16, bf16 KV, one query per seq",
+                   "num_seqs": 256, "num_heads": 32, "num_kv_heads": 8, "head_dim": 128,
+                   "block_size": 16, "seed": SEED, "parallelism": "single GPU"},
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "decode_bf16": dec,
+        "append_bf16": app,
+        "decode_fp8": fp8,
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    if args.only is not None:
+        result["config"]["workload"] = f"--only {args.only}"
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,84 @@
+"""Helpers shared by the GPU parity tests: seeded inputs, host<->device copies.
+
+Inputs are generated on the host with numpy (PCG64, seeded) and fed identically
+to the HIP path and to the oracle.  bf16 data is carried as uint16 bit patterns
+on the host and as torch.bfloat16 on the device; fp8 pools as uint8.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+import oracle
+
+DEV = "cuda"
+
+
+def to_dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(DEV)
+    return torch.from_numpy(a).to(DEV)
+
+
+def to_host(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    if t.dtype == getattr(torch, "float8_e4m3fn", None):
+        return t.view(torch.uint8).cpu().numpy()
+    return t.cpu().numpy()
+
+
+def as_f32(a: np.ndarray, dtype: int) -> np.ndarray:
+    """Values of a host array of the given oracle dtype, as float32."""
+    if dtype == oracle.BF16:
+        return oracle.f32_from_bf16_bits(a).reshape(a.shape)
+    if dtype == oracle.FP8:
+        return oracle.f32_from_e4m3_bits(a).reshape(a.shape)
+    return a.astype(np.float32)
+
+
+def normal(rng, shape, dtype: int) -> np.ndarray:
+    """N(0,1) values (fp64 -> fp32 -> dtype with round-to-nearest-even)."""
+    x = rng.standard_normal(shape).astype(np.float32)
+    if dtype == oracle.BF16:
+        return oracle.bf16_bits_from_f32(x).reshape(shape)
+    return x
+
+
+def paged_tables(rng, lens, block_size, slack=0.1, min_free=3):
+    """Random non-contiguous block tables for the given context lengths.
+
+    Returns (block_tables [N, max_blocks] int32 with -1 padding, num_blocks)."""
+    pages = [(int(L) + block_size - 1) // block_size for L in lens]
+    total = sum(pages)
+    nb = int(math.ceil(total * (1 + slack))) + min_free
+    perm = rng.permutation(nb).astype(np.int32)
+    mb = max(max(pages), 1)
+    bt = -np.ones((len(lens), mb), np.int32)
+    o = 0
+    for n, p in enumerate(pages):
+        bt[n, :p] = perm[o:o + p]
+        o += p
+    return bt, nb
+
+
+def decode_case(seed, H, Hkv, D, lens, kv_dtype, q_dtype=None, block_size=16):
+    rng = np.random.default_rng(seed)
+    q_dtype = kv_dtype if q_dtype is None else q_dtype
+    bt, nb = paged_tables(rng, lens, block_size)
+    kp = normal(rng, (nb, Hkv, block_size, D), kv_dtype)
+    vp = normal(rng, (nb, Hkv, block_size, D), kv_dtype)
+    q = normal(rng, (len(lens), H, D), q_dtype)
+    return q, kp, vp, bt, nb
+
+
+def max_abs_err(a, b) -> float:
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64)))) if np.size(a) else 0.0
+
+
+def announce(msg: str) -> None:
+    print(f"[gpu-case] {msg}", flush=True)

@@ -1,0 +1,266 @@
+"""BlockManager parity: the product's C++ allocator (through the C ABI) against
+the reference's known answers and against the reference model of
+src/block_manager.rs (oracle/block_manager_model.py).
+
+Mirrors the reference's tests/test_block_manager.py (same API, same error
+strings), its unit tests (src/block_manager.rs:179-249), the model-based
+property test (tests/block_manager_proptest.rs:139-259, with its regression
+seeds) and the loom invariants (src/block_manager.rs:304-548) as a threaded
+stress test.
+"""
+import json
+import os
+import random
+import threading
+
+import pytest
+
+from oracle.block_manager_model import BlockManagerModel, ModelError
+import zealot_amd as ze
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_known_answers.json")))
+
+
+# ------------------------------------------------ reference pytest, ported 1:1
+
+def test_module_exposes_classes():
+    for name in ("BlockManager", "BlockHandle"):
+        assert hasattr(ze, name)
+
+
+def test_allocate_returns_handle_and_tracks_free_blocks():
+    bm = ze.BlockManager(num_gpu_blocks=4, block_size=16)
+    assert bm.free_blocks == 4 and bm.num_gpu_blocks == 4 and bm.block_size == 16
+    h = bm.allocate()
+    assert isinstance(h, ze.BlockHandle)
+    assert isinstance(h.block_id, int) and isinstance(h.generation, int)
+    assert h.block_id == 0 and h.generation == 1
+    assert bm.free_blocks == 3
+
+
+def test_handle_attributes_and_repr():
+    h = ze.BlockHandle(block_id=7, generation=3)
+    assert h.block_id == 7 and h.generation == 3
+    assert "7" in repr(h) and "3" in repr(h)
+
+
+def test_large_pool_roundtrip():
+    bm = ze.BlockManager(1024, 16)
+    handles = [bm.allocate() for _ in range(1024)]
+    assert bm.free_blocks == 0
+    assert len({h.block_id for h in handles}) == 1024
+    for h in handles:
+        bm.free(h)
+    assert bm.free_blocks == 1024
+
+
+def test_errors_are_runtime_errors_with_detail():
+    bm = ze.BlockManager(1, 16)
+    h = bm.allocate()
+    bm.free(h)
+    with pytest.raises(RuntimeError) as ei:
+        bm.free(h)
+    assert "Stale handle" in str(ei.value) and "block 0" in str(ei.value)
+    assert str(ei.value) == "Stale handle: block 0 was freed (gen 1, current 2)"
+    with pytest.raises(RuntimeError, match=r"^Out of blocks: requested 1, available 0$"):
+        h2 = bm.allocate()
+        bm.allocate()
+    with pytest.raises(RuntimeError, match=r"^Block 5 is not allocated$"):
+        bm.free(ze.BlockHandle(5, 1))
+
+
+# ------------------------------------------------ known-answer scripts
+
+def _run_script(make, ops):
+    bm = make()
+    handles = []
+    for op in ops:
+        kind = op[0]
+        if kind in ("free_blocks", "num_gpu_blocks", "block_size"):
+            got = bm.available() if kind == "free_blocks" else getattr(bm, kind)
+            assert got == op[1], (kind, got, op[1])
+        elif kind == "allocate":
+            h = bm.allocate()
+            hid, gen = (h.block_id, h.generation) if hasattr(h, "block_id") else h
+            assert {"block_id": hid, "generation": gen} == op[1]
+            handles.append((hid, gen))
+        elif kind == "allocate_error":
+            with pytest.raises((RuntimeError, ModelError)) as ei:
+                bm.allocate()
+            if isinstance(ei.value, RuntimeError):
+                assert op[1] in str(ei.value)
+            else:
+                assert ei.value.kind == "OutOfBlocks"
+        elif kind in ("free", "reference"):
+            hid, gen = handles[op[1]]
+            expect = op[2]
+            fn = getattr(bm, kind)
+            arg = (ze.BlockHandle(hid, gen),) if isinstance(bm, ze.BlockManager) else (hid, gen)
+            if expect is None:
+                fn(*arg)
+            else:
+                with pytest.raises((RuntimeError, ModelError)) as ei:
+                    fn(*arg)
+                if isinstance(ei.value, RuntimeError):
+                    assert expect in str(ei.value)
+                else:
+                    assert ei.value.kind == "StaleHandle"
+        else:
+            raise AssertionError(kind)
+
+
+class _ModelAdapter(BlockManagerModel):
+    @property
+    def num_gpu_blocks(self):
+        return self.num_blocks
+
+
+@pytest.mark.parametrize("case", GOLD["block_manager"], ids=lambda c: c["source"])
+def test_known_answer_scripts_product(case):
+    _run_script(lambda: ze.BlockManager(case["num_blocks"], case["block_size"]), case["ops"])
+
+
+@pytest.mark.parametrize("case", GOLD["block_manager"], ids=lambda c: c["source"])
+def test_known_answer_scripts_model(case):
+    _run_script(lambda: _ModelAdapter(case["num_blocks"], case["block_size"]), case["ops"])
+
+
+@pytest.mark.parametrize("case", GOLD["block_manager_create_errors"], ids=lambda c: c["source"])
+def test_create_errors(case):
+    with pytest.raises(RuntimeError, match=case["expected_error"]):
+        ze.BlockManager(case["num_blocks"], case["block_size"])
+    with pytest.raises(ModelError):
+        BlockManagerModel(case["num_blocks"], case["block_size"])
+
+
+# ------------------------------------------------ model-based property test
+
+def _random_ops(rng, n):
+    return [rng.choice(["allocate", "free", "reference"]) if True else None for _ in range(n)], \
+           [rng.randrange(16) for _ in range(n)]
+
+
+@pytest.mark.parametrize("seed", range(300))
+def test_random_ops_match_model(seed):
+    """tests/block_manager_proptest.rs:139-239: op-by-op equality with the model."""
+    rng = random.Random(seed)
+    num_blocks = 1 if seed % 5 == 0 else rng.randrange(1, 8)  # single_block_pool_torture share
+    ops, idxs = _random_ops(rng, rng.randrange(1, 300))
+    bm = ze.BlockManager(num_blocks, 16)
+    model = BlockManagerModel(num_blocks, 16)
+    handles, held = [], 0
+    for op, idx in zip(ops, idxs):
+        if op == "allocate":
+            try:
+                h = bm.allocate()
+            except RuntimeError as e:
+                assert "Out of blocks" in str(e)
+                assert model.available() == 0
+                with pytest.raises(ModelError):
+                    model.allocate()
+            else:
+                mid, mgen = model.allocate()
+                assert (h.block_id, h.generation) == (mid, mgen)
+                handles.append(h)
+                held += 1
+        else:
+            if not handles:
+                continue
+            h = handles[idx % len(handles)]
+            try:
+                expect = getattr(model, op)(h.block_id, h.generation)
+                model_err = None
+            except ModelError as e:
+                model_err = e
+            try:
+                getattr(bm, op)(h)
+                err = None
+            except RuntimeError as e:
+                err = e
+            assert (err is None) == (model_err is None), (op, err, model_err)
+            if err is not None:
+                assert "Stale handle" in str(err) and model_err.kind == "StaleHandle"
+            else:
+                held += 1 if op == "reference" else -1
+                if op == "free" and expect:
+                    assert model.free_stack[-1] == h.block_id
+        # reference conservation (block_manager_proptest.rs:219-231)
+        assert held == sum(model.refcount(b) for b in range(num_blocks))
+        assert bm.available() == model.available()
+        for b in range(num_blocks):
+            assert bm.refcount(b) == model.refcount(b)
+    assert model.allocated_count() == num_blocks - bm.available()
+
+
+# ------------------------------------------------ concurrency (loom invariants)
+
+def test_concurrent_alloc_free_unique_ownership_and_generations():
+    """block_manager.rs:304-345 and :449-516 as a threaded stress test."""
+    BLOCKS, THREADS, ITERS = 4, 8, 3000
+    bm = ze.BlockManager(BLOCKS, 16)
+    in_use = [threading.Lock() for _ in range(BLOCKS)]
+    logs = [[] for _ in range(THREADS)]
+    errors = []
+
+    def worker(tid):
+        try:
+            for _ in range(ITERS):
+                try:
+                    h = bm.allocate()
+                except RuntimeError as e:
+                    assert "Out of blocks" in str(e)
+                    continue
+                assert in_use[h.block_id].acquire(blocking=False), "double allocation"
+                logs[tid].append((h.block_id, h.generation))
+                in_use[h.block_id].release()
+                bm.free(h)
+        except Exception as e:  # pragma: no cover
+            errors.append(e)
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(THREADS)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors
+    for log in logs:  # per thread, generations of a block strictly increase
+        last = {}
+        for bid, gen in log:
+            assert gen > last.get(bid, 0)
+            last[bid] = gen
+    total = [0] * BLOCKS
+    for log in logs:
+        for bid, _ in log:
+            total[bid] += 1
+    for b in range(BLOCKS):  # generation == 1 + number of allocations
+        h = bm.allocate()
+        assert h.generation == 1 + total[h.block_id]
+        bm.free(h)
+        total[h.block_id] += 1
+    assert bm.free_blocks == BLOCKS
+
+
+def test_refcount_prevents_premature_reclaim_threaded():
+    bm = ze.BlockManager(2, 16)
+    h = bm.allocate()
+    for _ in range(7):
+        bm.reference(h)
+    ts = [threading.Thread(target=bm.free, args=(h,)) for _ in range(7)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert bm.free_blocks == 1 and bm.refcount(h.block_id) == 1
+    bm.free(h)
+    assert bm.free_blocks == 2
+    with pytest.raises(RuntimeError, match="Stale handle"):
+        bm.reference(h)
+
+
+def test_forged_handle_for_free_block_is_rejected():
+    bm = ze.BlockManager(2, 16)
+    with pytest.raises(RuntimeError, match="Block 0 is not allocated"):
+        bm.free(ze.BlockHandle(0, 1))
+    assert bm.free_blocks == 2
+    h = bm.allocate()
+    assert (h.block_id, h.generation) == (0, 1)

@@ -1,0 +1,189 @@
+"""Paged decode attention on the MI355X against the CPU oracle.
+
+Tolerances (absolute, on the output): 1e-5 for fp32 KV, 2e-2 for bf16 KV,
+5e-2 for fp8 KV against the fp32 oracle on the bf16 inputs the fp8 pool was
+quantised from.  The oracle computes in fp32 from the very same pool bytes.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.gpu_util import announce, as_f32, decode_case, max_abs_err, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+TOL = {oracle.F32: 1e-5, oracle.BF16: 2e-2}
+ORACLE_DT = {oracle.F32: oracle.F32, oracle.BF16: oracle.BF16}
+
+
+def _run(q, kp, vp, bt, lens, kv_dtype, mapping="grouped", **kw):
+    from zealot_amd import ops
+    out = ops.paged_decode(to_dev(q), to_dev(kp), to_dev(vp), to_dev(bt),
+                           to_dev(np.asarray(lens, np.int32)), mapping=mapping, **kw)
+    torch.cuda.synchronize()
+    return as_f32(to_host(out), oracle.BF16 if out.dtype == torch.bfloat16 else oracle.F32)
+
+
+def _oracle(q, kp, vp, bt, lens, kv_dtype, q_dtype, mapping):
+    Hkv, D = kp.shape[1], kp.shape[3]
+    qf = as_f32(q, q_dtype)
+    m = oracle.GROUPED if mapping == "grouped" else oracle.MODULO
+    return oracle.paged_decode(qf, kp, vp, kv_dtype, bt, lens, Hkv, D, kp.shape[2],
+                               np.float32(1.0 / math.sqrt(D)), m, threads=8)
+
+
+C2_LENS = [1, 15, 16, 17, 100, 511, 512, 513, 1000, 2048, 4097, 8192]
+
+
+@pytest.mark.parametrize("mapping", ["grouped", "modulo"])
+def test_c2_shape_bf16_small_batch(mapping):
+    announce(f"decode bf16 H32/Hkv8/D128 lens={C2_LENS} mapping={mapping}")
+    q, kp, vp, bt, nb = decode_case(20, 32, 8, 128, C2_LENS, oracle.BF16)
+    got = _run(q, kp, vp, bt, C2_LENS, oracle.BF16, mapping)
+    ref = _oracle(q, kp, vp, bt, C2_LENS, oracle.BF16, oracle.BF16, mapping)
+    assert max_abs_err(got, ref) <= 2e-2
+
+
+def test_c1_fp32_mha_d32():
+    # C1: 2 layers, 4 heads MHA, D=32, fp32; contexts after prompt + 8 decode steps
+    lens = [17 + 8, 40 + 8, 77 + 8, 130 + 8]
+    announce(f"decode fp32 H4/Hkv4/D32 lens={lens}")
+    q, kp, vp, bt, nb = decode_case(21, 4, 4, 32, lens, oracle.F32)
+    got = _run(q, kp, vp, bt, lens, oracle.F32)
+    ref = _oracle(q, kp, vp, bt, lens, oracle.F32, oracle.F32, "grouped")
+    assert max_abs_err(got, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("H,Hkv,D,dt", [
+    (8, 8, 128, oracle.BF16),    # G=1 (MHA) on MFMA
+    (16, 8, 128, oracle.BF16),   # G=2
+    (64, 8, 128, oracle.BF16),   # G=8
+    (32, 8, 64, oracle.BF16),    # D=64
+    (24, 8, 96, oracle.BF16),    # D=96 -> generic kernel
+    (48, 4, 128, oracle.BF16),   # G=12 -> generic kernel
+    (32, 8, 128, oracle.F32),    # fp32 GQA -> generic kernel
+    (4, 4, 256, oracle.F32),     # D=256
+])
+def test_head_shapes(H, Hkv, D, dt):
+    lens = [3, 16, 33, 700, 1500]
+    announce(f"decode H{H}/Hkv{Hkv}/D{D} dt={dt} lens={lens}")
+    q, kp, vp, bt, nb = decode_case(22 + H + D, H, Hkv, D, lens, dt)
+    for mapping in ("grouped", "modulo"):
+        got = _run(q, kp, vp, bt, lens, dt, mapping)
+        ref = _oracle(q, kp, vp, bt, lens, dt, dt, mapping)
+        assert max_abs_err(got, ref) <= TOL[dt], mapping
+
+
+def test_f32_queries_on_bf16_pool():
+    lens = [5, 300, 2100]
+    q, kp, vp, bt, nb = decode_case(23, 32, 8, 128, lens, oracle.BF16, q_dtype=oracle.F32)
+    got = _run(q, kp, vp, bt, lens, oracle.BF16)
+    ref = _oracle(q, kp, vp, bt, lens, oracle.BF16, oracle.F32, "grouped")
+    assert max_abs_err(got, ref) <= 2e-2
+
+
+def test_empty_context_sentinel_and_out_of_range_ids():
+    lens = [0, 40, 64, 50]
+    q, kp, vp, bt, nb = decode_case(24, 32, 8, 128, lens, oracle.BF16)
+    bt = bt.copy()
+    bt[2, 2] = -1           # walk of seq 2 stops after 2 pages (32 tokens)
+    bt[3, 1] = nb + 5       # an id outside the pool ends the walk too
+    got = _run(q, kp, vp, bt, lens, oracle.BF16)
+    assert np.all(got[0] == 0)
+    ref_lens = [0, 40, 32, 16]
+    ref = _oracle(q, kp, vp, bt, ref_lens, oracle.BF16, oracle.BF16, "grouped")
+    assert max_abs_err(got, ref) <= 2e-2
+
+
+def test_decode_is_deterministic():
+    lens = [700, 4000]
+    q, kp, vp, bt, nb = decode_case(25, 32, 8, 128, lens, oracle.BF16)
+    a = _run(q, kp, vp, bt, lens, oracle.BF16)
+    b = _run(q, kp, vp, bt, lens, oracle.BF16)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("src", [oracle.BF16, oracle.F32])
+def test_fp8_kv_decode(src):
+    """fp8 pools quantised on append (per-(seq, head) amax scales), decoded with
+    fp32 accumulation; checked against the fp32 oracle on the source values."""
+    from zealot_amd import ops
+    rng = np.random.default_rng(26)
+    H, Hkv, D, BS = 32, 8, 128, 16
+    lens = [1, 17, 1024, 3000, 5000]
+    from tests.gpu_util import normal, paged_tables
+    bt, nb = paged_tables(rng, lens, BS)
+    T = sum(lens)
+    k = normal(rng, (T, Hkv, D), src)
+    v = normal(rng, (T, Hkv, D), src)
+    q = normal(rng, (len(lens), H, D), oracle.BF16)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    slots = np.concatenate([bt[n, np.arange(L) // BS].astype(np.int64) * BS + np.arange(L) % BS
+                            for n, L in enumerate(lens)])
+    rows = np.repeat(np.arange(len(lens)), lens).astype(np.int32)
+    announce(f"fp8 decode src={src} lens={lens}")
+    kd, vd = to_dev(k), to_dev(v)
+    ks = ops.fp8_scales(kd, to_dev(cu))
+    vs = ops.fp8_scales(vd, to_dev(cu))
+    kpool = torch.zeros((nb, Hkv, BS, D), dtype=torch.uint8, device="cuda")
+    vpool = torch.zeros_like(kpool)
+    ops.append(kpool, vpool, kd, vd, to_dev(slots), k_scales=ks, v_scales=vs, token_row=to_dev(rows))
+    torch.cuda.synchronize()
+    # scales and quantised pages are bit-exact against the oracle
+    ks_ref = oracle.fp8_scales(k, src, cu, Hkv, D)
+    vs_ref = oracle.fp8_scales(v, src, cu, Hkv, D)
+    assert np.array_equal(to_host(ks), ks_ref) and np.array_equal(to_host(vs), vs_ref)
+    kp_ref = np.zeros((nb, Hkv, BS, D), np.uint8)
+    vp_ref = np.zeros_like(kp_ref)
+    oracle.append_slots(kp_ref, vp_ref, oracle.FP8, k, v, src, slots, Hkv, D, BS, nb, ks_ref,
+                        vs_ref, rows)
+    assert np.array_equal(to_host(kpool), kp_ref) and np.array_equal(to_host(vpool), vp_ref)
+    out = ops.paged_decode(to_dev(q), kpool, vpool, to_dev(bt), to_dev(np.asarray(lens, np.int32)),
+                           k_scales=ks, v_scales=vs)
+    torch.cuda.synchronize()
+    got = as_f32(to_host(out), oracle.BF16)
+    # against the fp32 oracle on the unquantised inputs (the bar)
+    kp_src = np.zeros((nb, Hkv, BS, D), np.float32)
+    vp_src = np.zeros_like(kp_src)
+    oracle.append_slots(kp_src, vp_src, oracle.F32, as_f32(k, src), as_f32(v, src), oracle.F32,
+                        slots, Hkv, D, BS, nb)
+    ref = _oracle(q, kp_src, vp_src, bt, lens, oracle.F32, oracle.BF16, "grouped")
+    assert max_abs_err(got, ref) <= 5e-2
+    # and tightly against the oracle on the dequantised fp8 pages
+    ref8 = oracle.paged_decode(as_f32(q, oracle.BF16), kp_ref, vp_ref, oracle.FP8, bt, lens, Hkv, D,
+                               BS, np.float32(1 / math.sqrt(D)), oracle.GROUPED, ks_ref, vs_ref, threads=8)
+    assert max_abs_err(got, ref8) <= 2e-2
+
+
+def test_c2_full_size_sampled_against_oracle():
+    """C2 at full size (256 seqs, ctx U[512, 8192], bf16) on the GPU; 8 sampled
+    sequences are checked against the oracle on their own pages."""
+    from zealot_amd import ops
+    from tests.gpu_util import paged_tables
+    rng = np.random.default_rng(27)
+    N, H, Hkv, D, BS = 256, 32, 8, 128, 16
+    lens = rng.integers(512, 8193, N)
+    bt, nb = paged_tables(rng, lens, BS)
+    announce(f"decode C2 full size N={N} sum_ctx={int(lens.sum())} blocks={nb}")
+    g = torch.Generator(device="cuda").manual_seed(27)
+    kpool = torch.randn((nb, Hkv, BS, D), generator=g, device="cuda").to(torch.bfloat16)
+    vpool = torch.randn((nb, Hkv, BS, D), generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn((N, H, D), generator=g, device="cuda").to(torch.bfloat16)
+    btd = to_dev(bt)
+    out = ops.paged_decode(q, kpool, vpool, btd, to_dev(lens.astype(np.int32)))
+    torch.cuda.synchronize()
+    got = as_f32(to_host(out), oracle.BF16)
+    assert np.all(np.isfinite(got))
+    pick = rng.choice(N, 8, replace=False)
+    for n in pick:
+        L = int(lens[n])
+        pages = bt[n, : (L + BS - 1) // BS]
+        idx = torch.from_numpy(pages.astype(np.int64)).cuda()
+        kp = to_host(kpool.index_select(0, idx))
+        vp = to_host(vpool.index_select(0, idx))
+        bt1 = np.arange(len(pages), dtype=np.int32)[None, :]
+        ref = _oracle(to_host(q[n:n + 1]), kp, vp, bt1, [L], oracle.BF16, oracle.BF16, "grouped")
+        assert max_abs_err(got[n:n + 1], ref) <= 2e-2, int(n)

@@ -1,0 +1,118 @@
+"""ctypes binding of libzealot_kv.so (the C ABI declared in include/zealot_kv.h).
+
+The library is the product: there is no Python or CPU fallback.  If the
+shared library is missing, importing any op raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libzealot_kv.so")
+
+# zk_status
+OK = 0
+ERR_BLOCK_ALREADY_ALLOCATED = 1
+ERR_BLOCK_NOT_ALLOCATED = 2
+ERR_OUT_OF_BLOCKS = 3
+ERR_INVALID_BLOCK_SIZE = 4
+ERR_STALE_HANDLE = 5
+ERR_SEQUENCE_TOO_LONG = 6
+ERR_FAILED_PRECONDITION = 7
+ERR_ALREADY_EXISTS = 8
+ERR_INTERNAL = 9
+ERR_INVALID_ARGUMENT = 10
+ERR_HIP = 11
+
+# zk_dtype
+F32, BF16, FP8_E4M3 = 0, 1, 2
+# zk_gqa_mapping
+GQA_GROUPED, GQA_MODULO = 0, 1
+
+
+class BlockHandleC(ctypes.Structure):
+    _fields_ = [("block_id", ctypes.c_uint64), ("generation", ctypes.c_uint64)]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+_CP = ctypes.c_char_p
+
+# name -> (restype, argtypes); every symbol declared in include/zealot_kv.h.
+SIGNATURES = {
+    "zk_last_error": (ctypes.c_char_p, []),
+    "zk_abi_version": (_I, []),
+    "zk_bm_create": (_I, [_SZ, _SZ, ctypes.POINTER(_P)]),
+    "zk_bm_destroy": (None, [_P]),
+    "zk_bm_allocate": (_I, [_P, ctypes.POINTER(BlockHandleC)]),
+    "zk_bm_free": (_I, [_P, BlockHandleC]),
+    "zk_bm_reference": (_I, [_P, BlockHandleC]),
+    "zk_bm_available": (_SZ, [_P]),
+    "zk_bm_num_gpu_blocks": (_SZ, [_P]),
+    "zk_bm_block_size": (_SZ, [_P]),
+    "zk_bm_refcount": (_SZ, [_P, ctypes.c_uint64]),
+    "zk_append": (_I, [_P, _P, _I, _P, _P, _I, _P, _I64, _I, _I, _I, _I64, _P, _P, _P, _P]),
+    "zk_fp8_scales": (_I, [_P, _I, _P, _I, _I, _I, _P, _P]),
+    "zk_gather": (_I, [_P, _P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I64, _P]),
+    "zk_copy_blocks": (_I, [_P, _I, _I64, _I64, _P, _P, _I64, _P]),
+    "zk_paged_decode_workspace_size": (_SZ, [_I, _I, _I, _I, _I]),
+    "zk_paged_decode": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _F, _I,
+                             _P, _P, _P, _SZ, _P]),
+    "zk_cache_create": (_I, [_SZ, _SZ, _SZ, _SZ, _SZ, _I, _SZ, _SZ, _P, ctypes.POINTER(_P)]),
+    "zk_cache_destroy": (None, [_P]),
+    "zk_cache_register_seq": (_I, [_P, _CP, _SZ]),
+    "zk_cache_alloc_block": (_I, [_P, _CP, _P, ctypes.POINTER(_SZ)]),
+    "zk_cache_release_seq": (_I, [_P, _CP]),
+    "zk_cache_fork_seq": (_I, [_P, _CP, _CP]),
+    "zk_cache_store_kv": (_I, [_P, _SZ, _CP, _P, _P, _I, _SZ, _SZ]),
+    "zk_cache_append_kv": (_I, [_P, _SZ, _CP, _P, _P, _I]),
+    "zk_cache_set_fp8_scales": (_I, [_P, _CP, _P, _P]),
+    "zk_cache_block_table_ptr": (_I, [_P, _CP, ctypes.POINTER(_P)]),
+    "zk_cache_k_pool_ptr": (_P, [_P, _SZ]),
+    "zk_cache_v_pool_ptr": (_P, [_P, _SZ]),
+    "zk_cache_max_blocks": (_I, [_P, _CP, ctypes.POINTER(_SZ)]),
+    "zk_cache_seq_state": (_I, [_P, _CP, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ),
+                                ctypes.POINTER(_SZ)]),
+    "zk_cache_block_ids": (_I, [_P, _CP, ctypes.POINTER(_I64), ctypes.POINTER(_SZ)]),
+    "zk_cache_paged_decode": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _I, _P, _I, _F, _I]),
+    "zk_timing_enable": (_I, [_I]),
+    "zk_timing_reset": (_I, []),
+    "zk_timing_query": (_I, [_CP, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
+    "zk_stream_copy": (_I, [_P, _P, _SZ, _P]),
+}
+
+_lib = None
+
+
+class ZealotError(RuntimeError):
+    """Error raised from a zk_status; str() is the reference's message."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m zealot_amd.build` "
+                "(there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        msg = lib().zk_last_error().decode("utf-8", "replace")
+        raise ZealotError(rc, msg)

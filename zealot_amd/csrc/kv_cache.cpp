@@ -1,0 +1,509 @@
+// kv_cache.cpp -- stateful paged KV cache (host side of src/kv_cache.rs).
+//
+// Owns the K and V pools of every layer in one HBM slab
+//   [layer][K|V][num_blocks][Hkv][block_size][D]
+// (per-pool layout of kv_cache.rs:41-50; one block id indexes every layer's
+// pool, kv_cache.rs:241-253) and one slab of per-sequence device block tables
+// [max_seqs][max_blocks_per_seq] (int32, -1 = unused, kv_cache.rs:107-124).
+// The host keeps each sequence's BlockManager handles, so block tables,
+// slot mappings and copy-on-write decisions are computed on the host and every
+// data movement is one kernel launch (zk_append / zk_copy_blocks /
+// zk_paged_decode) instead of per-(token, head) driver copies.
+//
+// Differences from the reference, all deliberate:
+//  - store_kv / append_kv write through one slot-mapping launch; a position
+//    without a block fails before anything is written.
+//  - The write position advances once per token, when the last layer is
+//    written (the reference advances on every append_kv call, i.e. once per
+//    layer, and never on store_kv).
+//  - release_seq returns the sequence's blocks to its BlockManager.
+//  - fork_seq / copy-on-write has no reference counterpart.
+// Not thread-safe: one thread drives a cache (as GpuContext, gpu_context.rs:23-26).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "zk_common.h"
+
+using zk::set_error;
+
+namespace {
+
+struct SeqState {
+    std::vector<zk_block_handle> handles;
+    zk_block_manager *bm = nullptr;
+    size_t cached_tokens = 0;
+    size_t block_offset = 0;
+    size_t max_blocks = 0;
+    size_t slot = 0;
+    std::vector<float> k_scales, v_scales;  // [layers * Hkv], fp8 pools
+};
+
+// Growable device buffer.
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    int ensure(size_t bytes, const char *what) {
+        if (bytes <= cap) return ZK_OK;
+        if (p) {
+            // kernels queued earlier may still read the old buffer
+            ZK_HIP_CHECK(hipDeviceSynchronize(), what);
+            (void)hipFree(p);
+        }
+        p = nullptr;
+        cap = 0;
+        size_t want = std::max<size_t>(bytes, 4096);
+        ZK_HIP_CHECK(hipMalloc(&p, want), what);
+        cap = want;
+        return ZK_OK;
+    }
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+// Pinned staging buffer; reuse waits for the copy that last read it.
+struct Staging {
+    void *p = nullptr;
+    size_t cap = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+    int ensure(size_t bytes) {
+        if (pending) {
+            ZK_HIP_CHECK(hipEventSynchronize(done), "KVCache staging wait");
+            pending = false;
+        }
+        if (!done) ZK_HIP_CHECK(hipEventCreateWithFlags(&done, hipEventDisableTiming), "KVCache event");
+        if (bytes <= cap) return ZK_OK;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+        size_t want = std::max<size_t>(bytes, 4096);
+        ZK_HIP_CHECK(hipHostMalloc(&p, want, hipHostMallocDefault), "KVCache pinned staging");
+        cap = want;
+        return ZK_OK;
+    }
+    ~Staging() {
+        if (pending && done) (void)hipEventSynchronize(done);
+        if (p) (void)hipHostFree(p);
+        if (done) (void)hipEventDestroy(done);
+    }
+};
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) (void)hipSetDevice(dev);
+        else prev = -1;
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+}  // namespace
+
+struct zk_kv_cache {
+    size_t num_blocks = 0, block_size = 0, num_layers = 0, num_kv_heads = 0, head_dim = 0;
+    int dtype = ZK_F32;
+    size_t max_seqs = 0, max_blocks_per_seq = 0;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    char *slab = nullptr;
+    size_t pool_bytes = 0;
+    int32_t *tables = nullptr;
+    std::vector<size_t> free_slots;
+    std::unordered_map<std::string, SeqState> seqs;
+    DevBuf d_meta;  // slot mappings, token rows, scales, copy pairs
+    DevBuf d_batch; // decode batch tables + lengths + scales
+    DevBuf d_ws;    // decode workspace
+    Staging stage;
+
+    size_t block_bytes() const { return block_size * num_kv_heads * head_dim * zk::elt_size(dtype); }
+    char *k_pool(size_t layer) const { return slab + (2 * layer) * pool_bytes; }
+    char *v_pool(size_t layer) const { return slab + (2 * layer + 1) * pool_bytes; }
+    int32_t *table_row(size_t slot) const { return tables + slot * max_blocks_per_seq; }
+
+    ~zk_kv_cache() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (slab) (void)hipFree(slab);
+        if (tables) (void)hipFree(tables);
+    }
+};
+
+namespace {
+
+int find_seq(zk_kv_cache *c, const char *id, SeqState **out) {
+    if (!c || !id) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache: NULL argument");
+    auto it = c->seqs.find(id);
+    if (it == c->seqs.end())
+        return set_error(ZK_ERR_INTERNAL, std::string("Internal error: KVCache: unknown seq ") + id);
+    *out = &it->second;
+    return ZK_OK;
+}
+
+// Upload `bytes` from host memory to device memory on the cache stream.
+int upload(zk_kv_cache *c, void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return ZK_OK;
+    if (int rc = c->stage.ensure(bytes)) return rc;
+    std::memcpy(c->stage.p, src, bytes);
+    ZK_HIP_CHECK(hipMemcpyAsync(dst, c->stage.p, bytes, hipMemcpyHostToDevice, c->stream), "KVCache upload");
+    ZK_HIP_CHECK(hipEventRecord(c->stage.done, c->stream), "KVCache upload event");
+    c->stage.pending = true;
+    return ZK_OK;
+}
+
+int write_table_entry(zk_kv_cache *c, const SeqState &s, size_t idx, int32_t value) {
+    return upload(c, c->table_row(s.slot) + idx, &value, sizeof(value));
+}
+
+// Copy-on-write of s.handles[idx]: fresh block, copy every pool, drop the
+// shared reference, point the table at the copy.
+int cow_block(zk_kv_cache *c, SeqState &s, size_t idx) {
+    zk_block_handle fresh;
+    if (int rc = zk_bm_allocate(s.bm, &fresh)) return rc;
+    int32_t pair[2] = {(int32_t)s.handles[idx].block_id, (int32_t)fresh.block_id};
+    if (int rc = c->d_meta.ensure(sizeof(pair), "KVCache cow scratch")) {
+        (void)zk_bm_free(s.bm, fresh);
+        return rc;
+    }
+    if (int rc = upload(c, c->d_meta.p, pair, sizeof(pair))) {
+        (void)zk_bm_free(s.bm, fresh);
+        return rc;
+    }
+    std::vector<void *> pools(2 * c->num_layers);
+    for (size_t l = 0; l < c->num_layers; ++l) {
+        pools[2 * l] = c->k_pool(l);
+        pools[2 * l + 1] = c->v_pool(l);
+    }
+    const int32_t *d = (const int32_t *)c->d_meta.p;
+    if (int rc = zk_copy_blocks(pools.data(), (int)pools.size(), (int64_t)c->block_bytes(),
+                                (int64_t)c->num_blocks, d, d + 1, 1, c->stream)) {
+        (void)zk_bm_free(s.bm, fresh);
+        return rc;
+    }
+    if (int rc = zk_bm_free(s.bm, s.handles[idx])) return rc;
+    s.handles[idx] = fresh;
+    return write_table_entry(c, s, idx, (int32_t)fresh.block_id);
+}
+
+int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, const void *k, const void *v,
+                 zk_dtype src_dtype, size_t start, size_t n, const char *what) {
+    if (layer >= c->num_layers)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache ") + what +
+                                                      ": layer " + std::to_string(layer) + " out of range");
+    if (src_dtype != ZK_F32 && src_dtype != ZK_BF16)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache ") + what + ": bad src dtype");
+    if (n == 0) return ZK_OK;
+    if (!k || !v) return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache ") + what + ": NULL k/v");
+    const size_t bs = c->block_size;
+    size_t last_idx = (start + n - 1) / bs;
+    if (last_idx >= s.handles.size())  // kv_cache.rs:234-239
+        return set_error(ZK_ERR_INTERNAL, std::string("Internal error: KVCache ") + what + ": block_idx " +
+                                              std::to_string(last_idx) + " OOB (have " +
+                                              std::to_string(s.handles.size()) + " blocks)");
+    if (c->dtype == ZK_FP8_E4M3 && s.k_scales.empty())
+        return set_error(ZK_ERR_FAILED_PRECONDITION,
+                         std::string("Failed precondition: fp8 scales not set for seq ") + id);
+    // Copy-on-write every shared block this write touches.
+    for (size_t idx = start / bs; idx <= last_idx; ++idx)
+        if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1)
+            if (int rc = cow_block(c, s, idx)) return rc;
+
+    const size_t H = c->num_kv_heads;
+    const bool fp8 = c->dtype == ZK_FP8_E4M3;
+    size_t slots_bytes = n * sizeof(int64_t);
+    size_t rows_bytes = fp8 ? n * sizeof(int32_t) : 0;
+    size_t scale_bytes = fp8 ? 2 * H * sizeof(float) : 0;
+    size_t total = slots_bytes + rows_bytes + scale_bytes;
+    std::vector<char> host(total);
+    int64_t *slots = (int64_t *)host.data();
+    for (size_t t = 0; t < n; ++t) {
+        size_t g = start + t;
+        slots[t] = (int64_t)s.handles[g / bs].block_id * (int64_t)bs + (int64_t)(g % bs);
+    }
+    if (fp8) {
+        std::memset(host.data() + slots_bytes, 0, rows_bytes);  // every token uses scale row 0
+        float *sc = (float *)(host.data() + slots_bytes + rows_bytes);
+        std::memcpy(sc, s.k_scales.data() + layer * H, H * sizeof(float));
+        std::memcpy(sc + H, s.v_scales.data() + layer * H, H * sizeof(float));
+    }
+    if (int rc = c->d_meta.ensure(total, "KVCache slot mapping")) return rc;
+    if (int rc = upload(c, c->d_meta.p, host.data(), total)) return rc;
+    char *d = (char *)c->d_meta.p;
+    const int32_t *d_rows = fp8 ? (const int32_t *)(d + slots_bytes) : nullptr;
+    const float *d_ks = fp8 ? (const float *)(d + slots_bytes + rows_bytes) : nullptr;
+    const float *d_vs = fp8 ? d_ks + H : nullptr;
+    if (int rc = zk_append(c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, k, v, src_dtype,
+                           (const int64_t *)d, (int64_t)n, (int)H, (int)c->head_dim, (int)bs,
+                           (int64_t)c->num_blocks, d_ks, d_vs, d_rows, c->stream))
+        return rc;
+    if (layer + 1 == c->num_layers) {
+        s.cached_tokens = std::max(s.cached_tokens, start + n);
+        s.block_offset = s.cached_tokens % bs;
+    }
+    return ZK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int zk_cache_create(size_t num_blocks, size_t block_size, size_t num_layers, size_t num_kv_heads,
+                    size_t head_dim, zk_dtype dtype, size_t max_seqs, size_t max_blocks_per_seq,
+                    void *stream, zk_kv_cache **out) {
+    if (!out) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_cache_create: out is NULL");
+    *out = nullptr;
+    if (block_size == 0) return set_error(ZK_ERR_INVALID_BLOCK_SIZE, "Invalid block size: 0");
+    if (!zk::valid_dtype(dtype) || num_blocks == 0 || num_layers == 0 || num_kv_heads == 0 ||
+        head_dim == 0 || max_seqs == 0 || max_blocks_per_seq == 0 || num_blocks > 0x7fffffffu)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_cache_create: bad shape");
+    auto *c = new (std::nothrow) zk_kv_cache();
+    if (!c) return set_error(ZK_ERR_INTERNAL, "Internal error: KVCache allocation failed");
+    c->num_blocks = num_blocks;
+    c->block_size = block_size;
+    c->num_layers = num_layers;
+    c->num_kv_heads = num_kv_heads;
+    c->head_dim = head_dim;
+    c->dtype = dtype;
+    c->max_seqs = max_seqs;
+    c->max_blocks_per_seq = max_blocks_per_seq;
+    c->stream = (hipStream_t)stream;
+    if (hipGetDevice(&c->device) != hipSuccess) c->device = 0;
+    c->pool_bytes = ((num_blocks * c->block_bytes()) + 255) & ~(size_t)255;
+    size_t slab_bytes = 2 * num_layers * c->pool_bytes;
+    hipError_t e = hipMalloc((void **)&c->slab, slab_bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(c->slab, 0, slab_bytes, c->stream);  // alloc_zeros, kv_cache.rs:79-88
+    if (e == hipSuccess) e = hipMalloc((void **)&c->tables, max_seqs * max_blocks_per_seq * sizeof(int32_t));
+    if (e == hipSuccess)
+        e = hipMemsetAsync(c->tables, 0xff, max_seqs * max_blocks_per_seq * sizeof(int32_t), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        delete c;
+        return set_error(ZK_ERR_HIP, std::string("Internal error: KVCache pool alloc: ") + hipGetErrorString(e));
+    }
+    c->free_slots.reserve(max_seqs);
+    for (size_t i = 0; i < max_seqs; ++i) c->free_slots.push_back(max_seqs - 1 - i);
+    *out = c;
+    return ZK_OK;
+}
+
+void zk_cache_destroy(zk_kv_cache *c) { delete c; }
+
+int zk_cache_register_seq(zk_kv_cache *c, const char *id, size_t max_blocks) {
+    if (!c || !id) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache: NULL argument");
+    if (c->seqs.count(id)) return set_error(ZK_ERR_ALREADY_EXISTS, std::string("Already exists: seq ") + id);
+    if (max_blocks == 0 || max_blocks > c->max_blocks_per_seq)
+        return set_error(ZK_ERR_SEQUENCE_TOO_LONG,
+                         "Sequence too long: worst case needs " + std::to_string(max_blocks) +
+                             " blocks, pool capacity is " + std::to_string(c->max_blocks_per_seq));
+    if (c->free_slots.empty())
+        return set_error(ZK_ERR_FAILED_PRECONDITION, "Failed precondition: KVCache: all sequence slots in use");
+    DeviceGuard g(c->device);
+    SeqState s;
+    s.max_blocks = max_blocks;
+    s.slot = c->free_slots.back();
+    std::vector<int32_t> row(c->max_blocks_per_seq, -1);
+    if (int rc = upload(c, c->table_row(s.slot), row.data(), row.size() * sizeof(int32_t))) return rc;
+    c->free_slots.pop_back();
+    c->seqs.emplace(id, std::move(s));
+    return ZK_OK;
+}
+
+int zk_cache_alloc_block(zk_kv_cache *c, const char *id, zk_block_manager *bm, size_t *block_id) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    if (!bm) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache alloc_block: NULL manager");
+    if (s->bm && s->bm != bm)
+        return set_error(ZK_ERR_FAILED_PRECONDITION,
+                         "Failed precondition: KVCache alloc_block: sequence uses another BlockManager");
+    if (zk_bm_num_gpu_blocks(bm) > c->num_blocks)
+        return set_error(ZK_ERR_FAILED_PRECONDITION,
+                         "Failed precondition: KVCache alloc_block: BlockManager larger than the pool");
+    if (s->handles.size() >= s->max_blocks)
+        return set_error(ZK_ERR_INTERNAL, "Internal error: block_table slice oob");  // kv_cache.rs:148
+    DeviceGuard g(c->device);
+    zk_block_handle h;
+    if (int rc = zk_bm_allocate(bm, &h)) return rc;
+    if (int rc = write_table_entry(c, *s, s->handles.size(), (int32_t)h.block_id)) {
+        (void)zk_bm_free(bm, h);
+        return rc;
+    }
+    s->bm = bm;
+    s->handles.push_back(h);
+    if (block_id) *block_id = (size_t)h.block_id;
+    return ZK_OK;
+}
+
+int zk_cache_release_seq(zk_kv_cache *c, const char *id) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    DeviceGuard g(c->device);
+    int first_rc = ZK_OK;
+    std::string first_msg;
+    for (const auto &h : s->handles) {
+        int rc = zk_bm_free(s->bm, h);
+        if (rc && !first_rc) {
+            first_rc = rc;
+            first_msg = zk_last_error();
+        }
+    }
+    std::vector<int32_t> row(c->max_blocks_per_seq, -1);
+    int rc = upload(c, c->table_row(s->slot), row.data(), row.size() * sizeof(int32_t));
+    c->free_slots.push_back(s->slot);
+    c->seqs.erase(id);
+    if (first_rc) return set_error(first_rc, first_msg);
+    return rc;
+}
+
+int zk_cache_fork_seq(zk_kv_cache *c, const char *parent, const char *child) {
+    SeqState *p;
+    if (int rc = find_seq(c, parent, &p)) return rc;
+    if (!child) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache fork: NULL child");
+    if (c->seqs.count(child)) return set_error(ZK_ERR_ALREADY_EXISTS, std::string("Already exists: seq ") + child);
+    if (c->free_slots.empty())
+        return set_error(ZK_ERR_FAILED_PRECONDITION, "Failed precondition: KVCache: all sequence slots in use");
+    DeviceGuard g(c->device);
+    size_t done = 0;
+    for (; done < p->handles.size(); ++done)
+        if (zk_bm_reference(p->bm, p->handles[done])) break;
+    if (done < p->handles.size()) {
+        std::string msg = zk_last_error();
+        for (size_t i = 0; i < done; ++i) (void)zk_bm_free(p->bm, p->handles[i]);
+        return set_error(ZK_ERR_STALE_HANDLE, msg);
+    }
+    SeqState s = *p;
+    s.slot = c->free_slots.back();
+    ZK_HIP_CHECK(hipMemcpyAsync(c->table_row(s.slot), c->table_row(p->slot),
+                                c->max_blocks_per_seq * sizeof(int32_t), hipMemcpyDeviceToDevice, c->stream),
+                 "KVCache fork table copy");
+    c->free_slots.pop_back();
+    c->seqs.emplace(child, std::move(s));
+    return ZK_OK;
+}
+
+int zk_cache_store_kv(zk_kv_cache *c, size_t layer, const char *id, const void *k, const void *v,
+                      zk_dtype src_dtype, size_t start_token, size_t n_tokens) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    DeviceGuard g(c->device);
+    return write_tokens(c, layer, *s, id, k, v, src_dtype, start_token, n_tokens, "store_kv");
+}
+
+int zk_cache_append_kv(zk_kv_cache *c, size_t layer, const char *id, const void *k, const void *v,
+                       zk_dtype src_dtype) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    DeviceGuard g(c->device);
+    return write_tokens(c, layer, *s, id, k, v, src_dtype, s->cached_tokens, 1, "append_kv");
+}
+
+int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales, const float *v_scales) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    if (c->dtype != ZK_FP8_E4M3)
+        return set_error(ZK_ERR_FAILED_PRECONDITION, "Failed precondition: KVCache pools are not fp8");
+    if (!k_scales || !v_scales)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache set_fp8_scales: NULL scales");
+    size_t n = c->num_layers * c->num_kv_heads;
+    for (size_t i = 0; i < n; ++i)
+        if (!(k_scales[i] > 0.0f) || !(v_scales[i] > 0.0f))
+            return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache set_fp8_scales: scales must be > 0");
+    s->k_scales.assign(k_scales, k_scales + n);
+    s->v_scales.assign(v_scales, v_scales + n);
+    return ZK_OK;
+}
+
+int zk_cache_block_table_ptr(zk_kv_cache *c, const char *id, const int32_t **out) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    if (!out) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache: NULL out");
+    *out = c->table_row(s->slot);
+    return ZK_OK;
+}
+
+void *zk_cache_k_pool_ptr(zk_kv_cache *c, size_t layer) {
+    return (c && layer < c->num_layers) ? c->k_pool(layer) : nullptr;
+}
+void *zk_cache_v_pool_ptr(zk_kv_cache *c, size_t layer) {
+    return (c && layer < c->num_layers) ? c->v_pool(layer) : nullptr;
+}
+
+int zk_cache_max_blocks(zk_kv_cache *c, const char *id, size_t *out) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    if (out) *out = s->max_blocks;
+    return ZK_OK;
+}
+
+int zk_cache_seq_state(zk_kv_cache *c, const char *id, size_t *cached_tokens, size_t *block_offset,
+                       size_t *num_blocks) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    if (cached_tokens) *cached_tokens = s->cached_tokens;
+    if (block_offset) *block_offset = s->block_offset;
+    if (num_blocks) *num_blocks = s->handles.size();
+    return ZK_OK;
+}
+
+int zk_cache_block_ids(zk_kv_cache *c, const char *id, int64_t *ids, size_t *n) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    if (!n) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache block_ids: NULL n");
+    size_t cnt = std::min(*n, s->handles.size());
+    for (size_t i = 0; ids && i < cnt; ++i) ids[i] = (int64_t)s->handles[i].block_id;
+    *n = s->handles.size();
+    return ZK_OK;
+}
+
+int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *q,
+                          zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping) {
+    if (!c || (n > 0 && !ids)) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode: NULL argument");
+    if (layer >= c->num_layers)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode: layer out of range");
+    if (n <= 0) return ZK_OK;
+    DeviceGuard g(c->device);
+    const size_t MB = c->max_blocks_per_seq, H = c->num_kv_heads;
+    const bool fp8 = c->dtype == ZK_FP8_E4M3;
+    size_t tbl_bytes = (size_t)n * MB * sizeof(int32_t);
+    size_t len_bytes = (size_t)n * sizeof(int32_t);
+    size_t sc_bytes = fp8 ? 2 * (size_t)n * H * sizeof(float) : 0;
+    size_t off_len = (tbl_bytes + 255) & ~(size_t)255;
+    size_t off_sc = off_len + ((len_bytes + 255) & ~(size_t)255);
+    size_t total = off_sc + sc_bytes;
+    std::vector<char> host(total, 0);
+    int32_t *tbl = (int32_t *)host.data();
+    int32_t *lens = (int32_t *)(host.data() + off_len);
+    float *sc = (float *)(host.data() + off_sc);
+    for (int i = 0; i < n; ++i) {
+        SeqState *s;
+        if (int rc = find_seq(c, ids[i], &s)) return rc;
+        for (size_t j = 0; j < MB; ++j) tbl[(size_t)i * MB + j] = j < s->handles.size() ? (int32_t)s->handles[j].block_id : -1;
+        lens[i] = (int32_t)s->cached_tokens;
+        if (fp8) {
+            if (s->k_scales.empty())
+                return set_error(ZK_ERR_FAILED_PRECONDITION,
+                                 std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
+            std::memcpy(sc + (size_t)i * H, s->k_scales.data() + layer * H, H * sizeof(float));
+            std::memcpy(sc + (size_t)n * H + (size_t)i * H, s->v_scales.data() + layer * H, H * sizeof(float));
+        }
+    }
+    if (int rc = c->d_batch.ensure(total, "KVCache decode batch")) return rc;
+    if (int rc = upload(c, c->d_batch.p, host.data(), total)) return rc;
+    size_t ws = zk_paged_decode_workspace_size(n, num_heads, (int)c->head_dim, (int)MB, (int)c->block_size);
+    if (int rc = c->d_ws.ensure(ws, "KVCache decode workspace")) return rc;
+    char *d = (char *)c->d_batch.p;
+    const float *dks = fp8 ? (const float *)(d + off_sc) : nullptr;
+    const float *dvs = fp8 ? dks + (size_t)n * H : nullptr;
+    return zk_paged_decode(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
+                           (const int32_t *)d, (const int32_t *)(d + off_len), n, num_heads, (int)H,
+                           (int)c->head_dim, (int)c->block_size, (int)MB, (int64_t)c->num_blocks, scale,
+                           mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,433 @@
+// kv_ops.hip -- KV append (slot-mapping scatter), fp8 scales, block-table
+// gather and copy-on-write block copy for gfx950.
+//
+// All four are HBM-bound byte movers.  Each lane moves 16-byte vectors
+// (global_load/store_dwordx4); a thread issues all of its loads before its
+// stores so several 16-B requests per lane are in flight.
+//
+// Pool layout (src/kv_cache.rs:41-50): a (block, kv_head) page is block_size
+// contiguous rows of head_dim elements, so a token row of one head is
+// row_bytes = head_dim * elt contiguous bytes at
+//   ((block * Hkv + head) * block_size + token_in_block) * row_bytes.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "zk_common.h"
+
+using namespace zk;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+__device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ void st16(void *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
+
+// ------------------------------------------------------------------ append
+// Same-dtype append: one 16-B chunk per (token, K|V, head, chunk) index, in
+// that order, so a wavefront reads one token's contiguous K (or V) rows and
+// writes whole 16-B-aligned pieces of the destination rows.
+__global__ void __launch_bounds__(kThreads)
+append_copy_kernel(const char *__restrict__ k, const char *__restrict__ v, char *__restrict__ k_pool,
+                   char *__restrict__ v_pool, const int64_t *__restrict__ slots, uint32_t total,
+                   uint32_t chunks_per_row, uint32_t hkv, uint32_t row_bytes, uint32_t block_size,
+                   int64_t num_slots) {
+    uint32_t base = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+    uint4 data[kUnroll];
+    char *dst[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        uint32_t idx = base + u * kThreads;
+        dst[u] = nullptr;
+        if (idx < total) {
+            uint32_t c = idx % chunks_per_row;
+            uint32_t r = idx / chunks_per_row;
+            uint32_t h = r % hkv;
+            r /= hkv;
+            uint32_t kv = r & 1u;
+            uint32_t t = r >> 1;
+            int64_t slot = slots[t];
+            size_t src_off = ((size_t)t * hkv + h) * row_bytes + (size_t)c * 16;
+            data[u] = ld16((kv ? v : k) + src_off);
+            if (slot >= 0 && slot < num_slots) {
+                int64_t blk = slot / block_size, tib = slot % block_size;
+                dst[u] = (kv ? v_pool : k_pool) +
+                         (((size_t)blk * hkv + h) * block_size + (size_t)tib) * row_bytes +
+                         (size_t)c * 16;
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+        if (dst[u]) st16(dst[u], data[u]);
+}
+
+// Quantising append into an fp8 pool: one 16-element chunk per index; the
+// source chunk is 32 B (bf16) or 64 B (f32), the destination chunk 16 B.
+template <int SRC>  // ZK_BF16 or ZK_F32
+__global__ void __launch_bounds__(kThreads)
+append_fp8_kernel(const char *__restrict__ k, const char *__restrict__ v, uint8_t *__restrict__ k_pool,
+                  uint8_t *__restrict__ v_pool, const int64_t *__restrict__ slots,
+                  const float *__restrict__ k_scales, const float *__restrict__ v_scales,
+                  const int32_t *__restrict__ token_row, uint32_t total, uint32_t chunks_per_row,
+                  uint32_t hkv, uint32_t head_dim, uint32_t block_size, int64_t num_slots) {
+    uint32_t idx = blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= total) return;
+    uint32_t c = idx % chunks_per_row;
+    uint32_t r = idx / chunks_per_row;
+    uint32_t h = r % hkv;
+    r /= hkv;
+    uint32_t kv = r & 1u;
+    uint32_t t = r >> 1;
+    int64_t slot = slots[t];
+    if (slot < 0 || slot >= num_slots) return;
+    float s = (kv ? v_scales : k_scales)[(size_t)token_row[t] * hkv + h];
+    float inv = 1.0f / s;  // IEEE division, identical to the host's
+    size_t elem = ((size_t)t * hkv + h) * head_dim + (size_t)c * 16;
+    float x[16];
+    if (SRC == ZK_BF16) {
+        const char *src = (kv ? v : k) + elem * 2;
+        uint4 a = ld16(src), b = ld16(src + 16);
+        uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[2 * i] = bf16lo(w[i]);
+            x[2 * i + 1] = bf16hi(w[i]);
+        }
+    } else {
+        const char *src = (kv ? v : k) + elem * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint4 a = ld16(src + 16 * i);
+            x[4 * i] = __uint_as_float(a.x);
+            x[4 * i + 1] = __uint_as_float(a.y);
+            x[4 * i + 2] = __uint_as_float(a.z);
+            x[4 * i + 3] = __uint_as_float(a.w);
+        }
+    }
+    uint4 o;
+    o.x = e4m3x4(x[0] * inv, x[1] * inv, x[2] * inv, x[3] * inv);
+    o.y = e4m3x4(x[4] * inv, x[5] * inv, x[6] * inv, x[7] * inv);
+    o.z = e4m3x4(x[8] * inv, x[9] * inv, x[10] * inv, x[11] * inv);
+    o.w = e4m3x4(x[12] * inv, x[13] * inv, x[14] * inv, x[15] * inv);
+    int64_t blk = slot / block_size, tib = slot % block_size;
+    uint8_t *dst = (kv ? v_pool : k_pool) +
+                   (((size_t)blk * hkv + h) * block_size + (size_t)tib) * head_dim + (size_t)c * 16;
+    st16(dst, o);
+}
+
+// Element-wise append for shapes whose rows are not 16-B multiples and for
+// f32<->bf16 conversion on the way into the pool.
+__global__ void __launch_bounds__(kThreads)
+append_elem_kernel(const void *__restrict__ k, const void *__restrict__ v, void *__restrict__ k_pool,
+                   void *__restrict__ v_pool, int src_dt, int cache_dt,
+                   const int64_t *__restrict__ slots, const float *__restrict__ k_scales,
+                   const float *__restrict__ v_scales, const int32_t *__restrict__ token_row,
+                   uint64_t total, uint32_t hkv, uint32_t head_dim, uint32_t block_size,
+                   int64_t num_slots) {
+    uint64_t idx = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= total) return;
+    uint64_t d = idx % head_dim;
+    uint64_t r = idx / head_dim;
+    uint64_t h = r % hkv;
+    r /= hkv;
+    uint32_t kv = (uint32_t)(r & 1u);
+    uint64_t t = r >> 1;
+    int64_t slot = slots[t];
+    if (slot < 0 || slot >= num_slots) return;
+    uint64_t src_i = (t * hkv + h) * head_dim + d;
+    const void *src = kv ? v : k;
+    int64_t blk = slot / block_size, tib = slot % block_size;
+    uint64_t dst_i = (((uint64_t)blk * hkv + h) * block_size + (uint64_t)tib) * head_dim + d;
+    void *pool = kv ? v_pool : k_pool;
+    if (src_dt == cache_dt) {
+        if (cache_dt == ZK_F32) ((float *)pool)[dst_i] = ((const float *)src)[src_i];
+        else ((uint16_t *)pool)[dst_i] = ((const uint16_t *)src)[src_i];
+        return;
+    }
+    float x = src_dt == ZK_F32 ? ((const float *)src)[src_i]
+                               : __uint_as_float((uint32_t)((const uint16_t *)src)[src_i] << 16);
+    if (cache_dt == ZK_F32) {
+        ((float *)pool)[dst_i] = x;
+    } else if (cache_dt == ZK_BF16) {
+        ((uint16_t *)pool)[dst_i] = (uint16_t)f32_to_bf16_bits(x);
+    } else {
+        float s = (kv ? v_scales : k_scales)[(size_t)token_row[t] * hkv + h];
+        float inv = 1.0f / s;
+        ((uint8_t *)pool)[dst_i] = (uint8_t)(e4m3x4(x * inv, 0.f, 0.f, 0.f) & 0xffu);
+    }
+}
+
+// ------------------------------------------------------------- fp8 scales
+__global__ void __launch_bounds__(kThreads)
+fp8_scales_kernel(const void *__restrict__ x, int src_dt, const int64_t *__restrict__ cu,
+                  uint32_t hkv, uint32_t head_dim, float *__restrict__ scales) {
+    __shared__ float red[kThreads / 64];
+    uint32_t n = blockIdx.x, h = blockIdx.y;
+    int64_t t0 = cu[n], t1 = cu[n + 1];
+    uint64_t cnt = (uint64_t)(t1 > t0 ? t1 - t0 : 0) * head_dim;
+    float amax = 0.0f;
+    for (uint64_t i = threadIdx.x; i < cnt; i += kThreads) {
+        uint64_t t = (uint64_t)t0 + i / head_dim, d = i % head_dim;
+        uint64_t off = (t * hkv + h) * head_dim + d;
+        float val = src_dt == ZK_F32 ? ((const float *)x)[off]
+                                     : __uint_as_float((uint32_t)((const uint16_t *)x)[off] << 16);
+        amax = fmaxf(amax, fabsf(val));
+    }
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float m = red[0];
+        for (int i = 1; i < kThreads / 64; ++i) m = fmaxf(m, red[i]);
+        scales[(size_t)n * hkv + h] = m > 0.0f ? m / 448.0f : 1.0f;
+    }
+}
+
+// ------------------------------------------------------------------ gather
+// One workgroup per (page index j, sequence n).  The walk stops at the first
+// table entry that is negative or >= num_blocks (paged_attention.cu:66-67),
+// so page j is copied only when entries 0..j are all valid.
+__global__ void __launch_bounds__(kThreads)
+gather_kernel(const char *__restrict__ k_pool, const char *__restrict__ v_pool,
+              const int32_t *__restrict__ bt, uint32_t max_blocks, const int32_t *__restrict__ ctx,
+              const int64_t *__restrict__ out_off, char *__restrict__ k_out, char *__restrict__ v_out,
+              uint32_t hkv, uint32_t row_bytes, uint32_t block_size, int64_t num_blocks, bool vec16) {
+    uint32_t j = blockIdx.x, n = blockIdx.y;
+    int64_t len = ctx[n];
+    if ((int64_t)j * block_size >= len) return;
+    const int32_t *row = bt + (size_t)n * max_blocks;
+    int bad = 0;
+    for (uint32_t i = threadIdx.x; i <= j; i += kThreads) {
+        int32_t b = row[i];
+        bad |= (b < 0) | ((int64_t)b >= num_blocks);
+    }
+    if (__syncthreads_or(bad)) return;
+    int64_t blk = row[j];
+    int64_t rem = len - (int64_t)j * block_size;
+    uint32_t nt = rem < (int64_t)block_size ? (uint32_t)rem : block_size;
+    size_t dst_row0 = (size_t)(out_off[n] + (int64_t)j * block_size);
+    if (vec16) {
+        uint32_t cpr = row_bytes >> 4;
+        uint32_t total = 2u * nt * hkv * cpr;
+        for (uint32_t i = threadIdx.x; i < total; i += kThreads) {
+            uint32_t c = i % cpr, r = i / cpr;
+            uint32_t h = r % hkv;
+            r /= hkv;
+            uint32_t t = r % nt, kv = r / nt;
+            const char *src = (kv ? v_pool : k_pool) +
+                              (((size_t)blk * hkv + h) * block_size + t) * row_bytes + (size_t)c * 16;
+            char *dst = (kv ? v_out : k_out) + ((dst_row0 + t) * hkv + h) * row_bytes + (size_t)c * 16;
+            st16(dst, ld16(src));
+        }
+    } else {
+        uint32_t total = 2u * nt * hkv * row_bytes;
+        for (uint32_t i = threadIdx.x; i < total; i += kThreads) {
+            uint32_t c = i % row_bytes, r = i / row_bytes;
+            uint32_t h = r % hkv;
+            r /= hkv;
+            uint32_t t = r % nt, kv = r / nt;
+            (kv ? v_out : k_out)[((dst_row0 + t) * hkv + h) * row_bytes + c] =
+                (kv ? v_pool : k_pool)[(((size_t)blk * hkv + h) * block_size + t) * row_bytes + c];
+        }
+    }
+}
+
+// ------------------------------------------------------------- copy blocks
+constexpr int kMaxPoolsPerLaunch = 64;
+struct PoolArgs {
+    char *p[kMaxPoolsPerLaunch];
+};
+
+// One workgroup per (pair i, pool p): block dst[i] := block src[i].
+__global__ void __launch_bounds__(kThreads)
+copy_blocks_kernel(PoolArgs pools, const int32_t *__restrict__ src, const int32_t *__restrict__ dst,
+                   uint64_t block_bytes, int64_t num_blocks) {
+    uint32_t i = blockIdx.x, p = blockIdx.y;
+    int64_t s = src[i], d = dst[i];
+    if (s < 0 || d < 0 || s >= num_blocks || d >= num_blocks) return;
+    char *base = pools.p[p];
+    const char *from = base + (size_t)s * block_bytes;
+    char *to = base + (size_t)d * block_bytes;
+    if ((block_bytes & 15u) == 0 && ((uintptr_t)base & 15u) == 0) {
+        uint64_t n16 = block_bytes >> 4;
+        uint64_t i0 = threadIdx.x;
+        for (; i0 + 3 * kThreads < n16; i0 += 4 * kThreads) {
+            uint4 a = ld16(from + 16 * i0), b = ld16(from + 16 * (i0 + kThreads));
+            uint4 c = ld16(from + 16 * (i0 + 2 * kThreads)), e = ld16(from + 16 * (i0 + 3 * kThreads));
+            st16(to + 16 * i0, a);
+            st16(to + 16 * (i0 + kThreads), b);
+            st16(to + 16 * (i0 + 2 * kThreads), c);
+            st16(to + 16 * (i0 + 3 * kThreads), e);
+        }
+        for (; i0 < n16; i0 += kThreads) st16(to + 16 * i0, ld16(from + 16 * i0));
+    } else {
+        for (uint64_t b = threadIdx.x; b < block_bytes; b += kThreads) to[b] = from[b];
+    }
+}
+
+// Streaming copy (bandwidth yardstick): 4 x 16 B per lane in flight.
+__global__ void __launch_bounds__(kThreads)
+stream_copy_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, uint64_t n16) {
+    uint64_t i = (uint64_t)blockIdx.x * kThreads * 4 + threadIdx.x;
+    const uint64_t stride = (uint64_t)gridDim.x * kThreads * 4;
+    for (; i + 3 * kThreads < n16; i += stride) {
+        uint4 a = src[i], b = src[i + kThreads], c = src[i + 2 * kThreads], d = src[i + 3 * kThreads];
+        dst[i] = a;
+        dst[i + kThreads] = b;
+        dst[i + 2 * kThreads] = c;
+        dst[i + 3 * kThreads] = d;
+    }
+    for (; i < n16; i += kThreads) dst[i] = src[i];
+}
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(ZK_ERR_HIP, std::string("Internal error: ") + what + ": " + hipGetErrorString(e));
+    return ZK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int zk_append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, const void *v,
+              zk_dtype src_dtype, const int64_t *slot_mapping, int64_t num_tokens, int num_kv_heads,
+              int head_dim, int block_size, int64_t num_blocks, const float *k_scales,
+              const float *v_scales, const int32_t *token_row, void *stream) {
+    if (!valid_dtype(cache_dtype) || (src_dtype != ZK_F32 && src_dtype != ZK_BF16))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: unsupported dtype");
+    if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks <= 0)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: bad shape");
+    if (num_tokens == 0) return ZK_OK;
+    if (!k_pool || !v_pool || !k || !v || !slot_mapping)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: NULL pointer");
+    bool fp8 = cache_dtype == ZK_FP8_E4M3;
+    if (fp8 && (!k_scales || !v_scales || !token_row))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: fp8 pool needs scales and token_row");
+    if (!fp8 && (k_scales || v_scales || token_row))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: scales given for a non-fp8 pool");
+    hipStream_t s = (hipStream_t)stream;
+    int64_t num_slots = num_blocks * block_size;
+    uint32_t row_bytes = (uint32_t)head_dim * elt_size(cache_dtype);
+    uint64_t total_rows = (uint64_t)num_tokens * 2 * num_kv_heads;
+    bool aligned = (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_pool | (uintptr_t)v_pool) & 15u) == 0;
+    if (aligned && cache_dtype == src_dtype && (row_bytes % 16) == 0 && total_rows * (row_bytes / 16) < (1ull << 31)) {
+        uint32_t cpr = row_bytes / 16;
+        uint32_t total = (uint32_t)(total_rows * cpr);
+        uint32_t grid = (total + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+        KernelTimer timer("append", s);
+        append_copy_kernel<<<grid, kThreads, 0, s>>>((const char *)k, (const char *)v, (char *)k_pool,
+                                                     (char *)v_pool, slot_mapping, total, cpr,
+                                                     num_kv_heads, row_bytes, block_size, num_slots);
+        return check_launch("zk_append");
+    }
+    if (aligned && fp8 && (head_dim % 16) == 0 && total_rows * (head_dim / 16) < (1ull << 31)) {
+        uint32_t cpr = head_dim / 16;
+        uint32_t total = (uint32_t)(total_rows * cpr);
+        uint32_t grid = (total + kThreads - 1) / kThreads;
+        KernelTimer timer("append", s);
+        if (src_dtype == ZK_BF16)
+            append_fp8_kernel<ZK_BF16><<<grid, kThreads, 0, s>>>(
+                (const char *)k, (const char *)v, (uint8_t *)k_pool, (uint8_t *)v_pool, slot_mapping,
+                k_scales, v_scales, token_row, total, cpr, num_kv_heads, head_dim, block_size, num_slots);
+        else
+            append_fp8_kernel<ZK_F32><<<grid, kThreads, 0, s>>>(
+                (const char *)k, (const char *)v, (uint8_t *)k_pool, (uint8_t *)v_pool, slot_mapping,
+                k_scales, v_scales, token_row, total, cpr, num_kv_heads, head_dim, block_size, num_slots);
+        return check_launch("zk_append");
+    }
+    uint64_t total = total_rows * (uint64_t)head_dim;
+    uint64_t grid = (total + kThreads - 1) / kThreads;
+    if (grid > 0x7fffffffull)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: too many tokens for one launch");
+    KernelTimer timer("append", s);
+    append_elem_kernel<<<(uint32_t)grid, kThreads, 0, s>>>(k, v, k_pool, v_pool, src_dtype, cache_dtype,
+                                                           slot_mapping, k_scales, v_scales, token_row,
+                                                           total, num_kv_heads, head_dim, block_size,
+                                                           num_slots);
+    return check_launch("zk_append");
+}
+
+int zk_fp8_scales(const void *x, zk_dtype src_dtype, const int64_t *cu_seqlens, int num_seqs,
+                  int num_kv_heads, int head_dim, float *scales, void *stream) {
+    if (src_dtype != ZK_F32 && src_dtype != ZK_BF16)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_fp8_scales: unsupported dtype");
+    if (num_seqs < 0 || num_kv_heads <= 0 || head_dim <= 0)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_fp8_scales: bad shape");
+    if (num_seqs == 0) return ZK_OK;
+    if (!x || !cu_seqlens || !scales)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_fp8_scales: NULL pointer");
+    dim3 grid(num_seqs, num_kv_heads);
+    KernelTimer timer("fp8_scales", (hipStream_t)stream);
+    fp8_scales_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(x, src_dtype, cu_seqlens, num_kv_heads,
+                                                                 head_dim, scales);
+    return check_launch("zk_fp8_scales");
+}
+
+int zk_gather(const void *k_pool, const void *v_pool, zk_dtype dtype, const int32_t *block_tables,
+              int max_blocks_per_seq, const int32_t *ctx_lens, const int64_t *out_offsets, int num_seqs,
+              void *k_out, void *v_out, int num_kv_heads, int head_dim, int block_size,
+              int64_t num_blocks, void *stream) {
+    if (!valid_dtype(dtype))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_gather: unsupported dtype");
+    if (num_seqs < 0 || max_blocks_per_seq <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_gather: bad shape");
+    if (num_seqs == 0) return ZK_OK;
+    if (!k_pool || !v_pool || !block_tables || !ctx_lens || !out_offsets || !k_out || !v_out)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_gather: NULL pointer");
+    dim3 grid(max_blocks_per_seq, num_seqs);
+    uint32_t row_bytes = (uint32_t)head_dim * elt_size(dtype);
+    bool vec16 = (row_bytes % 16) == 0 &&
+                 (((uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)k_out | (uintptr_t)v_out) & 15u) == 0;
+    KernelTimer timer("gather", (hipStream_t)stream);
+    gather_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(
+        (const char *)k_pool, (const char *)v_pool, block_tables, max_blocks_per_seq, ctx_lens,
+        out_offsets, (char *)k_out, (char *)v_out, num_kv_heads, row_bytes, block_size, num_blocks, vec16);
+    return check_launch("zk_gather");
+}
+
+int zk_copy_blocks(void *const *pools, int n_pools, int64_t block_bytes, int64_t num_blocks,
+                   const int32_t *src, const int32_t *dst, int64_t n, void *stream) {
+    if (n < 0 || n_pools < 0 || block_bytes <= 0 || num_blocks <= 0)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_copy_blocks: bad shape");
+    if (n == 0 || n_pools == 0) return ZK_OK;
+    if (!pools || !src || !dst)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_copy_blocks: NULL pointer");
+    if (n > 0x7fffffff)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_copy_blocks: too many pairs");
+    for (int p0 = 0; p0 < n_pools; p0 += kMaxPoolsPerLaunch) {
+        int np = n_pools - p0 < kMaxPoolsPerLaunch ? n_pools - p0 : kMaxPoolsPerLaunch;
+        PoolArgs a{};
+        for (int i = 0; i < np; ++i) {
+            if (!pools[p0 + i])
+                return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_copy_blocks: NULL pool");
+            a.p[i] = (char *)pools[p0 + i];
+        }
+        dim3 grid((uint32_t)n, np);
+        KernelTimer timer("copy_blocks", (hipStream_t)stream);
+        copy_blocks_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(a, src, dst, (uint64_t)block_bytes,
+                                                                      num_blocks);
+        if (int rc = check_launch("zk_copy_blocks")) return rc;
+    }
+    return ZK_OK;
+}
+
+int zk_stream_copy(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return ZK_OK;
+    if (!dst || !src || (bytes & 15u) || (((uintptr_t)dst | (uintptr_t)src) & 15u))
+        return set_error(ZK_ERR_INVALID_ARGUMENT,
+                         "Internal error: zk_stream_copy: needs 16-B aligned pointers and size");
+    uint64_t n16 = bytes / 16;
+    uint64_t want = (n16 + kThreads * 4 - 1) / (kThreads * 4);
+    uint32_t grid = (uint32_t)(want < 16384 ? (want ? want : 1) : 16384);
+    KernelTimer timer("stream_copy", (hipStream_t)stream);
+    stream_copy_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>((const uint4 *)src, (uint4 *)dst, n16);
+    return check_launch("zk_stream_copy");
+}
+
+}  // extern "C"

@@ -1,0 +1,101 @@
+// zk_common.h -- shared host/device helpers of the gfx950 paged-KV library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/zealot_kv.h"
+
+namespace zk {
+
+// ------------------------------------------------------------------ errors
+// Thread-local last-error message (zk_last_error); set_error returns the code
+// so call sites read `return set_error(ZK_ERR_..., "...")`.
+int set_error(int code, const std::string &msg);
+void clear_error();
+
+#define ZK_HIP_CHECK(expr, ctx)                                                         \
+    do {                                                                                \
+        hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return ::zk::set_error(ZK_ERR_HIP, std::string("Internal error: ") + (ctx) + \
+                                                   ": " + hipGetErrorString(e_));       \
+    } while (0)
+
+// Brackets one kernel launch with hipEvents when timing is enabled
+// (zk_timing_enable); a no-op otherwise.
+class KernelTimer {
+  public:
+    KernelTimer(const char *name, hipStream_t stream);
+    ~KernelTimer();
+    KernelTimer(const KernelTimer &) = delete;
+    KernelTimer &operator=(const KernelTimer &) = delete;
+
+  private:
+    const char *name_;
+    hipStream_t stream_;
+    hipEvent_t start_ = nullptr, stop_ = nullptr;
+    bool active_ = false;
+};
+
+inline int elt_size(int dt) { return dt == ZK_F32 ? 4 : dt == ZK_BF16 ? 2 : 1; }
+inline bool valid_dtype(int dt) { return dt == ZK_F32 || dt == ZK_BF16 || dt == ZK_FP8_E4M3; }
+
+// ----------------------------------------------------------- device helpers
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// bf16 <-> f32.  A bf16 value is the high half of the f32 with the same value.
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // quiet NaN
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;                 // round to nearest even
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// f32 -> OCP e4m3 (e4m3fn), round to nearest even, saturating at +-448, NaN
+// keeps its sign as S.1111.111.  The gfx950 converter rounds in-range values
+// to nearest even; clamping first makes it saturate, and NaN is patched.
+__device__ __forceinline__ float clamp448(float x) { return fminf(fmaxf(x, -448.0f), 448.0f); }
+__device__ __forceinline__ uint32_t nan_code(float x) {
+    return (__float_as_uint(x) >> 24 & 0x80u) | 0x7fu;
+}
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(a), clamp448(b), 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(c), clamp448(d), w, true);
+    uint32_t r = (uint32_t)w;
+    if (__builtin_expect(a != a || b != b || c != c || d != d, 0)) {
+        if (a != a) r = (r & 0xffffff00u) | nan_code(a);
+        if (b != b) r = (r & 0xffff00ffu) | (nan_code(b) << 8);
+        if (c != c) r = (r & 0xff00ffffu) | (nan_code(c) << 16);
+        if (d != d) r = (r & 0x00ffffffu) | (nan_code(d) << 24);
+    }
+    return r;
+}
+// Four e4m3 bytes -> four f32 (exact).
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float *o) {
+    f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    o[0] = lo[0]; o[1] = lo[1]; o[2] = hi[0]; o[3] = hi[1];
+}
+// Four e4m3 bytes -> four bf16 packed in two dwords (exact: every e4m3 value
+// is a bf16 value, so the high half of the f32 is the bf16).
+__device__ __forceinline__ u32x2 e4m3x4_to_bf16x4(uint32_t w) {
+    f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    u32x2 r;
+    r[0] = __builtin_amdgcn_perm(__float_as_uint(lo[1]), __float_as_uint(lo[0]), 0x07060302u);
+    r[1] = __builtin_amdgcn_perm(__float_as_uint(hi[1]), __float_as_uint(hi[0]), 0x07060302u);
+    return r;
+}
+
+}  // namespace zk

@@ -1,0 +1,175 @@
+"""KVCache over the C ABI -- the host mirror of src/kv_cache.rs:51-356.
+
+Method names and argument meaning follow the reference (register_seq,
+alloc_block, release_seq, store_kv, append_kv, block_table_ptr, k_pool_ptr,
+v_pool_ptr, max_blocks, seq_state); tensors are torch device tensors and
+errors are RuntimeErrors with the reference's messages.  All state and every
+launch live in C++ (zealot_amd/csrc/kv_cache.cpp).  Additions: fork_seq
+(prefix sharing with copy-on-write), set_fp8_scales (fp8 pools), paged_decode
+(batched decode of registered sequences), k_pool/v_pool (tensor views of the
+pools, for tests and callers that launch their own kernels).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from .block_manager import BlockManager
+from .ops import zk_dtype, _stream, _dev
+
+_TORCH_TO_ZK = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+if hasattr(torch, "float8_e4m3fn"):
+    _TORCH_TO_ZK[torch.float8_e4m3fn] = _lib.FP8_E4M3
+_TORCH_TO_ZK[torch.uint8] = _lib.FP8_E4M3
+
+
+@dataclass
+class SeqKvState:
+    """kv_cache.rs:24-35 (block_table is exposed as a device pointer)."""
+    block_table: int
+    block_ids: list = field(default_factory=list)
+    cached_tokens: int = 0
+    block_offset: int = 0
+    max_blocks: int = 0
+
+
+def _id(s: str) -> bytes:
+    return s.encode("utf-8")
+
+
+class KVCache:
+    """kv_cache.rs:51-102.  One HBM slab holds every layer's K and V pool."""
+
+    def __init__(self, num_blocks: int, block_size: int, num_layers: int, num_kv_heads: int,
+                 head_dim: int, dtype=torch.float32, max_seqs: int = 256,
+                 max_blocks_per_seq: int = 1024, stream=None):
+        self._h = None
+        if dtype not in _TORCH_TO_ZK:
+            raise TypeError(f"unsupported KV dtype {dtype}")
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_layers = num_layers
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.dtype = dtype
+        self._stream_obj = stream
+        h = ctypes.c_void_p()
+        _lib.check(_lib.lib().zk_cache_create(num_blocks, block_size, num_layers, num_kv_heads,
+                                              head_dim, _TORCH_TO_ZK[dtype], max_seqs,
+                                              max_blocks_per_seq, _stream(stream), ctypes.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            _lib.lib().zk_cache_destroy(self._h)
+            self._h = None
+
+    # -- sequence lifecycle (kv_cache.rs:104-166) --------------------------
+    def register_seq(self, id: str, max_blocks: int) -> None:
+        _lib.check(_lib.lib().zk_cache_register_seq(self._h, _id(id), max_blocks))
+
+    def alloc_block(self, id: str, bm: BlockManager) -> int:
+        out = ctypes.c_size_t()
+        _lib.check(_lib.lib().zk_cache_alloc_block(self._h, _id(id), bm.handle, ctypes.byref(out)))
+        return int(out.value)
+
+    def release_seq(self, id: str) -> None:
+        _lib.check(_lib.lib().zk_cache_release_seq(self._h, _id(id)))
+
+    def fork_seq(self, parent: str, child: str) -> None:
+        _lib.check(_lib.lib().zk_cache_fork_seq(self._h, _id(parent), _id(child)))
+
+    def set_fp8_scales(self, id: str, k_scales, v_scales) -> None:
+        ks = torch.as_tensor(k_scales, dtype=torch.float32).contiguous().cpu()
+        vs = torch.as_tensor(v_scales, dtype=torch.float32).contiguous().cpu()
+        n = self.num_layers * self.num_kv_heads
+        if ks.numel() != n or vs.numel() != n:
+            raise ValueError(f"scales must hold num_layers * num_kv_heads = {n} values")
+        _lib.check(_lib.lib().zk_cache_set_fp8_scales(self._h, _id(id), ks.data_ptr(), vs.data_ptr()))
+
+    # -- queries (kv_cache.rs:168-204) --------------------------------------
+    def seq_state(self, id: str) -> SeqKvState:
+        L = _lib.lib()
+        ct, bo, nb = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        _lib.check(L.zk_cache_seq_state(self._h, _id(id), ctypes.byref(ct), ctypes.byref(bo),
+                                        ctypes.byref(nb)))
+        ids = (ctypes.c_int64 * max(1, nb.value))()
+        n = ctypes.c_size_t(nb.value)
+        _lib.check(L.zk_cache_block_ids(self._h, _id(id), ids, ctypes.byref(n)))
+        return SeqKvState(block_table=self.block_table_ptr(id), block_ids=list(ids[:n.value]),
+                          cached_tokens=ct.value, block_offset=bo.value,
+                          max_blocks=self.max_blocks(id))
+
+    def max_blocks(self, id: str) -> int:
+        out = ctypes.c_size_t()
+        _lib.check(_lib.lib().zk_cache_max_blocks(self._h, _id(id), ctypes.byref(out)))
+        return int(out.value)
+
+    def block_table_ptr(self, id: str) -> int:
+        out = ctypes.c_void_p()
+        _lib.check(_lib.lib().zk_cache_block_table_ptr(self._h, _id(id), ctypes.byref(out)))
+        return int(out.value)
+
+    def k_pool_ptr(self, layer: int) -> int:
+        return int(_lib.lib().zk_cache_k_pool_ptr(self._h, layer) or 0)
+
+    def v_pool_ptr(self, layer: int) -> int:
+        return int(_lib.lib().zk_cache_v_pool_ptr(self._h, layer) or 0)
+
+    # -- store / append (kv_cache.rs:206-356) -------------------------------
+    def _kv(self, k, v, rows):
+        for name, t in (("k", k), ("v", v)):
+            _dev(t, name)
+            if t.dtype not in (torch.float32, torch.bfloat16):
+                raise TypeError(f"{name} must be float32 or bfloat16")
+            if t.numel() != rows * self.num_kv_heads * self.head_dim:
+                raise RuntimeError(f"Internal error: KVCache: {name} has {t.numel()} elements, expected "
+                                   f"{rows * self.num_kv_heads * self.head_dim}")
+        if k.dtype != v.dtype:
+            raise TypeError("k and v must share a dtype")
+        return zk_dtype(k)
+
+    def store_kv(self, layer: int, id: str, k, v, start_token: int, n_tokens: int) -> None:
+        dt = self._kv(k, v, n_tokens)
+        _lib.check(_lib.lib().zk_cache_store_kv(self._h, layer, _id(id), k.data_ptr(), v.data_ptr(),
+                                                dt, start_token, n_tokens))
+
+    def append_kv(self, layer: int, id: str, k, v) -> None:
+        dt = self._kv(k, v, 1)
+        _lib.check(_lib.lib().zk_cache_append_kv(self._h, layer, _id(id), k.data_ptr(), v.data_ptr(),
+                                                 dt))
+
+    # -- decode --------------------------------------------------------------
+    def paged_decode(self, layer: int, ids, q, out=None, scale=None, mapping="grouped"):
+        """Decode attention for registered sequences `ids` (batch order), q [N, H, D]."""
+        _dev(q, "q")
+        n, h, d = q.shape
+        if n != len(ids) or d != self.head_dim:
+            raise ValueError("q must be [len(ids), H, head_dim]")
+        if out is None:
+            out = torch.empty_like(q)
+        if scale is None:
+            scale = 1.0 / math.sqrt(d)
+        arr = (ctypes.c_char_p * n)(*[_id(i) for i in ids])
+        m = {"grouped": _lib.GQA_GROUPED, "modulo": _lib.GQA_MODULO}[mapping]
+        _lib.check(_lib.lib().zk_cache_paged_decode(self._h, layer, arr, n, q.data_ptr(),
+                                                    zk_dtype(q), _dev(out, "out"), h, float(scale), m))
+        return out
+
+    # -- pool views ----------------------------------------------------------
+    def _pool_view(self, ptr: int) -> torch.Tensor:
+        """Device tensor aliasing a pool (shape [num_blocks, Hkv, bs, D])."""
+        from ._devmem import tensor_from_device_ptr
+        shape = (self.num_blocks, self.num_kv_heads, self.block_size, self.head_dim)
+        dtype = self.dtype
+        return tensor_from_device_ptr(ptr, shape, dtype, owner=self)
+
+    def k_pool(self, layer: int) -> torch.Tensor:
+        return self._pool_view(self.k_pool_ptr(layer))
+
+    def v_pool(self, layer: int) -> torch.Tensor:
+        return self._pool_view(self.v_pool_ptr(layer))
