@@ -128,3 +128,8 @@ def test_product_does_not_import_the_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "from oracle" not in text, f
                 assert "zk_oracle" not in text and "liboracle" not in text, f
+
+
+def test_package_imports_without_gpu():
+    from zealot_amd import HipAttention, KVCache, ops  # noqa: F401
+    assert callable(ops.paged_decode) and callable(ops.append)

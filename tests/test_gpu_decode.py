@@ -106,14 +106,21 @@ def test_decode_is_deterministic():
     assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("src", [oracle.BF16, oracle.F32])
-def test_fp8_kv_decode(src):
+@pytest.mark.parametrize("src,lens", [
+    (oracle.BF16, [1024, 3000, 5000, 16384]),  # C5 context range: the 5e-2 bar applies
+    (oracle.F32, [1100, 2500, 9000]),
+    (oracle.BF16, [1, 17, 200]),                # short contexts: fp8-oracle check only
+])
+def test_fp8_kv_decode(src, lens):
     """fp8 pools quantised on append (per-(seq, head) amax scales), decoded with
-    fp32 accumulation; checked against the fp32 oracle on the source values."""
+    fp32 accumulation.  For C5-range contexts (>= 1024 tokens) the output is
+    within 5e-2 of the fp32 oracle on the unquantised inputs; for any context it
+    is within 2e-2 of the oracle on the dequantised fp8 pages.  (At ctx = 1 the
+    output is one dequantised V row, whose e4m3 rounding error -- up to 2^-4
+    relative -- is not averaged away, so the 5e-2 bar is a long-context bar.)"""
     from zealot_amd import ops
     rng = np.random.default_rng(26)
     H, Hkv, D, BS = 32, 8, 128, 16
-    lens = [1, 17, 1024, 3000, 5000]
     from tests.gpu_util import normal, paged_tables
     bt, nb = paged_tables(rng, lens, BS)
     T = sum(lens)
@@ -150,8 +157,9 @@ def test_fp8_kv_decode(src):
     vp_src = np.zeros_like(kp_src)
     oracle.append_slots(kp_src, vp_src, oracle.F32, as_f32(k, src), as_f32(v, src), oracle.F32,
                         slots, Hkv, D, BS, nb)
-    ref = _oracle(q, kp_src, vp_src, bt, lens, oracle.F32, oracle.BF16, "grouped")
-    assert max_abs_err(got, ref) <= 5e-2
+    if min(lens) >= 1024:
+        ref = _oracle(q, kp_src, vp_src, bt, lens, oracle.F32, oracle.BF16, "grouped")
+        assert max_abs_err(got, ref) <= 5e-2
     # and tightly against the oracle on the dequantised fp8 pages
     ref8 = oracle.paged_decode(as_f32(q, oracle.BF16), kp_ref, vp_ref, oracle.FP8, bt, lens, Hkv, D,
                                BS, np.float32(1 / math.sqrt(D)), oracle.GROUPED, ks_ref, vs_ref, threads=8)

@@ -77,8 +77,9 @@ def test_c1_plumbing_through_kvcache():
     # errors follow kv_cache.rs
     with pytest.raises(RuntimeError, match="unknown seq nope"):
         cache.seq_state("nope")
+    one = to_dev(normal(rng, (1, H, D), oracle.F32))
     with pytest.raises(RuntimeError, match=r"block_idx 9 OOB \(have 9 blocks\)"):
-        cache.store_kv(0, "s3", to_dev(k), to_dev(v), 9 * 16, 1)
+        cache.store_kv(0, "s3", one, one, 9 * 16, 1)
     for sid in ids:
         cache.release_seq(sid)
     assert bm.free_blocks == NB

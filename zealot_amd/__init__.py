@@ -18,13 +18,11 @@ __all__ = ["BlockHandle", "BlockManager", "ZealotError", "lib", "ops", "KVCache"
 
 def __getattr__(name):
     # torch-dependent modules load lazily so BlockManager works without torch
+    import importlib
     if name == "KVCache":
-        from .kv_cache import KVCache
-        return KVCache
+        return importlib.import_module(".kv_cache", __name__).KVCache
     if name == "HipAttention":
-        from .attention import HipAttention
-        return HipAttention
+        return importlib.import_module(".attention", __name__).HipAttention
     if name == "ops":
-        from . import ops
-        return ops
+        return importlib.import_module(".ops", __name__)
     raise AttributeError(name)
