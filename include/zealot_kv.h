@@ -218,7 +218,7 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
  * synchronises on the recorded events and returns the launch count and total
  * milliseconds of one kernel name since the last reset.  Kernel names:
  * "append", "fp8_scales", "gather", "copy_blocks", "decode_seq_info",
- * "decode_partials", "decode_reduce", "stream_copy". */
+ * "decode_plan", "decode_partials", "decode_reduce", "stream_copy". */
 int zk_timing_enable(int on);
 int zk_timing_reset(void);
 int zk_timing_query(const char *kernel, int64_t *launches, double *total_ms);

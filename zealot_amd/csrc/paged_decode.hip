@@ -12,17 +12,15 @@
 // Kernels
 //   seq_info_kernel   effective length: the page walk stops at the first table
 //                     entry that is < 0 or >= num_blocks (paged_attention.cu:66-67)
+//   plan_kernel       prefix sums of partitions -> work items; resets the queue
 //   decode_mfma_kernel  bf16 / fp8 pools, D in {64,128}, G in {1,2,4,8}:
-//       QK^T on MFMA (v_mfma_f32_16x16x32_bf16): A = one 16-token page of K
-//       (rows = tokens, loaded straight from HBM, 16 B per lane), B = the G
-//       query heads replicated over the 16 columns.  Lane l then holds the
-//       scores of tokens 4*(l/16)+i (i<4) for head (l%16)%G, which are exactly
-//       the tokens whose V rows the same lane loads for the PV product, so P
-//       never leaves the lane's 16-lane row: the other heads' weights arrive by
-//       DPP quad_perm (G<=4) or ds_swizzle (G=8) broadcasts.  Each 16-lane row
-//       keeps its own online-softmax state; rows merge once per partition.
+//       persistent one-wave workgroups pull (sequence, partition, kv-head)
+//       items from an atomic queue (no tail of short waves), stream each page
+//       through LDS with global_load_lds, and run QK^T on MFMA, softmax and PV
+//       on the VALU with DPP broadcasts (details at the kernel).
 //   decode_generic_kernel  any dtype / D <= 256 / G <= 16 (fp32 pools):
-//       token-per-lane QK on the VALU, readlane-broadcast PV.
+//       one wavefront per (partition, kv-head, sequence); token-per-lane QK on
+//       the VALU, readlane-broadcast PV.
 //   decode_reduce_kernel  log-sum-exp merge of the partitions.
 // Softmax runs in the log2 domain: scores are pre-multiplied by
 // scale * log2(e) and exponentiated with exp2 (the FlashAttention trick).
@@ -43,15 +41,26 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWave = 64;
 
-int part_pages_config() {
+// Pages per work item.  ZEALOT_DECODE_PART_PAGES (1..64) overrides; otherwise
+// an item covers ~128 KiB of K+V: 16 pages of bf16 D=128, 32 of fp8 D=128.
+int part_pages_env() {
     static int v = [] {
         const char *e = std::getenv("ZEALOT_DECODE_PART_PAGES");
-        int p = e ? std::atoi(e) : 32;
-        if (p < 1) p = 1;
-        if (p > 64) p = 64;
-        return p;
+        int p = e ? std::atoi(e) : 0;
+        return p < 0 ? 0 : (p > 64 ? 64 : p);
     }();
     return v;
+}
+int part_pages_for(int kv_dtype, int head_dim, int block_size) {
+    if (int e = part_pages_env()) return e;
+    const long page_bytes = (long)block_size * head_dim * (kv_dtype == ZK_FP8_E4M3 ? 1 : 2);
+    long p = (128 * 1024) / (2 * page_bytes);
+    return (int)(p < 16 ? 16 : (p > 64 ? 64 : p));
+}
+// Smallest partition any path uses for this head_dim (sizes the workspace).
+int min_part_pages(int head_dim, int block_size) {
+    int a = part_pages_for(ZK_BF16, head_dim, block_size), b = part_pages_for(ZK_F32, head_dim, block_size);
+    return a < b ? a : b;
 }
 
 struct Params {
@@ -63,14 +72,18 @@ struct Params {
     const int32_t *seq_lens;
     const float *k_scales;
     const float *v_scales;
-    int32_t *eff_len;
+    int32_t *eff_len;     // [N] length after the page walk
+    int32_t *item_start;  // [N + 1] first work item of each sequence (MFMA path)
+    int2 *item_map;       // [N * MP] work item -> (sequence, partition) (MFMA path)
+    int32_t *work;        // [2] total items, queue head (MFMA path)
     float2 *ml;   // [N][H][MP] (m, l), log2 domain
     float *po;    // [N][H][MP][D]
-    int num_heads, num_kv_heads, head_dim, block_size, max_blocks, part_pages, max_parts;
+    int num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks, part_pages, max_parts;
     int64_t num_blocks;
     float scale_log2;  // softmax scale * log2(e)
     int grouped;       // 1: kv = h / G, 0: kv = h % Hkv
     int q_f32;         // Q / out dtype: 1 f32, 0 bf16
+    int nominal_parts; // 1: partitions counted from seq_lens (MFMA path), 0: from eff_len
 };
 
 __device__ __forceinline__ int qhead_of(const Params &p, int kvh, int j, int G) {
@@ -84,6 +97,11 @@ __device__ __forceinline__ float load_q(const Params &p, size_t i) {
 __device__ __forceinline__ void store_out(const Params &p, size_t i, float x) {
     if (p.q_f32) ((float *)p.out)[i] = x;
     else ((uint16_t *)p.out)[i] = (uint16_t)f32_to_bf16_bits(x);
+}
+
+__device__ __forceinline__ int clamped_len(const Params &p, int n) {
+    const int len = p.seq_lens[n], cap = p.max_blocks * p.block_size;
+    return len < 0 ? 0 : (len > cap ? cap : len);
 }
 
 __device__ __forceinline__ int num_parts_for(const Params &p, int len) {
@@ -142,219 +160,339 @@ __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ------------------------------------------------------------ work plan
+// One work item = (sequence, partition, kv-head), numbered sequence-major so
+// consecutive items share a sequence's pages.  plan_kernel counts
+// max(1, partitions) per sequence from the (clamped) seq_lens, writes
+// item_start[n] and the item -> (sequence, partition) map, and resets the
+// queue head; the persistent MFMA kernel pulls items with atomicAdd.
+__global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
+    __shared__ int sums[1024];
+    const int t = threadIdx.x;
+    const int per = (num_seqs + 1023) / 1024;
+    const int n0 = min(num_seqs, t * per), n1 = min(num_seqs, n0 + per);
+    int local = 0;
+    for (int n = n0; n < n1; ++n) local += max(1, num_parts_for(p, clamped_len(p, n)));
+    sums[t] = local;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+        int v = t >= o ? sums[t - o] : 0;
+        __syncthreads();
+        sums[t] += v;
+        __syncthreads();
+    }
+    int run = sums[t] - local;
+    for (int n = n0; n < n1; ++n) {
+        p.item_start[n] = run;
+        const int np = max(1, num_parts_for(p, clamped_len(p, n)));
+        for (int k = 0; k < np; ++k) p.item_map[run + k] = make_int2(n, k);
+        run += np;
+    }
+    if (t == 1023) {
+        p.item_start[num_seqs] = sums[1023];
+        p.work[0] = sums[1023] * p.num_kv_heads;  // total items
+    }
+    if (t == 0) p.work[1] = 0;  // queue head
+}
+
 // ------------------------------------------------------------ MFMA kernel
-// KV: ZK_BF16 or ZK_FP8_E4M3.  Template D (64 or 128), G (1, 2, 4, 8).
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4; no VGPRs, counted by vmcnt).
+__device__ __forceinline__ void g2l16(const void *g, lds_void *l) {
+    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+// s_waitcnt vmcnt(N) alone (gfx9 encoding: expcnt 7 and lgkmcnt 15 mean "no wait").
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+template <int BYTES>
+struct LdsVec;
+template <>
+struct LdsVec<16> { typedef u32x4 T; };
+template <>
+struct LdsVec<8> { typedef u32x2 T; };
+template <>
+struct LdsVec<4> { typedef uint32_t T; };
+
+// Persistent split-K decode for bf16 / fp8 pools, D in {64, 128}, block_size 16,
+// G = H/Hkv in {1, 2, 4, 8}.  The grid holds a fixed number of one-wave
+// workgroups; each loops over work items.  Per item, the partition's pages
+// stream through two LDS stages per wave: every page (K and V, 16 rows of
+// D elements each) arrives by global_load_lds_dwordx4, 1 KiB contiguous per
+// instruction, so the next page is in flight while this one is computed.
+//   K stage layout: 16-byte chunk c of row r sits at chunk slot
+//     r * CPR + (c ^ (r % CPR)), so the MFMA fragment reads (16 rows, same c)
+//     hit distinct LDS banks.
+//   V stage layout: natural [row][D].
+// Scores: QK^T on v_mfma_f32_16x16x32_bf16 with A = K rows (tokens), B = the G
+// query heads replicated over the 16 columns; lane l gets tokens 4*(l/16)+i of
+// head (l%16)%G.  PV: each lane accumulates D/16 dims of all G heads for the
+// four tokens 4*(l/16)+r, taking the other heads' weights by DPP/ds_swizzle
+// broadcasts; each 16-lane row keeps its own online-softmax state and the
+// rows merge once per item.
 template <int KV, int D, int G>
 __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
-    constexpr int BS = 16;          // tokens per page (block_size)
-    constexpr int DG = D / 4;       // dims per 16-lane row in the QK operand
-    constexpr int KK = DG / 8;      // MFMA steps over the head dim
-    constexpr int DV = D / 16;      // dims per lane in the PV product
+    constexpr int BS = 16;
     constexpr int ELT = KV == ZK_BF16 ? 2 : 1;
-    constexpr int KBYTES = DG * ELT;  // K bytes per lane per page
-    constexpr int VBYTES = DV * ELT;  // V bytes per lane per token row
-    static_assert(KBYTES % 16 == 0 || KBYTES == 8, "K fragment size");
+    constexpr int DG = D / 4;            // head dims per 16-lane row in QK
+    constexpr int KK = DG / 8;           // MFMA k-steps
+    constexpr int DV = D / 16;           // dims per lane in PV
+    constexpr int RB = D * ELT;          // bytes per token row
+    constexpr int CPR = RB / 16;         // 16-byte chunks per row
+    constexpr int PAGE = BS * RB;        // bytes per (block, kv-head) page
+    constexpr int LPK = PAGE / 1024;     // global_load_lds per page of K (or V)
+    constexpr int LPP = 2 * LPK;         // per page, K and V
+    constexpr int KBYTES = DG * ELT;     // K fragment bytes per lane per page
+    constexpr int KCH = KBYTES / 16;     // ... in 16-byte chunks
+    constexpr int VBYTES = DV * ELT;     // V bytes per lane per token row
+    static_assert(PAGE % 1024 == 0 && KBYTES % 16 == 0, "page shape");
+    typedef typename LdsVec<VBYTES>::T vrow_t;
+    __shared__ __attribute__((aligned(16))) char lds[2][2][PAGE];  // [stage][K|V]
 
-    const int part = blockIdx.x, kvh = blockIdx.y, n = blockIdx.z;
-    const int lane = threadIdx.x;
-    const int col = lane & 15, grp = lane >> 4;
-    const int len = p.eff_len[n];
-    const int pages = (len + BS - 1) / BS;
-    const int nparts = (pages + p.part_pages - 1) / p.part_pages;
-    if (part >= (nparts > 0 ? nparts : 1)) return;
+    const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
     const int H = p.num_heads, Hkv = p.num_kv_heads;
-
-    // ---- Q fragments (B operand): column col -> head col % G
     const int my_head = col % G;
-    bf16x8 qf[KK];
-    {
-        const size_t qb = ((size_t)n * H + qhead_of(p, kvh, my_head, G)) * D + (size_t)grp * DG;
+
+    // per-lane byte offsets, fixed for the whole kernel
+    uint32_t kg[LPK], vg[LPK];  // global offsets inside a page
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            uint32_t w[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float a = load_q(p, qb + 8 * kk + 2 * j), b = load_q(p, qb + 8 * kk + 2 * j + 1);
-                w[j] = p.q_f32 ? pack_bf16x2(a, b) : (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
-            }
-            u32x4 v = {w[0], w[1], w[2], w[3]};
-            qf[kk] = __builtin_bit_cast(bf16x8, v);
-        }
+    for (int j = 0; j < LPK; ++j) {
+        const int q = 64 * j + lane, row = q / CPR, c = (q % CPR) ^ (row % CPR);
+        kg[j] = row * RB + c * 16;
+        vg[j] = q * 16;
     }
-    float sl2 = p.scale_log2;
-    float vscale = 1.0f;
-    if constexpr (KV == ZK_FP8_E4M3) {
-        sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
-        vscale = p.v_scales[(size_t)n * Hkv + kvh];
+    uint32_t kl[KCH];  // LDS offsets of this lane's K fragment chunks
+#pragma unroll
+    for (int f = 0; f < KCH; ++f) {
+        const int row = col, c = grp * KCH + f;
+        kl[f] = (row * CPR + (c ^ (row % CPR))) * 16;
     }
+    const uint32_t vl = (uint32_t)((4 * grp) * RB + col * VBYTES);  // + r * RB
 
-    const int page0 = part * p.part_pages;
-    const int np = nparts > 0 ? min(p.part_pages, pages - page0) : 0;
-    // Block ids of this partition: lane i holds page page0 + i.
-    const int32_t *btrow = p.bt + (size_t)n * p.max_blocks + page0;
-    int bid_lane = lane < np ? btrow[lane] : 0;
-
-    const size_t page_elems = (size_t)BS * D;
-    const size_t head_stride = page_elems;             // (block, head) page
-    const size_t block_stride = page_elems * Hkv;      // block
-    const char *kbase = p.k_pool + ((size_t)kvh * head_stride) * ELT;
-    const char *vbase = p.v_pool + ((size_t)kvh * head_stride) * ELT;
-    // lane offsets inside a page (bytes)
-    const size_t k_lane_off = ((size_t)col * D + (size_t)grp * DG) * ELT;
-    const size_t v_lane_off = ((size_t)(4 * grp) * D + (size_t)col * DV) * ELT;
-
-    typedef uint32_t kfrag_t __attribute__((ext_vector_type(KBYTES / 4)));
-    typedef uint32_t vrow_t __attribute__((ext_vector_type(VBYTES >= 4 ? VBYTES / 4 : 1)));
-    kfrag_t kcur, knext;
-    vrow_t vcur[4], vnext[4];
-
-    auto load_page = [&](int pi, kfrag_t &kf, vrow_t *vr) {
-        int blk = __builtin_amdgcn_readlane(bid_lane, pi);
-        const char *kp = kbase + (size_t)blk * block_stride * ELT + k_lane_off;
-        const char *vp = vbase + (size_t)blk * block_stride * ELT + v_lane_off;
-        kf = *reinterpret_cast<const kfrag_t *>(kp);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vr[r] = *reinterpret_cast<const vrow_t *>(vp + (size_t)r * D * ELT);
-    };
-
-    float o[G][DV];
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int d = 0; d < DV; ++d) o[h][d] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    if (np > 0) load_page(0, kcur, vcur);
-    for (int pi = 0; pi < np; ++pi) {
-        if (pi + 1 < np) load_page(pi + 1, knext, vnext);
-
-        // ---- scores: S[token 4*grp + i][col] for i < 4
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            bf16x8 a;
-            if constexpr (KV == ZK_BF16) {
-                u32x4 w = {kcur[4 * kk], kcur[4 * kk + 1], kcur[4 * kk + 2], kcur[4 * kk + 3]};
-                a = __builtin_bit_cast(bf16x8, w);
-            } else {
-                u32x2 lo = e4m3x4_to_bf16x4(kcur[2 * kk]);
-                u32x2 hi = e4m3x4_to_bf16x4(kcur[2 * kk + 1]);
-                u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
-                a = __builtin_bit_cast(bf16x8, w);
-            }
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[kk], acc, 0, 0, 0);
+    const int total = p.work[0];
+    int item = 0;
+    if (lane == 0) item = atomicAdd(&p.work[1], 1);
+    item = __builtin_amdgcn_readfirstlane(item);
+    while (item < total) {
+        int next = 0;
+        if (lane == 0) next = atomicAdd(&p.work[1], 1);  // older than this item's page loads
+        const int kvh = item % Hkv;
+        const int2 np_pair = p.item_map[item / Hkv];
+        const int n = np_pair.x, part = np_pair.y;
+        const int len_nom = clamped_len(p, n);
+        const int pages_nom = (len_nom + BS - 1) / BS;
+        const int nparts = (pages_nom + p.part_pages - 1) / p.part_pages;
+        const int page0 = part * p.part_pages;
+        const int np_nom = nparts > 0 ? min(p.part_pages, pages_nom - page0) : 0;
+        // The page walk stops at the first table entry < 0 or >= num_blocks
+        // (paged_attention.cu:66-67): scan entries [0, page0 + np_nom).
+        const int32_t *row = p.bt + (size_t)n * p.max_blocks;
+        const int scan = page0 + np_nom;
+        int bad = scan;
+        for (int i = lane; i < scan; i += kWave) {
+            const int32_t b = row[i];
+            if (b < 0 || (int64_t)b >= p.num_blocks) bad = min(bad, i);
         }
-        const int tok0 = (page0 + pi) * BS + 4 * grp;
-        float s[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] = (tok0 + i < len) ? acc[i] * sl2 : -INFINITY;
+        for (int o = 32; o > 0; o >>= 1) bad = min(bad, __shfl_xor(bad, o));
+        const int np = max(0, min(np_nom, bad - page0));
+        const int len = min(len_nom, bad * BS);
 
-        // ---- V rows of tokens 4*grp + r, dims col*DV .. +DV (as f32)
-        float v[4][DV];
+        // Q fragment (B operand): column col -> head col % G
+        bf16x8 qf[KK];
+        {
+            const size_t qb = ((size_t)n * H + qhead_of(p, kvh, my_head, G)) * D + (size_t)grp * DG;
+            if (p.q_f32) {
+                const float *qq = (const float *)p.q + qb;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if constexpr (KV == ZK_BF16) {
+                for (int kk = 0; kk < KK; ++kk) {
+                    u32x4 w;
 #pragma unroll
-                for (int j = 0; j < DV / 2; ++j) {
-                    v[r][2 * j] = bf16lo(vcur[r][j]);
-                    v[r][2 * j + 1] = bf16hi(vcur[r][j]);
+                    for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(qq[8 * kk + 2 * j], qq[8 * kk + 2 * j + 1]);
+                    qf[kk] = __builtin_bit_cast(bf16x8, w);
                 }
             } else {
+                const uint16_t *qq = (const uint16_t *)p.q + qb;
 #pragma unroll
-                for (int j = 0; j < DV / 4; ++j) e4m3x4_to_f32(vcur[r][j], &v[r][4 * j]);
+                for (int kk = 0; kk < KK; ++kk) qf[kk] = *reinterpret_cast<const bf16x8 *>(qq + 8 * kk);
             }
         }
-        if (tok0 + 4 > len) {  // partial last page: stale rows must not reach O
+        float sl2 = p.scale_log2, vscale = 1.0f;
+        if constexpr (KV == ZK_FP8_E4M3) {
+            sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
+            vscale = p.v_scales[(size_t)n * Hkv + kvh];
+        }
+        const int bid_lane = lane < np ? row[page0 + lane] : 0;
+        const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
+        const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
+        const size_t block_bytes = (size_t)PAGE * Hkv;
+
+        auto issue = [&](int pi, int s) {
+            const int blk = __builtin_amdgcn_readlane(bid_lane, pi);
+            const char *kp = kbase + (size_t)blk * block_bytes;
+            const char *vp = vbase + (size_t)blk * block_bytes;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (tok0 + r >= len)
+            for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[s][0] + 1024 * j));
 #pragma unroll
-                    for (int d = 0; d < DV; ++d) v[r][d] = 0.0f;
+            for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[s][1] + 1024 * j));
+        };
+
+        float o[G][DV];
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int d = 0; d < DV; ++d) o[h][d] = 0.0f;
+        float m_run = -INFINITY, l_run = 0.0f;
+
+        auto page = [&](int pi, int s) {
+            if (pi + 1 < np) wait_vmcnt<LPP>();  // page pi landed, pi + 1 may still fly
+            else wait_vmcnt<0>();
+            uint32_t kw[KBYTES / 4];
+#pragma unroll
+            for (int f = 0; f < KCH; ++f) {
+                const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[s][0] + kl[f]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kw[4 * f + j] = c4[j];
+            }
+            vrow_t vr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) vr[r] = *reinterpret_cast<const vrow_t *>(lds[s][1] + vl + r * RB);
+            wait_lgkmcnt0();
+            if (pi + 2 < np) issue(pi + 2, s);  // the stage is free again
+
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                u32x4 w;
+                if constexpr (KV == ZK_BF16) {
+                    w = u32x4{kw[4 * kk], kw[4 * kk + 1], kw[4 * kk + 2], kw[4 * kk + 3]};
+                } else {
+                    const u32x2 lo2 = e4m3x4_to_bf16x4(kw[2 * kk]), hi2 = e4m3x4_to_bf16x4(kw[2 * kk + 1]);
+                    w = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), qf[kk], acc, 0, 0, 0);
+            }
+            const int tok0 = (page0 + pi) * BS + 4 * grp;
+            float sc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < len) ? acc[i] * sl2 : -INFINITY;
+
+            float v[4][DV];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                uint32_t w[VBYTES / 4];
+                __builtin_memcpy(w, &vr[r], VBYTES);
+                if constexpr (KV == ZK_BF16) {
+#pragma unroll
+                    for (int j = 0; j < DV / 2; ++j) {
+                        v[r][2 * j] = bf16lo(w[j]);
+                        v[r][2 * j + 1] = bf16hi(w[j]);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < DV / 4; ++j) e4m3x4_to_f32(w[j], &v[r][4 * j]);
+                }
+            }
+            if (tok0 + 4 > len) {  // partial last page: stale rows must not reach O
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (tok0 + r >= len)
+#pragma unroll
+                        for (int d = 0; d < DV; ++d) v[r][d] = 0.0f;
+            }
+
+            const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            const float m_new = fmaxf(m_run, mx);
+            float alpha, pr[4];
+            if (m_new == -INFINITY) {
+                alpha = 1.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pr[i] = 0.0f;
+            } else {
+                alpha = exp2_fast(m_run - m_new);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pr[i] = exp2_fast(sc[i] - m_new);
+            }
+            l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+            m_run = m_new;
+            static_for<G>([&](auto hc) {
+                constexpr int h = decltype(hc)::value;
+                const float a_h = head_bcast<G, h>(alpha);
+                float ph[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ph[r] = head_bcast<G, h>(pr[r]);
+#pragma unroll
+                for (int d = 0; d < DV; ++d) {
+                    float x = o[h][d] * a_h;
+                    x = fmaf(ph[0], v[0][d], x);
+                    x = fmaf(ph[1], v[1][d], x);
+                    x = fmaf(ph[2], v[2][d], x);
+                    x = fmaf(ph[3], v[3][d], x);
+                    o[h][d] = x;
+                }
+            });
+        };
+
+        if (np > 0) issue(0, 0);
+        if (np > 1) issue(1, 1);
+        for (int pi = 0; pi < np; pi += 2) {
+            page(pi, 0);
+            if (pi + 1 < np) page(pi + 1, 1);
         }
 
-        // ---- online softmax, per 16-lane row, for head my_head
-        float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        float m_new = fmaxf(m_run, mx);
-        float alpha, pr[4];
-        if (m_new == -INFINITY) {
-            alpha = 1.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pr[i] = 0.0f;
-        } else {
-            alpha = exp2_fast(m_run - m_new);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pr[i] = exp2_fast(s[i] - m_new);
-        }
-        l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-        m_run = m_new;
-
+        // merge the four 16-lane rows
+        float M = fmaxf(m_run, xor16(m_run));
+        M = fmaxf(M, xor32(M));
+        const float f = (m_run == -INFINITY) ? 0.0f : exp2_fast(m_run - M);
+        float lsum = l_run * f;
+        lsum += xor16(lsum);
+        lsum += xor32(lsum);
         static_for<G>([&](auto hc) {
             constexpr int h = decltype(hc)::value;
-            const float a_h = head_bcast<G, h>(alpha);
-            float ph[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ph[r] = head_bcast<G, h>(pr[r]);
+            const float f_h = head_bcast<G, h>(f);
 #pragma unroll
             for (int d = 0; d < DV; ++d) {
-                float x = o[h][d] * a_h;
-                x = fmaf(ph[0], v[0][d], x);
-                x = fmaf(ph[1], v[1][d], x);
-                x = fmaf(ph[2], v[2][d], x);
-                x = fmaf(ph[3], v[3][d], x);
-                o[h][d] = x;
+                float x = o[h][d] * f_h;
+                x += xor16(x);
+                x += xor32(x);
+                o[h][d] = x * vscale;
             }
         });
-
-        if (pi + 1 < np) {
-            kcur = knext;
+        // lanes 0..15 hold o[h][col*DV + d]; lane h < G holds (M, lsum) of head h
+        if (nparts <= 1) {
+            static_for<G>([&](auto hc) {
+                constexpr int h = decltype(hc)::value;
+                const float l_h = head_bcast<G, h>(lsum);
+                const float inv = l_h > 0.0f ? 1.0f / l_h : 0.0f;
+                if (grp == 0) {
+                    const size_t ob = ((size_t)n * H + qhead_of(p, kvh, h, G)) * D + (size_t)col * DV;
+                    if (p.q_f32) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) vcur[r] = vnext[r];
+                        for (int d = 0; d < DV; ++d) ((float *)p.out)[ob + d] = o[h][d] * inv;
+                    } else {
+#pragma unroll
+                        for (int d = 0; d < DV; ++d) ((uint16_t *)p.out)[ob + d] = (uint16_t)f32_to_bf16_bits(o[h][d] * inv);
+                    }
+                }
+            });
+        } else {
+            static_for<G>([&](auto hc) {
+                constexpr int h = decltype(hc)::value;
+                const size_t slot = ((size_t)n * H + qhead_of(p, kvh, h, G)) * p.max_parts + part;
+                if (grp == 0) {
+                    float *dst = p.po + slot * D + (size_t)col * DV;
+#pragma unroll
+                    for (int d = 0; d < DV; ++d) dst[d] = o[h][d];
+                }
+                if (lane == h) p.ml[slot] = make_float2(M, lsum);
+            });
         }
-    }
-
-    // ---- merge the four 16-lane rows
-    float M = fmaxf(m_run, xor16(m_run));
-    M = fmaxf(M, xor32(M));
-    float f = (m_run == -INFINITY) ? 0.0f : exp2_fast(m_run - M);
-    float lsum = l_run * f;
-    lsum += xor16(lsum);
-    lsum += xor32(lsum);
-    static_for<G>([&](auto hc) {
-        constexpr int h = decltype(hc)::value;
-        const float f_h = head_bcast<G, h>(f);
-#pragma unroll
-        for (int d = 0; d < DV; ++d) {
-            float x = o[h][d] * f_h;
-            x += xor16(x);
-            x += xor32(x);
-            o[h][d] = x * vscale;
-        }
-    });
-
-    // Lanes 0..15 now hold o[h][col*DV + d]; lanes h < G hold (M, lsum) of head h.
-    if (nparts <= 1) {
-        static_for<G>([&](auto hc) {
-            constexpr int h = decltype(hc)::value;
-            const float l_h = head_bcast<G, h>(lsum);
-            const float inv = l_h > 0.0f ? 1.0f / l_h : 0.0f;
-            if (grp == 0) {
-                const size_t ob = ((size_t)n * H + qhead_of(p, kvh, h, G)) * D + (size_t)col * DV;
-#pragma unroll
-                for (int d = 0; d < DV; ++d) store_out(p, ob + d, o[h][d] * inv);
-            }
-        });
-    } else {
-        static_for<G>([&](auto hc) {
-            constexpr int h = decltype(hc)::value;
-            const int qh = qhead_of(p, kvh, h, G);
-            const size_t slot = ((size_t)n * H + qh) * p.max_parts + part;
-            if (grp == 0) {
-                float *dst = p.po + slot * D + (size_t)col * DV;
-#pragma unroll
-                for (int d = 0; d < DV; ++d) dst[d] = o[h][d];
-            }
-            if (lane == h) p.ml[slot] = make_float2(M, lsum);
-        });
+        item = __builtin_amdgcn_readfirstlane(next);
     }
 }
 
@@ -488,10 +626,12 @@ __global__ void __launch_bounds__(kWave) decode_generic_kernel(Params p) {
 }
 
 // ------------------------------------------------------------ reduce
-// One wavefront per (q-head, sequence): o = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p.
+// One wavefront per (q-head, sequence): o = sum_p w_p o_p / sum_p w_p l_p with
+// w_p = 2^(m_p - M).  Lane i owns partition i's weight; the weighted sum walks
+// the partitions eight at a time so 16 loads per lane are in flight.
 __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    const int len = p.eff_len[n];
+    const int len = p.nominal_parts ? clamped_len(p, n) : p.eff_len[n];
     const int nparts = num_parts_for(p, len);
     if (nparts <= 1) return;
     const int D = p.head_dim;
@@ -501,31 +641,50 @@ __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
     float L = 0.0f;
     for (int i = lane; i < nparts; i += kWave) {
-        float2 v = p.ml[base + i];
+        const float2 v = p.ml[base + i];
         L += v.x == -INFINITY ? 0.0f : v.y * exp2f(v.x - M);
     }
     for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    for (int d = lane; d < D; d += kWave) {
-        float acc = 0.0f;
-        for (int i = 0; i < nparts; ++i) {
-            float2 v = p.ml[base + i];
-            float w = v.x == -INFINITY ? 0.0f : exp2f(v.x - M);
-            acc = fmaf(w, p.po[(base + i) * D + d], acc);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // d = lane + 64 * c, D <= 256
+    for (int c0 = 0; c0 < nparts; c0 += kWave) {
+        float w = 0.0f;
+        if (c0 + lane < nparts) {
+            const float2 v = p.ml[base + c0 + lane];
+            w = v.x == -INFINITY ? 0.0f : exp2f(v.x - M);
         }
-        store_out(p, ((size_t)n * p.num_heads + h) * D + d, acc * inv);
+        const int cnt = min(kWave, nparts - c0);
+        for (int i0 = 0; i0 < cnt; i0 += 8) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + u;
+                if (i < cnt) {
+                    const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i));
+                    const float *src = p.po + (base + c0 + i) * D;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (lane + 64 * c < D) acc[c] = fmaf(wi, src[lane + 64 * c], acc[c]);
+                }
+            }
+        }
     }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        if (lane + 64 * c < D) store_out(p, ((size_t)n * p.num_heads + h) * D + lane + 64 * c, acc[c] * inv);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
-    size_t eff, ml, po, total;
+    size_t eff, items, map, work, ml, po, total;
 };
 WsLayout ws_layout(int num_seqs, int num_heads, int head_dim, int max_parts) {
     WsLayout w;
     w.eff = 0;
-    w.ml = align256(sizeof(int32_t) * (size_t)num_seqs);
+    w.items = align256(sizeof(int32_t) * (size_t)num_seqs);
+    w.map = w.items + align256(sizeof(int32_t) * ((size_t)num_seqs + 1));
+    w.work = w.map + align256(sizeof(int2) * (size_t)num_seqs * max_parts);
+    w.ml = w.work + 256;
     size_t slots = (size_t)num_seqs * num_heads * max_parts;
     w.po = w.ml + align256(sizeof(float2) * slots);
     w.total = w.po + align256(sizeof(float) * slots * head_dim);
@@ -534,28 +693,44 @@ WsLayout ws_layout(int num_seqs, int num_heads, int head_dim, int max_parts) {
 
 int max_parts_for(int max_blocks, int part_pages) { return (max_blocks + part_pages - 1) / part_pages; }
 
-template <int KV, int D, int G>
-void launch_mfma(const Params &p, dim3 grid, hipStream_t s) {
-    decode_mfma_kernel<KV, D, G><<<grid, kWave, 0, s>>>(p);
+int waves_per_simd_config() {
+    static int v = [] {
+        const char *e = std::getenv("ZEALOT_DECODE_WAVES_PER_SIMD");
+        int w = e ? std::atoi(e) : 2;
+        return w < 1 ? 1 : (w > 8 ? 8 : w);
+    }();
+    return v;
+}
+
+// Persistent grid: waves_per_simd one-wave workgroups per SIMD (4 SIMDs per CU).
+int persistent_grid() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return cus * 4 * waves_per_simd_config();
 }
 
 template <int KV, int D>
-bool dispatch_g(const Params &p, dim3 grid, hipStream_t s, int G) {
+bool launch_mfma_g(const Params &p, int grid, hipStream_t s, int G) {
     switch (G) {
-        case 1: launch_mfma<KV, D, 1>(p, grid, s); return true;
-        case 2: launch_mfma<KV, D, 2>(p, grid, s); return true;
-        case 4: launch_mfma<KV, D, 4>(p, grid, s); return true;
-        case 8: launch_mfma<KV, D, 8>(p, grid, s); return true;
+        case 1: decode_mfma_kernel<KV, D, 1><<<grid, kWave, 0, s>>>(p); return true;
+        case 2: decode_mfma_kernel<KV, D, 2><<<grid, kWave, 0, s>>>(p); return true;
+        case 4: decode_mfma_kernel<KV, D, 4><<<grid, kWave, 0, s>>>(p); return true;
+        case 8: decode_mfma_kernel<KV, D, 8><<<grid, kWave, 0, s>>>(p); return true;
         default: return false;
     }
 }
 
 template <int KV>
-bool dispatch_mfma(const Params &p, dim3 grid, hipStream_t s, int G) {
-    if (p.block_size != 16) return false;
-    if (p.head_dim == 128) return dispatch_g<KV, 128>(p, grid, s, G);
-    if (p.head_dim == 64) return dispatch_g<KV, 64>(p, grid, s, G);
-    return false;
+bool launch_mfma(const Params &p, int grid, hipStream_t s, int G) {
+    if (p.head_dim == 128) return launch_mfma_g<KV, 128>(p, grid, s, G);
+    return launch_mfma_g<KV, 64>(p, grid, s, G);
+}
+
+bool mfma_supported(int kv_dtype, int head_dim, int block_size, int G) {
+    return (kv_dtype == ZK_BF16 || kv_dtype == ZK_FP8_E4M3) && block_size == 16 &&
+           (head_dim == 128 || head_dim == 64) && (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
 int check_launch(const char *what) {
@@ -571,9 +746,9 @@ extern "C" {
 
 size_t zk_paged_decode_workspace_size(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq,
                                       int block_size) {
-    (void)block_size;
     if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0) return 256;
-    return ws_layout(num_seqs, num_heads, head_dim, max_parts_for(max_blocks_per_seq, part_pages_config()))
+    return ws_layout(num_seqs, num_heads, head_dim,
+                     max_parts_for(max_blocks_per_seq, min_part_pages(head_dim, block_size)))
         .total;
 }
 
@@ -608,7 +783,8 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
     if (fp8 != (k_scales != nullptr && v_scales != nullptr))
         return set_error(ZK_ERR_INVALID_ARGUMENT,
                          "Internal error: zk_paged_decode: fp8 pools need k/v scales, other pools none");
-    const int part_pages = part_pages_config();
+    const bool use_mfma = mfma_supported(kv_dtype, head_dim, block_size, G);
+    const int part_pages = part_pages_for(use_mfma ? kv_dtype : ZK_F32, head_dim, block_size);
     const int max_parts = max_parts_for(max_blocks_per_seq, part_pages);
     WsLayout w = ws_layout(num_seqs, num_heads, head_dim, max_parts);
     if (workspace_bytes < w.total || ((uintptr_t)workspace & 255u))
@@ -627,8 +803,12 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
     p.v_scales = v_scales;
     char *ws = (char *)workspace;
     p.eff_len = (int32_t *)(ws + w.eff);
+    p.item_start = (int32_t *)(ws + w.items);
+    p.item_map = (int2 *)(ws + w.map);
+    p.work = (int32_t *)(ws + w.work);
     p.ml = (float2 *)(ws + w.ml);
     p.po = (float *)(ws + w.po);
+    p.num_seqs = num_seqs;
     p.num_heads = num_heads;
     p.num_kv_heads = num_kv_heads;
     p.head_dim = head_dim;
@@ -640,25 +820,30 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
     p.scale_log2 = scale * kLog2e;
     p.grouped = mapping == ZK_GQA_GROUPED ? 1 : 0;
     p.q_f32 = q_dtype == ZK_F32 ? 1 : 0;
+    p.nominal_parts = use_mfma ? 1 : 0;
 
     hipStream_t s = (hipStream_t)stream;
-    {
-        KernelTimer timer("decode_seq_info", s);
-        seq_info_kernel<<<num_seqs, kWave, 0, s>>>(p);
-    }
-    if (int rc = check_launch("zk_paged_decode seq_info")) return rc;
-
-    dim3 grid(max_parts, num_kv_heads, num_seqs);
-    bool done = false;
-    {
-    KernelTimer timer("decode_partials", s);
-    if (kv_dtype == ZK_BF16) done = dispatch_mfma<ZK_BF16>(p, grid, s, G);
-    else if (kv_dtype == ZK_FP8_E4M3) done = dispatch_mfma<ZK_FP8_E4M3>(p, grid, s, G);
-    if (!done) {
+    if (use_mfma) {
+        {
+            KernelTimer timer("decode_plan", s);
+            plan_kernel<<<1, 1024, 0, s>>>(p, num_seqs);
+        }
+        if (int rc = check_launch("zk_paged_decode plan")) return rc;
+        KernelTimer timer("decode_partials", s);
+        const int grid = persistent_grid();
+        if (kv_dtype == ZK_BF16) launch_mfma<ZK_BF16>(p, grid, s, G);
+        else launch_mfma<ZK_FP8_E4M3>(p, grid, s, G);
+    } else {
+        {
+            KernelTimer timer("decode_seq_info", s);
+            seq_info_kernel<<<num_seqs, kWave, 0, s>>>(p);
+        }
+        if (int rc = check_launch("zk_paged_decode seq_info")) return rc;
+        KernelTimer timer("decode_partials", s);
+        dim3 grid(max_parts, num_kv_heads, num_seqs);
         if (kv_dtype == ZK_F32) decode_generic_kernel<ZK_F32><<<grid, kWave, 0, s>>>(p);
         else if (kv_dtype == ZK_BF16) decode_generic_kernel<ZK_BF16><<<grid, kWave, 0, s>>>(p);
         else decode_generic_kernel<ZK_FP8_E4M3><<<grid, kWave, 0, s>>>(p);
-    }
     }
     if (int rc = check_launch("zk_paged_decode partials")) return rc;
     if (max_parts > 1) {
