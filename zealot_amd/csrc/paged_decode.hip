@@ -57,10 +57,13 @@ int part_pages_for(int kv_dtype, int head_dim, int block_size) {
     long p = (128 * 1024) / (2 * page_bytes);
     return (int)(p < 16 ? 16 : (p > 64 ? 64 : p));
 }
-// Smallest partition any path uses for this head_dim (sizes the workspace).
+// Smallest partition any path uses (sizes the workspace): every path uses at
+// least 16 pages unless ZEALOT_DECODE_PART_PAGES asks for fewer.
 int min_part_pages(int head_dim, int block_size) {
-    int a = part_pages_for(ZK_BF16, head_dim, block_size), b = part_pages_for(ZK_F32, head_dim, block_size);
-    return a < b ? a : b;
+    (void)head_dim;
+    (void)block_size;
+    const int e = part_pages_env();
+    return e ? e : 16;
 }
 
 struct Params {
@@ -161,38 +164,55 @@ __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ------------------------------------------------------------ work plan
-// One work item = (sequence, partition, kv-head), numbered sequence-major so
-// consecutive items share a sequence's pages.  plan_kernel counts
-// max(1, partitions) per sequence from the (clamped) seq_lens, writes
-// item_start[n] and the item -> (sequence, partition) map, and resets the
-// queue head; the persistent MFMA kernel pulls items with atomicAdd.
+// A work item is (sequence, partition, kv-head).  The host picks the
+// partition length (part_pages, up to kMaxItemPages) so the queue holds a few
+// items per wave; plan_kernel lists the (sequence, partition) pairs longest
+// first (counting sort on the page count) so that the persistent waves, which
+// take items in queue order, perform greedy longest-processing-time-first
+// scheduling.  Item i is pair i / Hkv, kv-head i % Hkv.  The kernel also
+// resets the queue head.
+constexpr int kMaxItemPages = 1024;
+
+__device__ __forceinline__ int pair_pages(const Params &p, int n, int k) {
+    const int pages = (clamped_len(p, n) + p.block_size - 1) / p.block_size;
+    return max(0, min(p.part_pages, pages - k * p.part_pages));
+}
+
 __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
-    __shared__ int sums[1024];
+    __shared__ int hist[kMaxItemPages + 2];
+    __shared__ int total_pairs;
     const int t = threadIdx.x;
-    const int per = (num_seqs + 1023) / 1024;
-    const int n0 = min(num_seqs, t * per), n1 = min(num_seqs, n0 + per);
-    int local = 0;
-    for (int n = n0; n < n1; ++n) local += max(1, num_parts_for(p, clamped_len(p, n)));
-    sums[t] = local;
+    for (int i = t; i < kMaxItemPages + 2; i += 1024) hist[i] = 0;
+    if (t == 0) total_pairs = 0;
     __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-        int v = t >= o ? sums[t - o] : 0;
-        __syncthreads();
-        sums[t] += v;
-        __syncthreads();
-    }
-    int run = sums[t] - local;
-    for (int n = n0; n < n1; ++n) {
-        p.item_start[n] = run;
+    int local = 0;
+    for (int n = t; n < num_seqs; n += 1024) {
         const int np = max(1, num_parts_for(p, clamped_len(p, n)));
-        for (int k = 0; k < np; ++k) p.item_map[run + k] = make_int2(n, k);
-        run += np;
+        local += np;
+        for (int k = 0; k < np; ++k) atomicAdd(&hist[pair_pages(p, n, k)], 1);
     }
-    if (t == 1023) {
-        p.item_start[num_seqs] = sums[1023];
-        p.work[0] = sums[1023] * p.num_kv_heads;  // total items
+    atomicAdd(&total_pairs, local);
+    __syncthreads();
+    if (t == 0) {  // bin b starts after every bin with more pages
+        int run = 0;
+        for (int b = kMaxItemPages; b >= 0; --b) {
+            const int c = hist[b];
+            hist[b] = run;
+            run += c;
+        }
     }
-    if (t == 0) p.work[1] = 0;  // queue head
+    __syncthreads();
+    for (int n = t; n < num_seqs; n += 1024) {
+        const int np = max(1, num_parts_for(p, clamped_len(p, n)));
+        for (int k = 0; k < np; ++k) {
+            const int pos = atomicAdd(&hist[pair_pages(p, n, k)], 1);
+            p.item_map[pos] = make_int2(n, k);
+        }
+    }
+    if (t == 0) {
+        p.work[0] = total_pairs * p.num_kv_heads;  // total items
+        p.work[1] = 0;                             // queue head
+    }
 }
 
 // ------------------------------------------------------------ MFMA kernel
@@ -254,6 +274,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     static_assert(PAGE % 1024 == 0 && KBYTES % 16 == 0, "page shape");
     typedef typename LdsVec<VBYTES>::T vrow_t;
     __shared__ __attribute__((aligned(16))) char lds[2][2][PAGE];  // [stage][K|V]
+    __shared__ int32_t bids[kMaxItemPages];                         // this item's block ids
 
     const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
     const int H = p.num_heads, Hkv = p.num_kv_heads;
@@ -327,13 +348,14 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
             vscale = p.v_scales[(size_t)n * Hkv + kvh];
         }
-        const int bid_lane = lane < np ? row[page0 + lane] : 0;
+        for (int i = lane; i < np; i += kWave) bids[i] = row[page0 + i];
+        wait_lgkmcnt0();  // this wave's LDS writes are visible to its own reads
         const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
         const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
         const size_t block_bytes = (size_t)PAGE * Hkv;
 
         auto issue = [&](int pi, int s) {
-            const int blk = __builtin_amdgcn_readlane(bid_lane, pi);
+            const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
             const char *kp = kbase + (size_t)blk * block_bytes;
             const char *vp = vbase + (size_t)blk * block_bytes;
 #pragma unroll
@@ -696,13 +718,37 @@ int max_parts_for(int max_blocks, int part_pages) { return (max_blocks + part_pa
 int waves_per_simd_config() {
     static int v = [] {
         const char *e = std::getenv("ZEALOT_DECODE_WAVES_PER_SIMD");
-        int w = e ? std::atoi(e) : 2;
+        int w = e ? std::atoi(e) : 1;
         return w < 1 ? 1 : (w > 8 ? 8 : w);
     }();
     return v;
 }
 
 // Persistent grid: waves_per_simd one-wave workgroups per SIMD (4 SIMDs per CU).
+// Partition length for the persistent kernel: enough (sequence, partition)
+// pairs for ~ZEALOT_DECODE_ITEMS_PER_WAVE (default 2) items per wave, at least
+// 16 pages, at most kMaxItemPages.
+int items_per_wave_config() {
+    static int v = [] {
+        const char *e = std::getenv("ZEALOT_DECODE_ITEMS_PER_WAVE");
+        int w = e ? std::atoi(e) : 2;
+        return w < 1 ? 1 : (w > 64 ? 64 : w);
+    }();
+    return v;
+}
+
+int persistent_grid();
+
+int mfma_part_pages(int num_seqs, int num_kv_heads, int max_blocks) {
+    if (int e = part_pages_env()) return e;
+    const long waves = persistent_grid();
+    const long pairs = (items_per_wave_config() * waves + num_kv_heads - 1) / num_kv_heads;
+    const long per_seq = (pairs + num_seqs - 1) / num_seqs;
+    long pp = (max_blocks + per_seq - 1) / per_seq;
+    pp = (pp + 15) / 16 * 16;
+    return (int)(pp < 16 ? 16 : (pp > kMaxItemPages ? kMaxItemPages : pp));
+}
+
 int persistent_grid() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -784,7 +830,8 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
         return set_error(ZK_ERR_INVALID_ARGUMENT,
                          "Internal error: zk_paged_decode: fp8 pools need k/v scales, other pools none");
     const bool use_mfma = mfma_supported(kv_dtype, head_dim, block_size, G);
-    const int part_pages = part_pages_for(use_mfma ? kv_dtype : ZK_F32, head_dim, block_size);
+    const int part_pages = use_mfma ? mfma_part_pages(num_seqs, num_kv_heads, max_blocks_per_seq)
+                                    : part_pages_for(ZK_F32, head_dim, block_size);
     const int max_parts = max_parts_for(max_blocks_per_seq, part_pages);
     WsLayout w = ws_layout(num_seqs, num_heads, head_dim, max_parts);
     if (workspace_bytes < w.total || ((uintptr_t)workspace & 255u))
