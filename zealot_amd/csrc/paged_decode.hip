@@ -86,7 +86,6 @@ struct Params {
     float scale_log2;  // softmax scale * log2(e)
     int grouped;       // 1: kv = h / G, 0: kv = h % Hkv
     int q_f32;         // Q / out dtype: 1 f32, 0 bf16
-    int nominal_parts; // 1: partitions counted from seq_lens (MFMA path), 0: from eff_len
 };
 
 __device__ __forceinline__ int qhead_of(const Params &p, int kvh, int j, int G) {
@@ -122,11 +121,20 @@ __global__ void __launch_bounds__(kWave) seq_info_kernel(Params p) {
     int pages = (len + p.block_size - 1) / p.block_size;
     const int32_t *row = p.bt + (size_t)n * p.max_blocks;
     int first_bad = pages;
-    for (int i = threadIdx.x; i < pages; i += kWave) {
-        int32_t b = row[i];
-        if (b < 0 || (int64_t)b >= p.num_blocks) { first_bad = i; break; }
+    for (int i0 = 0; i0 < pages && first_bad == pages; i0 += 8 * kWave) {
+        int32_t b[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {  // eight independent loads in flight per lane
+            const int i = i0 + j * kWave + (int)threadIdx.x;
+            b[j] = i < pages ? row[i] : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j * kWave + (int)threadIdx.x;
+            if (i < pages && (b[j] < 0 || (int64_t)b[j] >= p.num_blocks)) first_bad = min(first_bad, i);
+        }
+        for (int o = 32; o > 0; o >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, o));
     }
-    for (int o = 32; o > 0; o >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, o));
     if (threadIdx.x == 0) p.eff_len[n] = min(len, first_bad * p.block_size);
 }
 
@@ -166,7 +174,8 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // ------------------------------------------------------------ work plan
 // A work item is (sequence, partition, kv-head).  The host picks the
 // partition length (part_pages, up to kMaxItemPages) so the queue holds a few
-// items per wave; plan_kernel lists the (sequence, partition) pairs longest
+// items per wave; plan_kernel sizes pairs from the effective lengths of
+// seq_info_kernel and lists the (sequence, partition) pairs longest
 // first (counting sort on the page count) so that the persistent waves, which
 // take items in queue order, perform greedy longest-processing-time-first
 // scheduling.  Item i is pair i / Hkv, kv-head i % Hkv.  The kernel also
@@ -174,7 +183,7 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 constexpr int kMaxItemPages = 1024;
 
 __device__ __forceinline__ int pair_pages(const Params &p, int n, int k) {
-    const int pages = (clamped_len(p, n) + p.block_size - 1) / p.block_size;
+    const int pages = (p.eff_len[n] + p.block_size - 1) / p.block_size;
     return max(0, min(p.part_pages, pages - k * p.part_pages));
 }
 
@@ -187,7 +196,7 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
     __syncthreads();
     int local = 0;
     for (int n = t; n < num_seqs; n += 1024) {
-        const int np = max(1, num_parts_for(p, clamped_len(p, n)));
+        const int np = max(1, num_parts_for(p, p.eff_len[n]));
         local += np;
         for (int k = 0; k < np; ++k) atomicAdd(&hist[pair_pages(p, n, k)], 1);
     }
@@ -203,7 +212,7 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
     }
     __syncthreads();
     for (int n = t; n < num_seqs; n += 1024) {
-        const int np = max(1, num_parts_for(p, clamped_len(p, n)));
+        const int np = max(1, num_parts_for(p, p.eff_len[n]));
         for (int k = 0; k < np; ++k) {
             const int pos = atomicAdd(&hist[pair_pages(p, n, k)], 1);
             p.item_map[pos] = make_int2(n, k);
@@ -306,23 +315,12 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         const int kvh = item % Hkv;
         const int2 np_pair = p.item_map[item / Hkv];
         const int n = np_pair.x, part = np_pair.y;
-        const int len_nom = clamped_len(p, n);
-        const int pages_nom = (len_nom + BS - 1) / BS;
-        const int nparts = (pages_nom + p.part_pages - 1) / p.part_pages;
+        const int len = p.eff_len[n];  // walk already cut at the first invalid entry
+        const int pages = (len + BS - 1) / BS;
+        const int nparts = (pages + p.part_pages - 1) / p.part_pages;
         const int page0 = part * p.part_pages;
-        const int np_nom = nparts > 0 ? min(p.part_pages, pages_nom - page0) : 0;
-        // The page walk stops at the first table entry < 0 or >= num_blocks
-        // (paged_attention.cu:66-67): scan entries [0, page0 + np_nom).
+        const int np = nparts > 0 ? min(p.part_pages, pages - page0) : 0;
         const int32_t *row = p.bt + (size_t)n * p.max_blocks;
-        const int scan = page0 + np_nom;
-        int bad = scan;
-        for (int i = lane; i < scan; i += kWave) {
-            const int32_t b = row[i];
-            if (b < 0 || (int64_t)b >= p.num_blocks) bad = min(bad, i);
-        }
-        for (int o = 32; o > 0; o >>= 1) bad = min(bad, __shfl_xor(bad, o));
-        const int np = max(0, min(np_nom, bad - page0));
-        const int len = min(len_nom, bad * BS);
 
         // Q fragment (B operand): column col -> head col % G
         bf16x8 qf[KK];
@@ -348,7 +346,19 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
             vscale = p.v_scales[(size_t)n * Hkv + kvh];
         }
-        for (int i = lane; i < np; i += kWave) bids[i] = row[page0 + i];
+        for (int i0 = 0; i0 < np; i0 += 8 * kWave) {  // eight independent loads per lane per round
+            int32_t b[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave + lane;
+                b[j] = i < np ? row[page0 + i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave + lane;
+                if (i < np) bids[i] = b[j];
+            }
+        }
         wait_lgkmcnt0();  // this wave's LDS writes are visible to its own reads
         const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
         const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
@@ -653,7 +663,7 @@ __global__ void __launch_bounds__(kWave) decode_generic_kernel(Params p) {
 // the partitions eight at a time so 16 loads per lane are in flight.
 __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    const int len = p.nominal_parts ? clamped_len(p, n) : p.eff_len[n];
+    const int len = p.eff_len[n];
     const int nparts = num_parts_for(p, len);
     if (nparts <= 1) return;
     const int D = p.head_dim;
@@ -726,12 +736,12 @@ int waves_per_simd_config() {
 
 // Persistent grid: waves_per_simd one-wave workgroups per SIMD (4 SIMDs per CU).
 // Partition length for the persistent kernel: enough (sequence, partition)
-// pairs for ~ZEALOT_DECODE_ITEMS_PER_WAVE (default 2) items per wave, at least
+// pairs for ~ZEALOT_DECODE_ITEMS_PER_WAVE (default 6) items per wave, at least
 // 16 pages, at most kMaxItemPages.
 int items_per_wave_config() {
     static int v = [] {
         const char *e = std::getenv("ZEALOT_DECODE_ITEMS_PER_WAVE");
-        int w = e ? std::atoi(e) : 2;
+        int w = e ? std::atoi(e) : 6;
         return w < 1 ? 1 : (w > 64 ? 64 : w);
     }();
     return v;
@@ -867,9 +877,13 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
     p.scale_log2 = scale * kLog2e;
     p.grouped = mapping == ZK_GQA_GROUPED ? 1 : 0;
     p.q_f32 = q_dtype == ZK_F32 ? 1 : 0;
-    p.nominal_parts = use_mfma ? 1 : 0;
 
     hipStream_t s = (hipStream_t)stream;
+    {
+        KernelTimer timer("decode_seq_info", s);
+        seq_info_kernel<<<num_seqs, kWave, 0, s>>>(p);
+    }
+    if (int rc = check_launch("zk_paged_decode seq_info")) return rc;
     if (use_mfma) {
         {
             KernelTimer timer("decode_plan", s);
@@ -881,11 +895,6 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
         if (kv_dtype == ZK_BF16) launch_mfma<ZK_BF16>(p, grid, s, G);
         else launch_mfma<ZK_FP8_E4M3>(p, grid, s, G);
     } else {
-        {
-            KernelTimer timer("decode_seq_info", s);
-            seq_info_kernel<<<num_seqs, kWave, 0, s>>>(p);
-        }
-        if (int rc = check_launch("zk_paged_decode seq_info")) return rc;
         KernelTimer timer("decode_partials", s);
         dim3 grid(max_parts, num_kv_heads, num_seqs);
         if (kv_dtype == ZK_F32) decode_generic_kernel<ZK_F32><<<grid, kWave, 0, s>>>(p);
