@@ -75,6 +75,18 @@ def timed(fn, steps, warmup, torch):
     return e0.elapsed_time(e1) / steps
 
 
+def measured_traffic(key):
+    """HBM bytes per launch of the workload's dominant kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/hbm_traffic.json, scaled
+    by the stream-copy calibration recorded there); None if absent."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(key, {}).get("bytes")
+    except (OSError, ValueError):
+        return None
+
+
 def kernel_ms(lib, name):
     import ctypes
     n = ctypes.c_int64()
@@ -162,9 +174,9 @@ def bench_decode(args, torch, ops, lib, kv="bf16"):
                       "decode_plan": p_ms},
         "ms_per_step_with_kernel_events": ms_ev,
         "roofline": {"bound": "hbm", "achieved": kgbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": kgbps / PEAK_HBM_GBPS, "traffic": None,
+                     "frac": kgbps / PEAK_HBM_GBPS, "traffic": measured_traffic(f"decode_{kv}"),
                      "kernel": "decode_partials", "kernel_bytes_per_launch": alg_kernel,
-                     "launches": k_n},
+                     "launches": k_n, "traffic_source": "profiles/hbm_traffic.json"},
     }
     del kp, vp, q, out, ws
     torch.cuda.empty_cache()
@@ -238,8 +250,9 @@ def bench_append(args, torch, ops, lib):
            "tokens_per_s": T / (ms * 1e-3), "algorithmic_bytes": alg,
            "stream_copy_gbps": copy_gbps, "frac_of_stream_copy": gbps / copy_gbps,
            "roofline": {"bound": "hbm", "achieved": kgbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                        "frac": kgbps / PEAK_HBM_GBPS, "traffic": None, "kernel": "append",
-                        "launches": k_n}}
+                        "frac": kgbps / PEAK_HBM_GBPS, "traffic": measured_traffic("append_bf16"),
+                        "kernel": "append", "launches": k_n,
+                        "traffic_source": "profiles/hbm_traffic.json"}}
     del sets, kp, vp, a, b
     torch.cuda.empty_cache()
     return res
