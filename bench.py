@@ -5,8 +5,10 @@ Headline (value): paged decode attention GB/s at the Llama-3-8B decode shape
 bf16 KV, block_size 16).  A step is one batched decode pass over all 256
 sequences; inputs are resident in HBM before the timed region.  The same run
 also measures the chunked-prefill KV append (C3: 64 x 512 tokens at
-non-aligned offsets, bf16) and the fp8-KV decode (C5: 512 sequences, context
-U[1024, 16384]) and reports them as extra fields.
+non-aligned offsets, bf16), the fp8-KV decode (C5: 512 sequences, context
+U[1024, 16384]) and prefix sharing with copy-on-write through the stateful
+KVCache (C4: 16 prefixes x 2048+r tokens x 32 layers, 128 forks, 64 decode
+steps) and reports them as extra fields.
 
 Algorithmic bytes (unique bytes that must cross HBM):
   decode  sum(ctx) * 2 * Hkv * D * elt  + Q + O + block-table entries + seq_lens
@@ -262,6 +264,152 @@ def bench_append(args, torch, ops, lib):
     return res
 
 
+# ---------------------------------------------------------------- C4 prefix CoW
+
+def bench_c4(args, torch, lib):
+    """Prefix sharing with copy-on-write through the stateful KVCache: 16
+    prefixes of 2048 + r tokens (r in [1, 15], so the tail block is partial)
+    over 32 bf16 layers, 8 forks each; the forks' first append copies their
+    shared tail (one batched copy over all 64 pools), then decode steps of
+    (append_kv_batch + paged_decode) per layer for all 128 forks."""
+    import zealot_amd as ze
+    from zealot_amd.kv_cache import KVCache, SeqBatch
+    P, F, L, H, Hkv, D, BS = 16, 8, 32, 32, 8, 128, 16
+    STEPS, EV_STEPS, COW_REPS = 64, 8, 5
+    rng = np.random.default_rng(SEED + 4)
+    plen = 2048 + rng.integers(1, BS, P)
+    grow = 1 + STEPS + EV_STEPS
+    MB = (int(plen.max()) + grow + BS - 1) // BS + 1
+    NB = sum((int(x) + BS - 1) // BS for x in plen) + P * F * ((BS - 1 + grow + BS - 1) // BS + 1) + 64
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(SEED + 4)
+    bm = ze.BlockManager(NB, BS)
+    cache = KVCache(NB, BS, L, Hkv, D, dtype=torch.bfloat16, max_seqs=P * (F + 1), max_blocks_per_seq=MB)
+    log(f"c4: prefixes={P} x {int(plen.min())}..{int(plen.max())} tokens, layers={L}, forks={P * F}, pool blocks={NB}")
+    for p in range(P):
+        pid = f"p{p}"
+        cache.register_seq(pid, MB)
+        for _ in range((int(plen[p]) + BS - 1) // BS):
+            cache.alloc_block(pid, bm)
+        for layer in range(L):
+            k = torch.randn((int(plen[p]), Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+            v = torch.randn((int(plen[p]), Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+            cache.store_kv(layer, pid, k, v, 0, int(plen[p]))
+    torch.cuda.synchronize()
+    children = [f"p{p}.f{j}" for p in range(P) for j in range(F)]
+    parent = [p for p in range(P) for _ in range(F)]
+    batch = SeqBatch(children)
+    n = len(children)
+    R = 4
+    kin = [torch.randn((n, Hkv, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(R)]
+    vin = [torch.randn((n, Hkv, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(R)]
+    qin = [torch.randn((n, H, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(R)]
+    out = torch.empty((n, H, D), dtype=torch.bfloat16, device=dev)
+    # copy-on-write: fork every prefix, then the first append copies each tail
+    cow_kernel_ms, cow_call_ms = [], []
+    for rep in range(COW_REPS):
+        for cid, p in zip(children, parent):
+            cache.fork_seq(f"p{p}", cid)
+        torch.cuda.synchronize()
+        lib.zk_timing_reset()
+        lib.zk_timing_enable(1)
+        t0 = time.perf_counter()
+        cache.append_kv_batch(0, batch, kin[0], vin[0])
+        torch.cuda.synchronize()
+        cow_call_ms.append((time.perf_counter() - t0) * 1e3)
+        lib.zk_timing_enable(0)
+        c_ms, c_n = kernel_ms(lib, "copy_blocks")
+        assert c_n == 1, c_n
+        cow_kernel_ms.append(c_ms)
+        if rep + 1 < COW_REPS:
+            for cid in children:
+                cache.release_seq(cid)
+    lib.zk_timing_reset()
+    cow_bytes = 2 * n * 2 * L * BS * Hkv * D * 2  # read + write, every pool
+    cow_ms = float(np.median(cow_kernel_ms))
+    pos = [int(plen[p]) for p in parent]  # next token position of each fork
+    nblk = [(x + BS - 1) // BS for x in pos]
+
+    def step(_):
+        for i, cid in enumerate(children):
+            if pos[i] == nblk[i] * BS:
+                cache.alloc_block(cid, bm)
+                nblk[i] += 1
+        for layer in range(L):
+            cache.append_kv_batch(layer, batch, kin[layer % R], vin[layer % R])
+            cache.paged_decode(layer, batch, qin[layer % R], out=out)
+        for i in range(n):
+            pos[i] += 1
+
+    step(0)  # warm-up step (its layer-0 append rewrites the CoW step's token)
+    torch.cuda.synchronize()
+    ctx0 = np.array(pos, np.int64)
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(s)
+    for i in range(STEPS):
+        step(i)
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / STEPS
+    ms = e0.elapsed_time(e1) / STEPS
+    # decode lengths of the timed steps: ctx0 + s + 1 at every layer of step s
+    tok_per_layer = 2 * Hkv * D * 2
+    logical_ctx = sum(int((ctx0 + i + 1).sum()) for i in range(STEPS)) / STEPS
+    shared = P * (2048 // BS) * BS  # full prefix blocks, shared by 8 forks each
+    unique_ctx = shared + sum(int((ctx0 + i + 1).sum()) - P * F * 2048 for i in range(STEPS)) / STEPS
+    logical_bytes = logical_ctx * tok_per_layer * L
+    unique_bytes = unique_ctx * tok_per_layer * L
+    append_bytes = 2 * n * tok_per_layer * L + n * 8 * L
+    # per-kernel times from a few more steps with the library's hipEvents
+    lib.zk_timing_reset()
+    lib.zk_timing_enable(1)
+    for i in range(EV_STEPS):
+        step(i)
+    torch.cuda.synchronize()
+    lib.zk_timing_enable(0)
+    kt = {k: kernel_ms(lib, k) for k in ("decode_partials", "decode_reduce", "decode_seq_info",
+                                         "decode_plan", "append")}
+    lib.zk_timing_reset()
+    dec_kernel_ms = sum(kt[k][0] * kt[k][1] for k in ("decode_partials", "decode_reduce", "decode_seq_info",
+                                                      "decode_plan") if kt[k][1]) / EV_STEPS
+    # released handles are stale: a freed block's old handle is rejected
+    h = bm.allocate()
+    bm.free(h)
+    try:
+        bm.reference(h)
+        stale_rejected = False
+    except RuntimeError as e:
+        stale_rejected = "Stale handle" in str(e)
+    for cid in children:
+        cache.release_seq(cid)
+    for p in range(P):
+        cache.release_seq(f"p{p}")
+    assert bm.free_blocks == NB
+    res = {
+        "cow": {"forks": n, "pools": 2 * L, "bytes": cow_bytes, "kernel_ms": cow_ms,
+                "gbps": cow_bytes / (cow_ms * 1e-3) / 1e9, "first_append_call_ms": float(np.median(cow_call_ms)),
+                "reps": COW_REPS},
+        "decode_step": {"steps": STEPS, "ms_per_step": ms, "wall_ms_per_step": wall_ms,
+                        "layers": L, "seqs": n,
+                        "logical_ctx_per_layer": logical_ctx, "unique_ctx_per_layer": unique_ctx,
+                        "logical_bytes_per_step": logical_bytes, "unique_bytes_per_step": unique_bytes,
+                        "append_bytes_per_step": append_bytes,
+                        "logical_gbps": logical_bytes / (ms * 1e-3) / 1e9,
+                        "unique_gbps": (unique_bytes + append_bytes) / (ms * 1e-3) / 1e9,
+                        "tokens_per_s": n / (ms * 1e-3),
+                        "decode_kernels_ms_per_step": dec_kernel_ms,
+                        "decode_kernel_logical_gbps": logical_bytes / (dec_kernel_ms * 1e-3) / 1e9,
+                        "decode_kernel_unique_gbps": unique_bytes / (dec_kernel_ms * 1e-3) / 1e9,
+                        "kernel_ms": {k: v[0] for k, v in kt.items() if v[1]}},
+        "stale_handle_rejected": stale_rejected,
+    }
+    del cache, kin, vin, qin, out
+    torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 def cpu_model() -> str:
@@ -306,7 +454,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "append", "fp8"], default=None,
+    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4"], default=None,
                     help="run one workload (for profiler passes)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
@@ -325,7 +473,7 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     result = {}
-    dec = lens = app = fp8 = None
+    dec = lens = app = fp8 = c4 = None
     if args.only in (None, "decode"):
         dec, lens = bench_decode(args, torch, ops, lib, "bf16")
         log(f"decode bf16: {dec['ms_per_step']:.4f} ms {dec['gbps']:.1f} GB/s")
@@ -335,11 +483,18 @@ def main() -> int:
     if args.only in (None, "fp8"):
         fp8, _ = bench_decode(args, torch, ops, lib, "fp8")
         log(f"decode fp8: {fp8['ms_per_step']:.4f} ms {fp8['gbps']:.1f} GB/s")
+    if args.only in (None, "c4"):
+        c4 = bench_c4(args, torch, lib)
+        log(f"c4: cow {c4['cow']['gbps']:.1f} GB/s; step {c4['decode_step']['ms_per_step']:.3f} ms, "
+            f"logical {c4['decode_step']['logical_gbps']:.1f} GB/s, unique {c4['decode_step']['unique_gbps']:.1f} GB/s")
     cpu = None
     if args.only is None and not args.no_cpu_baseline:
         cpu = cpu_baseline(lens, args.cpu_sample_seqs)
         log(f"cpu baseline: {cpu['value']:.3f} GB/s (1 core), {cpu['omp_value']:.2f} GB/s ({cpu['omp_cores']} cores)")
-    head = dec if dec is not None else (app if app is not None else fp8)
+    head = next((x for x in (dec, app, fp8) if x is not None), None)
+    if head is None:  # --only c4
+        head = {"gbps": c4["decode_step"]["logical_gbps"], "ms_per_step": c4["decode_step"]["ms_per_step"],
+                "roofline": None}
     result = {
         "metric": METRIC,
         "value": round(head["gbps"], 2),
@@ -362,6 +517,7 @@ def main() -> int:
         "decode_bf16": dec,
         "append_bf16": app,
         "decode_fp8": fp8,
+        "prefix_cow_c4": c4,
         "gpu": torch.cuda.get_device_name(0),
     }
     if args.only is not None:

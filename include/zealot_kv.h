@@ -191,6 +191,13 @@ int zk_cache_store_kv(zk_kv_cache *c, size_t layer, const char *id, const void *
  * writing the last layer advances cached_tokens / block_offset. */
 int zk_cache_append_kv(zk_kv_cache *c, size_t layer, const char *id, const void *k,
                        const void *v, zk_dtype src_dtype);
+/* Batched decode append for one layer: token i of k/v ([n, Hkv, D]) goes to
+ * sequence ids[i] at its cached_tokens position (copy-on-write first where the
+ * target block is shared); one launch for the whole batch.  Writing the last
+ * layer advances each sequence by one token.  Batched form of append_kv
+ * (kv_cache.rs:281-356) for a runner that steps all sequences together. */
+int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *ids, int n,
+                             const void *k, const void *v, zk_dtype src_dtype);
 /* fp8 pools: set the per-(layer, kv_head) dequant scales of a sequence
  * (k_scales/v_scales: host arrays of num_layers * Hkv floats). */
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales,

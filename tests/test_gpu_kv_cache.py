@@ -137,3 +137,128 @@ def test_prefix_fork_copy_on_write():
     assert bm.free_blocks == NB
     with pytest.raises(RuntimeError, match="Stale handle"):
         bm.reference(h_old)
+
+
+def _expected_bytes(tokens_k, tokens_v, src, H, D, BS, ks=None, vs=None):
+    """Pool-format bytes [T, H, D] of a token sequence, written by the oracle
+    into a contiguous scratch pool (fp8: quantised with scale row 0)."""
+    T = tokens_k.shape[0]
+    nb = (T + BS - 1) // BS
+    fp8 = ks is not None
+    dt = oracle.FP8 if fp8 else oracle.BF16
+    pool_dtype = np.uint8 if fp8 else np.uint16
+    kp = np.zeros((nb, H, BS, D), pool_dtype)
+    vp = np.zeros((nb, H, BS, D), pool_dtype)
+    rows = np.zeros(T, np.int32) if fp8 else None
+    oracle.append_slots(kp, vp, dt, tokens_k, tokens_v, src, np.arange(T), H, D, BS, nb,
+                        ks, vs, rows)
+    bt = np.arange(nb, dtype=np.int32)
+    return (oracle.gather(kp, dt, bt, T, H, D, BS, pool_dtype),
+            oracle.gather(vp, dt, bt, T, H, D, BS, pool_dtype))
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_append_kv_batch_forks_layerwise_decode(kv):
+    """Batched decode append over forked sequences: the first append copies each
+    fork's shared tail (one batched copy), every layer's decode sees the token
+    appended at that layer, and the pool bytes equal the oracle's."""
+    import zealot_amd as ze
+    from zealot_amd import KVCache
+    rng = np.random.default_rng(42 if kv == "bf16" else 43)
+    L, H, Hkv, D, BS, NB = 2, 8, 2, 128, 16, 64
+    fp8 = kv == "fp8"
+    cdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    kvdt = oracle.FP8 if fp8 else oracle.BF16
+    prefixes = {"pa": 16 * 3 + 5, "pb": 16 * 2 + 9}
+    bm = ze.BlockManager(NB, BS)
+    cache = KVCache(NB, BS, L, Hkv, D, dtype=cdt, max_seqs=16, max_blocks_per_seq=8)
+    toks = {}  # seq -> layer -> (k list, v list) of bf16 bit arrays [1, Hkv, D]
+    scales = {}
+    for pid, p in prefixes.items():
+        cache.register_seq(pid, 8)
+        for _ in range((p + BS - 1) // BS):
+            cache.alloc_block(pid, bm)
+        kl = [normal(rng, (p, Hkv, D), oracle.BF16) for _ in range(L)]
+        vl = [normal(rng, (p, Hkv, D), oracle.BF16) for _ in range(L)]
+        if fp8:
+            ks = np.stack([np.abs(as_f32(x, oracle.BF16)).max(axis=(0, 2)) / 448 for x in kl]).astype(np.float32)
+            vs = np.stack([np.abs(as_f32(x, oracle.BF16)).max(axis=(0, 2)) / 448 for x in vl]).astype(np.float32)
+            cache.set_fp8_scales(pid, ks.ravel(), vs.ravel())
+            scales[pid] = (ks, vs)
+        for layer in range(L):
+            cache.store_kv(layer, pid, to_dev(kl[layer]), to_dev(vl[layer]), 0, p)
+        toks[pid] = {l: ([kl[l]], [vl[l]]) for l in range(L)}
+    children = []
+    for pid in prefixes:
+        for j in range(3):
+            cid = f"{pid}.{j}"
+            cache.fork_seq(pid, cid)
+            children.append(cid)
+            toks[cid] = {l: (list(toks[pid][l][0]), list(toks[pid][l][1])) for l in range(L)}
+            scales[cid] = scales.get(pid)
+    parent_of = {c: c.split(".")[0] for c in children}
+    announce(f"kvcache append_kv_batch forks kv={kv}")
+    n = len(children)
+    scale = np.float32(1 / math.sqrt(D))
+    for step in range(12):
+        for cid in children:
+            st = cache.seq_state(cid)
+            if st.cached_tokens == len(st.block_ids) * BS:
+                cache.alloc_block(cid, bm)
+        for layer in range(L):
+            k = normal(rng, (n, Hkv, D), oracle.BF16)
+            v = normal(rng, (n, Hkv, D), oracle.BF16)
+            cache.append_kv_batch(layer, children, to_dev(k), to_dev(v))
+            for i, cid in enumerate(children):
+                toks[cid][layer][0].append(k[i:i + 1])
+                toks[cid][layer][1].append(v[i:i + 1])
+            q = normal(rng, (n, H, D), oracle.BF16)
+            out = to_host(cache.paged_decode(layer, children, to_dev(q)))
+            kp, vp = to_host(cache.k_pool(layer)), to_host(cache.v_pool(layer))
+            lens = [prefixes[parent_of[c]] + step + 1 for c in children]
+            bt = -np.ones((n, 8), np.int32)
+            for i, cid in enumerate(children):
+                b = cache.seq_state(cid).block_ids
+                bt[i, :len(b)] = b
+            kw = {}
+            if fp8:
+                kw = dict(k_scales=np.stack([scales[c][0][layer] for c in children]),
+                          v_scales=np.stack([scales[c][1][layer] for c in children]))
+            ref = oracle.paged_decode(as_f32(q, oracle.BF16), kp, vp, kvdt, bt, lens, Hkv, D, BS,
+                                      scale, **kw)
+            assert max_abs_err(as_f32(out, oracle.BF16), ref) <= 2e-2, (step, layer)
+        for cid in children:
+            assert cache.seq_state(cid).cached_tokens == prefixes[parent_of[cid]] + step + 1
+    torch.cuda.synchronize()
+    # every fork copied its tail once; parents keep their blocks and bytes
+    for pid, p in prefixes.items():
+        pb = cache.seq_state(pid).block_ids
+        full = p // BS
+        for b in pb[:full]:
+            assert bm.refcount(b) == 4
+        assert bm.refcount(pb[full]) == 1
+        for j in range(3):
+            cb = cache.seq_state(f"{pid}.{j}").block_ids
+            assert cb[:full] == pb[:full] and cb[full] != pb[full]
+    for sid in list(prefixes) + children:
+        T = cache.seq_state(sid).cached_tokens
+        for layer in range(L):
+            kk = np.concatenate(toks[sid][layer][0])
+            vv = np.concatenate(toks[sid][layer][1])
+            sc = (scales[sid][0][layer][None], scales[sid][1][layer][None]) if fp8 else (None, None)
+            ek, ev = _expected_bytes(kk, vv, oracle.BF16, Hkv, D, BS, *sc)
+            pdt = np.uint8 if fp8 else np.uint16
+            kp, vp = to_host(cache.k_pool(layer)), to_host(cache.v_pool(layer))
+            bt = np.asarray(cache.seq_state(sid).block_ids, np.int32)
+            gk = oracle.gather(kp, kvdt, bt, T, Hkv, D, BS, pdt)
+            gv = oracle.gather(vp, kvdt, bt, T, Hkv, D, BS, pdt)
+            assert np.array_equal(gk, ek) and np.array_equal(gv, ev), (sid, layer)
+    # batch errors: duplicate ids, unknown ids, and missing blocks fail before any write
+    one = to_dev(normal(rng, (2, Hkv, D), oracle.BF16))
+    with pytest.raises(RuntimeError, match="twice"):
+        cache.append_kv_batch(0, [children[0], children[0]], one, one)
+    with pytest.raises(RuntimeError, match="unknown seq nope"):
+        cache.append_kv_batch(0, [children[0], "nope"], one, one)
+    for sid in children + list(prefixes):
+        cache.release_seq(sid)
+    assert bm.free_blocks == NB

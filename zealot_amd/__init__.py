@@ -13,14 +13,15 @@ zealot_amd/csrc with `python -m zealot_amd.build`):
 from ._lib import ZealotError, lib  # noqa: F401
 from .block_manager import BlockHandle, BlockManager  # noqa: F401
 
-__all__ = ["BlockHandle", "BlockManager", "ZealotError", "lib", "ops", "KVCache", "HipAttention"]
+__all__ = ["BlockHandle", "BlockManager", "ZealotError", "lib", "ops", "KVCache", "SeqBatch",
+           "HipAttention"]
 
 
 def __getattr__(name):
     # torch-dependent modules load lazily so BlockManager works without torch
     import importlib
-    if name == "KVCache":
-        return importlib.import_module(".kv_cache", __name__).KVCache
+    if name in ("KVCache", "SeqBatch"):
+        return getattr(importlib.import_module(".kv_cache", __name__), name)
     if name == "HipAttention":
         return importlib.import_module(".attention", __name__).HipAttention
     if name == "ops":

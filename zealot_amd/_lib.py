@@ -70,6 +70,7 @@ SIGNATURES = {
     "zk_cache_fork_seq": (_I, [_P, _CP, _CP]),
     "zk_cache_store_kv": (_I, [_P, _SZ, _CP, _P, _P, _I, _SZ, _SZ]),
     "zk_cache_append_kv": (_I, [_P, _SZ, _CP, _P, _P, _I]),
+    "zk_cache_append_kv_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _P, _I]),
     "zk_cache_set_fp8_scales": (_I, [_P, _CP, _P, _P]),
     "zk_cache_block_table_ptr": (_I, [_P, _CP, ctypes.POINTER(_P)]),
     "zk_cache_k_pool_ptr": (_P, [_P, _SZ]),

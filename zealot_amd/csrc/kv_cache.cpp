@@ -17,7 +17,10 @@
 //    written (the reference advances on every append_kv call, i.e. once per
 //    layer, and never on store_kv).
 //  - release_seq returns the sequence's blocks to its BlockManager.
-//  - fork_seq / copy-on-write has no reference counterpart.
+//  - fork_seq / copy-on-write and append_kv_batch have no reference
+//    counterpart.
+//  - Decode at layer l sees every token written at layer l, so a decode step
+//    may interleave append_kv(l) and paged_decode(l) layer by layer.
 // Not thread-safe: one thread drives a cache (as GpuContext, gpu_context.rs:23-26).
 #include <hip/hip_runtime.h>
 
@@ -37,10 +40,11 @@ namespace {
 struct SeqState {
     std::vector<zk_block_handle> handles;
     zk_block_manager *bm = nullptr;
-    size_t cached_tokens = 0;
+    size_t cached_tokens = 0;     // tokens written at the last layer
     size_t block_offset = 0;
     size_t max_blocks = 0;
     size_t slot = 0;
+    std::vector<size_t> layer_len;  // tokens written per layer (decode length)
     std::vector<float> k_scales, v_scales;  // [layers * Hkv], fp8 pools
 };
 
@@ -67,7 +71,9 @@ struct DevBuf {
     }
 };
 
-// Pinned staging buffer; reuse waits for the copy that last read it.
+// Pinned staging buffer; reuse waits for the copy that last read it.  The
+// cache cycles through a ring of them so the host only waits when the device
+// is a whole ring of uploads behind.
 struct Staging {
     void *p = nullptr;
     size_t cap = 0;
@@ -95,6 +101,14 @@ struct Staging {
     }
 };
 
+// Device buffer whose last uploaded bytes are remembered: an upload of the
+// same bytes is skipped (a decode step writes the same slot mapping and
+// lengths for every layer).
+struct CachedBuf {
+    DevBuf dev;
+    std::vector<char> last;
+};
+
 struct DeviceGuard {
     int prev = -1;
     explicit DeviceGuard(int dev) {
@@ -119,10 +133,22 @@ struct zk_kv_cache {
     int32_t *tables = nullptr;
     std::vector<size_t> free_slots;
     std::unordered_map<std::string, SeqState> seqs;
-    DevBuf d_meta;  // slot mappings, token rows, scales, copy pairs
-    DevBuf d_batch; // decode batch tables + lengths + scales
-    DevBuf d_ws;    // decode workspace
-    Staging stage;
+    CachedBuf d_meta;  // slot mappings, token rows, scales
+    DevBuf d_cow;      // copy-on-write (src, dst) block ids
+    DevBuf d_tblupd;   // block-table updates (offset, value)
+    CachedBuf d_tbl;   // decode batch block tables [n][stride]
+    CachedBuf d_batch; // decode batch lengths + scales
+    DevBuf d_ws;     // decode workspace
+    static constexpr int kStages = 16;
+    Staging stage[kStages];
+    int next_stage = 0;
+    std::vector<int2> tbl_updates;  // pending writes into `tables`
+    // Decode-table cache: the batch table is re-uploaded only when a block
+    // table changed (epoch) or the batch is a different list of sequences.
+    uint64_t epoch = 0;
+    uint64_t dec_epoch = ~0ull;
+    size_t dec_stride = 0;
+    std::vector<const SeqState *> dec_ids;
 
     size_t block_bytes() const { return block_size * num_kv_heads * head_dim * zk::elt_size(dtype); }
     char *k_pool(size_t layer) const { return slab + (2 * layer) * pool_bytes; }
@@ -150,46 +176,96 @@ int find_seq(zk_kv_cache *c, const char *id, SeqState **out) {
 // Upload `bytes` from host memory to device memory on the cache stream.
 int upload(zk_kv_cache *c, void *dst, const void *src, size_t bytes) {
     if (bytes == 0) return ZK_OK;
-    if (int rc = c->stage.ensure(bytes)) return rc;
-    std::memcpy(c->stage.p, src, bytes);
-    ZK_HIP_CHECK(hipMemcpyAsync(dst, c->stage.p, bytes, hipMemcpyHostToDevice, c->stream), "KVCache upload");
-    ZK_HIP_CHECK(hipEventRecord(c->stage.done, c->stream), "KVCache upload event");
-    c->stage.pending = true;
+    Staging &st = c->stage[c->next_stage];
+    c->next_stage = (c->next_stage + 1) % zk_kv_cache::kStages;
+    if (int rc = st.ensure(bytes)) return rc;
+    std::memcpy(st.p, src, bytes);
+    ZK_HIP_CHECK(hipMemcpyAsync(dst, st.p, bytes, hipMemcpyHostToDevice, c->stream), "KVCache upload");
+    ZK_HIP_CHECK(hipEventRecord(st.done, c->stream), "KVCache upload event");
+    st.pending = true;
     return ZK_OK;
 }
 
-int write_table_entry(zk_kv_cache *c, const SeqState &s, size_t idx, int32_t value) {
-    return upload(c, c->table_row(s.slot) + idx, &value, sizeof(value));
+// Upload into a CachedBuf unless it already holds exactly these bytes.
+int put(zk_kv_cache *c, CachedBuf &b, const void *host, size_t bytes, const char *what) {
+    if (bytes && b.last.size() == bytes && std::memcmp(b.last.data(), host, bytes) == 0) return ZK_OK;
+    b.last.clear();
+    if (int rc = b.dev.ensure(bytes, what)) return rc;
+    if (int rc = upload(c, b.dev.p, host, bytes)) return rc;
+    b.last.assign((const char *)host, (const char *)host + bytes);
+    return ZK_OK;
 }
 
-// Copy-on-write of s.handles[idx]: fresh block, copy every pool, drop the
-// shared reference, point the table at the copy.
-int cow_block(zk_kv_cache *c, SeqState &s, size_t idx) {
-    zk_block_handle fresh;
-    if (int rc = zk_bm_allocate(s.bm, &fresh)) return rc;
-    int32_t pair[2] = {(int32_t)s.handles[idx].block_id, (int32_t)fresh.block_id};
-    if (int rc = c->d_meta.ensure(sizeof(pair), "KVCache cow scratch")) {
-        (void)zk_bm_free(s.bm, fresh);
-        return rc;
+void queue_table_entry(zk_kv_cache *c, const SeqState &s, size_t idx, int32_t value) {
+    c->tbl_updates.push_back(make_int2((int)(s.slot * c->max_blocks_per_seq + idx), value));
+    ++c->epoch;
+}
+
+// Apply the queued block-table writes in one launch.
+int flush_tables(zk_kv_cache *c) {
+    if (c->tbl_updates.empty()) return ZK_OK;
+    const size_t n = c->tbl_updates.size();
+    int rc = c->d_tblupd.ensure(n * sizeof(int2), "KVCache table update");
+    if (!rc) rc = upload(c, c->d_tblupd.p, c->tbl_updates.data(), n * sizeof(int2));
+    if (!rc)
+        rc = zk::scatter_i32(c->tables, (int64_t)(c->max_seqs * c->max_blocks_per_seq), (const int2 *)c->d_tblupd.p,
+                             (int)n, c->stream);
+    c->tbl_updates.clear();
+    return rc;
+}
+
+// Copy-on-write of every (seq, block index) in `targets`: fresh blocks, one
+// copy launch over every pool (all layers, K and V), drop the shared
+// references, point the tables at the copies.  On an allocation failure
+// nothing has been copied and the fresh blocks are returned.
+int cow_blocks(zk_kv_cache *c, const std::vector<std::pair<SeqState *, size_t>> &targets) {
+    if (targets.empty()) return ZK_OK;
+    const size_t n = targets.size();
+    std::vector<zk_block_handle> fresh(n);
+    std::vector<int32_t> pairs(2 * n);
+    for (size_t i = 0; i < n; ++i) {
+        SeqState &s = *targets[i].first;
+        if (int rc = zk_bm_allocate(s.bm, &fresh[i])) {
+            std::string msg = zk_last_error();
+            for (size_t j = 0; j < i; ++j) (void)zk_bm_free(targets[j].first->bm, fresh[j]);
+            return set_error(rc, msg);
+        }
+        pairs[i] = (int32_t)s.handles[targets[i].second].block_id;
+        pairs[n + i] = (int32_t)fresh[i].block_id;
     }
-    if (int rc = upload(c, c->d_meta.p, pair, sizeof(pair))) {
-        (void)zk_bm_free(s.bm, fresh);
-        return rc;
+    int rc = c->d_cow.ensure(pairs.size() * sizeof(int32_t), "KVCache cow scratch");
+    if (!rc) rc = upload(c, c->d_cow.p, pairs.data(), pairs.size() * sizeof(int32_t));
+    if (!rc) {
+        std::vector<void *> pools(2 * c->num_layers);
+        for (size_t l = 0; l < c->num_layers; ++l) {
+            pools[2 * l] = c->k_pool(l);
+            pools[2 * l + 1] = c->v_pool(l);
+        }
+        const int32_t *d = (const int32_t *)c->d_cow.p;
+        rc = zk_copy_blocks(pools.data(), (int)pools.size(), (int64_t)c->block_bytes(), (int64_t)c->num_blocks,
+                            d, d + n, (int64_t)n, c->stream);
     }
-    std::vector<void *> pools(2 * c->num_layers);
-    for (size_t l = 0; l < c->num_layers; ++l) {
-        pools[2 * l] = c->k_pool(l);
-        pools[2 * l + 1] = c->v_pool(l);
+    if (rc) {
+        std::string msg = zk_last_error();
+        for (size_t j = 0; j < n; ++j) (void)zk_bm_free(targets[j].first->bm, fresh[j]);
+        return set_error(rc, msg);
     }
-    const int32_t *d = (const int32_t *)c->d_meta.p;
-    if (int rc = zk_copy_blocks(pools.data(), (int)pools.size(), (int64_t)c->block_bytes(),
-                                (int64_t)c->num_blocks, d, d + 1, 1, c->stream)) {
-        (void)zk_bm_free(s.bm, fresh);
-        return rc;
+    int first_rc = ZK_OK;
+    std::string first_msg;
+    for (size_t i = 0; i < n; ++i) {
+        SeqState &s = *targets[i].first;
+        size_t idx = targets[i].second;
+        int frc = zk_bm_free(s.bm, s.handles[idx]);
+        if (frc && !first_rc) {
+            first_rc = frc;
+            first_msg = zk_last_error();
+        }
+        s.handles[idx] = fresh[i];
+        queue_table_entry(c, s, idx, (int32_t)fresh[i].block_id);
     }
-    if (int rc = zk_bm_free(s.bm, s.handles[idx])) return rc;
-    s.handles[idx] = fresh;
-    return write_table_entry(c, s, idx, (int32_t)fresh.block_id);
+    rc = flush_tables(c);
+    if (first_rc) return set_error(first_rc, first_msg);
+    return rc;
 }
 
 int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, const void *k, const void *v,
@@ -211,9 +287,10 @@ int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, cons
         return set_error(ZK_ERR_FAILED_PRECONDITION,
                          std::string("Failed precondition: fp8 scales not set for seq ") + id);
     // Copy-on-write every shared block this write touches.
+    std::vector<std::pair<SeqState *, size_t>> shared;
     for (size_t idx = start / bs; idx <= last_idx; ++idx)
-        if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1)
-            if (int rc = cow_block(c, s, idx)) return rc;
+        if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1) shared.emplace_back(&s, idx);
+    if (int rc = cow_blocks(c, shared)) return rc;
 
     const size_t H = c->num_kv_heads;
     const bool fp8 = c->dtype == ZK_FP8_E4M3;
@@ -233,9 +310,8 @@ int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, cons
         std::memcpy(sc, s.k_scales.data() + layer * H, H * sizeof(float));
         std::memcpy(sc + H, s.v_scales.data() + layer * H, H * sizeof(float));
     }
-    if (int rc = c->d_meta.ensure(total, "KVCache slot mapping")) return rc;
-    if (int rc = upload(c, c->d_meta.p, host.data(), total)) return rc;
-    char *d = (char *)c->d_meta.p;
+    if (int rc = put(c, c->d_meta, host.data(), total, "KVCache slot mapping")) return rc;
+    char *d = (char *)c->d_meta.dev.p;
     const int32_t *d_rows = fp8 ? (const int32_t *)(d + slots_bytes) : nullptr;
     const float *d_ks = fp8 ? (const float *)(d + slots_bytes + rows_bytes) : nullptr;
     const float *d_vs = fp8 ? d_ks + H : nullptr;
@@ -243,6 +319,7 @@ int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, cons
                            (const int64_t *)d, (int64_t)n, (int)H, (int)c->head_dim, (int)bs,
                            (int64_t)c->num_blocks, d_ks, d_vs, d_rows, c->stream))
         return rc;
+    s.layer_len[layer] = std::max(s.layer_len[layer], start + n);
     if (layer + 1 == c->num_layers) {
         s.cached_tokens = std::max(s.cached_tokens, start + n);
         s.block_offset = s.cached_tokens % bs;
@@ -307,6 +384,7 @@ int zk_cache_register_seq(zk_kv_cache *c, const char *id, size_t max_blocks) {
     DeviceGuard g(c->device);
     SeqState s;
     s.max_blocks = max_blocks;
+    s.layer_len.assign(c->num_layers, 0);
     s.slot = c->free_slots.back();
     std::vector<int32_t> row(c->max_blocks_per_seq, -1);
     if (int rc = upload(c, c->table_row(s.slot), row.data(), row.size() * sizeof(int32_t))) return rc;
@@ -330,7 +408,8 @@ int zk_cache_alloc_block(zk_kv_cache *c, const char *id, zk_block_manager *bm, s
     DeviceGuard g(c->device);
     zk_block_handle h;
     if (int rc = zk_bm_allocate(bm, &h)) return rc;
-    if (int rc = write_table_entry(c, *s, s->handles.size(), (int32_t)h.block_id)) {
+    queue_table_entry(c, *s, s->handles.size(), (int32_t)h.block_id);
+    if (int rc = flush_tables(c)) {
         (void)zk_bm_free(bm, h);
         return rc;
     }
@@ -357,6 +436,7 @@ int zk_cache_release_seq(zk_kv_cache *c, const char *id) {
     int rc = upload(c, c->table_row(s->slot), row.data(), row.size() * sizeof(int32_t));
     c->free_slots.push_back(s->slot);
     c->seqs.erase(id);
+    ++c->epoch;
     if (first_rc) return set_error(first_rc, first_msg);
     return rc;
 }
@@ -384,6 +464,7 @@ int zk_cache_fork_seq(zk_kv_cache *c, const char *parent, const char *child) {
                  "KVCache fork table copy");
     c->free_slots.pop_back();
     c->seqs.emplace(child, std::move(s));
+    ++c->epoch;
     return ZK_OK;
 }
 
@@ -401,6 +482,80 @@ int zk_cache_append_kv(zk_kv_cache *c, size_t layer, const char *id, const void 
     if (int rc = find_seq(c, id, &s)) return rc;
     DeviceGuard g(c->device);
     return write_tokens(c, layer, *s, id, k, v, src_dtype, s->cached_tokens, 1, "append_kv");
+}
+
+int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *k,
+                             const void *v, zk_dtype src_dtype) {
+    if (!c || (n > 0 && !ids)) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache append batch: NULL argument");
+    if (layer >= c->num_layers)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache append batch: layer out of range");
+    if (src_dtype != ZK_F32 && src_dtype != ZK_BF16)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache append batch: bad src dtype");
+    if (n <= 0) return ZK_OK;
+    if (!k || !v) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache append batch: NULL k/v");
+    DeviceGuard g(c->device);
+    const size_t bs = c->block_size, H = c->num_kv_heads;
+    const bool fp8 = c->dtype == ZK_FP8_E4M3;
+    std::vector<SeqState *> seqs((size_t)n);
+    for (int i = 0; i < n; ++i) {
+        if (int rc = find_seq(c, ids[i], &seqs[i])) return rc;
+        for (int j = 0; j < i; ++j)
+            if (seqs[j] == seqs[i])
+                return set_error(ZK_ERR_INVALID_ARGUMENT,
+                                 std::string("Internal error: KVCache append batch: seq ") + ids[i] + " twice");
+        const SeqState &s = *seqs[i];
+        const size_t idx = s.cached_tokens / bs;
+        if (idx >= s.handles.size())  // kv_cache.rs:307-312
+            return set_error(ZK_ERR_INTERNAL, "Internal error: KVCache append_kv: block_idx " + std::to_string(idx) +
+                                                  " OOB (have " + std::to_string(s.handles.size()) + " blocks)");
+        if (fp8 && s.k_scales.empty())
+            return set_error(ZK_ERR_FAILED_PRECONDITION,
+                             std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
+    }
+    std::vector<std::pair<SeqState *, size_t>> shared;  // copy-on-write of shared targets
+    for (int i = 0; i < n; ++i) {
+        SeqState &s = *seqs[i];
+        const size_t idx = s.cached_tokens / bs;
+        if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1) shared.emplace_back(&s, idx);
+    }
+    if (int rc = cow_blocks(c, shared)) return rc;
+    const size_t slots_bytes = (size_t)n * sizeof(int64_t);
+    const size_t rows_bytes = fp8 ? (size_t)n * sizeof(int32_t) : 0;
+    const size_t scale_bytes = fp8 ? 2 * (size_t)n * H * sizeof(float) : 0;
+    std::vector<char> host(slots_bytes + rows_bytes + scale_bytes);
+    int64_t *slots = (int64_t *)host.data();
+    for (int i = 0; i < n; ++i) {
+        const SeqState &s = *seqs[i];
+        slots[i] = (int64_t)s.handles[s.cached_tokens / bs].block_id * (int64_t)bs + (int64_t)(s.cached_tokens % bs);
+    }
+    if (fp8) {
+        int32_t *rows = (int32_t *)(host.data() + slots_bytes);
+        float *sc = (float *)(host.data() + slots_bytes + rows_bytes);
+        for (int i = 0; i < n; ++i) {
+            rows[i] = i;
+            std::memcpy(sc + (size_t)i * H, seqs[i]->k_scales.data() + layer * H, H * sizeof(float));
+            std::memcpy(sc + (size_t)n * H + (size_t)i * H, seqs[i]->v_scales.data() + layer * H, H * sizeof(float));
+        }
+    }
+    if (int rc = put(c, c->d_meta, host.data(), host.size(), "KVCache slot mapping")) return rc;
+    char *d = (char *)c->d_meta.dev.p;
+    const int32_t *d_rows = fp8 ? (const int32_t *)(d + slots_bytes) : nullptr;
+    const float *d_ks = fp8 ? (const float *)(d + slots_bytes + rows_bytes) : nullptr;
+    const float *d_vs = fp8 ? d_ks + (size_t)n * H : nullptr;
+    if (int rc = zk_append(c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, k, v, src_dtype,
+                           (const int64_t *)d, (int64_t)n, (int)H, (int)c->head_dim, (int)bs,
+                           (int64_t)c->num_blocks, d_ks, d_vs, d_rows, c->stream))
+        return rc;
+    for (int i = 0; i < n; ++i) {
+        SeqState &s = *seqs[i];
+        s.layer_len[layer] = std::max(s.layer_len[layer], s.cached_tokens + 1);
+    }
+    if (layer + 1 == c->num_layers)
+        for (int i = 0; i < n; ++i) {
+            seqs[i]->cached_tokens += 1;
+            seqs[i]->block_offset = seqs[i]->cached_tokens % bs;
+        }
+    return ZK_OK;
 }
 
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales, const float *v_scales) {
@@ -468,41 +623,54 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode: layer out of range");
     if (n <= 0) return ZK_OK;
     DeviceGuard g(c->device);
-    const size_t MB = c->max_blocks_per_seq, H = c->num_kv_heads;
+    const size_t H = c->num_kv_heads;
     const bool fp8 = c->dtype == ZK_FP8_E4M3;
-    size_t tbl_bytes = (size_t)n * MB * sizeof(int32_t);
-    size_t len_bytes = (size_t)n * sizeof(int32_t);
-    size_t sc_bytes = fp8 ? 2 * (size_t)n * H * sizeof(float) : 0;
-    size_t off_len = (tbl_bytes + 255) & ~(size_t)255;
-    size_t off_sc = off_len + ((len_bytes + 255) & ~(size_t)255);
-    size_t total = off_sc + sc_bytes;
-    std::vector<char> host(total, 0);
-    int32_t *tbl = (int32_t *)host.data();
-    int32_t *lens = (int32_t *)(host.data() + off_len);
-    float *sc = (float *)(host.data() + off_sc);
+    std::vector<const SeqState *> seqs((size_t)n);
+    size_t stride = 1;
     for (int i = 0; i < n; ++i) {
         SeqState *s;
         if (int rc = find_seq(c, ids[i], &s)) return rc;
-        for (size_t j = 0; j < MB; ++j) tbl[(size_t)i * MB + j] = j < s->handles.size() ? (int32_t)s->handles[j].block_id : -1;
-        lens[i] = (int32_t)s->cached_tokens;
+        if (fp8 && s->k_scales.empty())
+            return set_error(ZK_ERR_FAILED_PRECONDITION,
+                             std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
+        seqs[i] = s;
+        stride = std::max(stride, s->handles.size());
+    }
+    // Block tables [n][stride]: re-uploaded only when some table changed or
+    // the batch differs from the previous call's.
+    if (c->dec_epoch != c->epoch || c->dec_ids != seqs || c->dec_stride != stride) {
+        std::vector<int32_t> tbl((size_t)n * stride, -1);
+        for (int i = 0; i < n; ++i)
+            for (size_t j = 0; j < seqs[i]->handles.size(); ++j)
+                tbl[(size_t)i * stride + j] = (int32_t)seqs[i]->handles[j].block_id;
+        c->dec_epoch = ~0ull;
+        if (int rc = put(c, c->d_tbl, tbl.data(), tbl.size() * sizeof(int32_t), "KVCache decode tables")) return rc;
+        c->dec_epoch = c->epoch;
+        c->dec_ids = seqs;
+        c->dec_stride = stride;
+    }
+    // Lengths at this layer, then (fp8) this layer's scales [2][n][H].
+    const size_t len_bytes = (((size_t)n * sizeof(int32_t)) + 255) & ~(size_t)255;
+    const size_t total = len_bytes + (fp8 ? 2 * (size_t)n * H * sizeof(float) : 0);
+    std::vector<char> host(total, 0);
+    int32_t *lens = (int32_t *)host.data();
+    float *sc = (float *)(host.data() + len_bytes);
+    for (int i = 0; i < n; ++i) {
+        lens[i] = (int32_t)seqs[i]->layer_len[layer];
         if (fp8) {
-            if (s->k_scales.empty())
-                return set_error(ZK_ERR_FAILED_PRECONDITION,
-                                 std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
-            std::memcpy(sc + (size_t)i * H, s->k_scales.data() + layer * H, H * sizeof(float));
-            std::memcpy(sc + (size_t)n * H + (size_t)i * H, s->v_scales.data() + layer * H, H * sizeof(float));
+            std::memcpy(sc + (size_t)i * H, seqs[i]->k_scales.data() + layer * H, H * sizeof(float));
+            std::memcpy(sc + (size_t)n * H + (size_t)i * H, seqs[i]->v_scales.data() + layer * H, H * sizeof(float));
         }
     }
-    if (int rc = c->d_batch.ensure(total, "KVCache decode batch")) return rc;
-    if (int rc = upload(c, c->d_batch.p, host.data(), total)) return rc;
-    size_t ws = zk_paged_decode_workspace_size(n, num_heads, (int)c->head_dim, (int)MB, (int)c->block_size);
+    if (int rc = put(c, c->d_batch, host.data(), total, "KVCache decode batch")) return rc;
+    size_t ws = zk_paged_decode_workspace_size(n, num_heads, (int)c->head_dim, (int)stride, (int)c->block_size);
     if (int rc = c->d_ws.ensure(ws, "KVCache decode workspace")) return rc;
-    char *d = (char *)c->d_batch.p;
-    const float *dks = fp8 ? (const float *)(d + off_sc) : nullptr;
+    char *d = (char *)c->d_batch.dev.p;
+    const float *dks = fp8 ? (const float *)(d + len_bytes) : nullptr;
     const float *dvs = fp8 ? dks + (size_t)n * H : nullptr;
     return zk_paged_decode(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
-                           (const int32_t *)d, (const int32_t *)(d + off_len), n, num_heads, (int)H,
-                           (int)c->head_dim, (int)c->block_size, (int)MB, (int64_t)c->num_blocks, scale,
+                           (const int32_t *)c->d_tbl.dev.p, (const int32_t *)d, n, num_heads, (int)H,
+                           (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
                            mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream);
 }
 

@@ -305,6 +305,16 @@ stream_copy_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, uint6
     for (; i < n16; i += kThreads) dst[i] = src[i];
 }
 
+// Block-table update: one entry per thread.
+__global__ void __launch_bounds__(kThreads)
+scatter_i32_kernel(int32_t *__restrict__ base, int64_t limit, const int2 *__restrict__ pairs, int n) {
+    int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) {
+        int2 e = pairs[i];
+        if (e.x >= 0 && e.x < limit) base[e.x] = e.y;
+    }
+}
+
 int check_launch(const char *what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
@@ -313,6 +323,12 @@ int check_launch(const char *what) {
 }
 
 }  // namespace
+
+int zk::scatter_i32(int32_t *base, int64_t limit, const int2 *pairs, int n, hipStream_t stream) {
+    if (n <= 0) return ZK_OK;
+    scatter_i32_kernel<<<(n + kThreads - 1) / kThreads, kThreads, 0, stream>>>(base, limit, pairs, n);
+    return check_launch("KVCache block-table update");
+}
 
 extern "C" {
 

@@ -40,6 +40,11 @@ class KernelTimer {
     bool active_ = false;
 };
 
+// Internal launcher (kv_ops.hip): base[pairs[i].x] = pairs[i].y for i < n,
+// offsets checked on the device against `limit`.  Used by the KV cache to
+// apply a batch of block-table updates in one launch.
+int scatter_i32(int32_t *base, int64_t limit, const int2 *pairs, int n, hipStream_t stream);
+
 inline int elt_size(int dt) { return dt == ZK_F32 ? 4 : dt == ZK_BF16 ? 2 : 1; }
 inline bool valid_dtype(int dt) { return dt == ZK_F32 || dt == ZK_BF16 || dt == ZK_FP8_E4M3; }
 

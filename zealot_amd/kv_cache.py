@@ -41,6 +41,23 @@ def _id(s: str) -> bytes:
     return s.encode("utf-8")
 
 
+class SeqBatch:
+    """A list of sequence ids packed once for the C ABI, for callers that issue
+    the same batched call for every layer (append_kv_batch, paged_decode)."""
+
+    def __init__(self, ids):
+        self.ids = [str(i) for i in ids]
+        self._raw = [_id(i) for i in self.ids]
+        self.arr = (ctypes.c_char_p * len(self._raw))(*self._raw)
+
+    def __len__(self) -> int:
+        return len(self.ids)
+
+
+def _batch(ids) -> SeqBatch:
+    return ids if isinstance(ids, SeqBatch) else SeqBatch(ids)
+
+
 class KVCache:
     """kv_cache.rs:51-102.  One HBM slab holds every layer's K and V pool."""
 
@@ -143,20 +160,30 @@ class KVCache:
         _lib.check(_lib.lib().zk_cache_append_kv(self._h, layer, _id(id), k.data_ptr(), v.data_ptr(),
                                                  dt))
 
+    def append_kv_batch(self, layer: int, ids, k, v) -> None:
+        """One decode token per sequence: k, v are [len(ids), Hkv, D]; ids is a
+        list of ids or a SeqBatch."""
+        b = _batch(ids)
+        n = len(b)
+        dt = self._kv(k, v, n)
+        _lib.check(_lib.lib().zk_cache_append_kv_batch(self._h, layer, b.arr, n, k.data_ptr(),
+                                                       v.data_ptr(), dt))
+
     # -- decode --------------------------------------------------------------
     def paged_decode(self, layer: int, ids, q, out=None, scale=None, mapping="grouped"):
-        """Decode attention for registered sequences `ids` (batch order), q [N, H, D]."""
+        """Decode attention for registered sequences `ids` (batch order; a list
+        or a SeqBatch), q [N, H, D]."""
         _dev(q, "q")
+        b = _batch(ids)
         n, h, d = q.shape
-        if n != len(ids) or d != self.head_dim:
+        if n != len(b) or d != self.head_dim:
             raise ValueError("q must be [len(ids), H, head_dim]")
         if out is None:
             out = torch.empty_like(q)
         if scale is None:
             scale = 1.0 / math.sqrt(d)
-        arr = (ctypes.c_char_p * n)(*[_id(i) for i in ids])
         m = {"grouped": _lib.GQA_GROUPED, "modulo": _lib.GQA_MODULO}[mapping]
-        _lib.check(_lib.lib().zk_cache_paged_decode(self._h, layer, arr, n, q.data_ptr(),
+        _lib.check(_lib.lib().zk_cache_paged_decode(self._h, layer, b.arr, n, q.data_ptr(),
                                                     zk_dtype(q), _dev(out, "out"), h, float(scale), m))
         return out
 
