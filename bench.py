@@ -353,6 +353,7 @@ def bench_c4(args, torch, lib):
     e1.record(s)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / STEPS
+    share_sg, share_pages = cache.decode_sharing()
     ms = e0.elapsed_time(e1) / STEPS
     # decode lengths of the timed steps: ctx0 + s + 1 at every layer of step s
     tok_per_layer = 2 * Hkv * D * 2
@@ -402,7 +403,8 @@ def bench_c4(args, torch, lib):
                         "decode_kernels_ms_per_step": dec_kernel_ms,
                         "decode_kernel_logical_gbps": logical_bytes / (dec_kernel_ms * 1e-3) / 1e9,
                         "decode_kernel_unique_gbps": unique_bytes / (dec_kernel_ms * 1e-3) / 1e9,
-                        "kernel_ms": {k: v[0] for k, v in kt.items() if v[1]}},
+                        "kernel_ms": {k: v[0] for k, v in kt.items() if v[1]},
+                        "prefix_subgroups": share_sg, "shared_pages_per_layer_kv_head": share_pages},
         "stale_handle_rejected": stale_rejected,
     }
     del cache, kin, vin, qin, out

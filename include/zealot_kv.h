@@ -213,10 +213,17 @@ int zk_cache_seq_state(zk_kv_cache *c, const char *id, size_t *cached_tokens,
 /* Host copy of a sequence's block ids (kv_cache.rs:28); *n in: capacity, out: count. */
 int zk_cache_block_ids(zk_kv_cache *c, const char *id, int64_t *ids, size_t *n);
 /* Batched decode for one layer over registered sequences `ids[0..n)`:
- * builds the batch's block tables / lengths and calls zk_paged_decode. */
+ * builds the batch's block tables / lengths and runs the paged decode
+ * (zk_paged_decode; replaces the per-sequence paged_forward loop of
+ * cuda_runner.rs:443-461).  Sequences forked from one prefix (fork_seq) whose
+ * tables start with the same blocks are decoded in subgroups that read the
+ * shared pages once (bf16 pools, MFMA shapes); no reference counterpart. */
 int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, int n,
                           const void *q, zk_dtype q_dtype, void *out, int num_heads, float scale,
                           zk_gqa_mapping mapping);
+/* Prefix sharing of the last zk_cache_paged_decode: subgroups formed and the
+ * pages they shared (sum over subgroups).  No reference counterpart. */
+int zk_cache_decode_sharing(zk_kv_cache *c, int *subgroups, int64_t *shared_pages);
 
 /* ======================================================= measurement
  * No reference counterpart (the reference's attention bench is a stub,

@@ -262,3 +262,66 @@ def test_append_kv_batch_forks_layerwise_decode(kv):
     for sid in children + list(prefixes):
         cache.release_seq(sid)
     assert bm.free_blocks == NB
+
+
+@pytest.mark.parametrize("G,D,qdt,mapping", [(4, 128, "bf16", "grouped"), (1, 128, "bf16", "grouped"),
+                                             (2, 64, "bf16", "grouped"), (8, 128, "bf16", "grouped"),
+                                             (4, 64, "f32", "grouped"), (4, 128, "bf16", "modulo")])
+def test_forked_prefix_decode_shares_pages(G, D, qdt, mapping):
+    """Forks of one prefix are decoded in subgroups that read the shared pages
+    once for up to 32 query rows (QK and PV on MFMA), then merged with each
+    fork's own pages; the result matches the oracle over every sequence's
+    full table, and the expected subgroups were formed."""
+    import zealot_amd as ze
+    from zealot_amd import KVCache
+    rng = np.random.default_rng(1000 + 10 * G + D)
+    Hkv, BS, NB, MB = 2, 16, 512, 32
+    H = G * Hkv
+    prefixes = {"pa": 16 * 17 + 3, "pb": 16 * 20, "solo": 16 * 18 + 1}
+    nforks = {"pa": 9, "pb": 3, "solo": 0}
+    bm = ze.BlockManager(NB, BS)
+    cache = KVCache(NB, BS, 1, Hkv, D, dtype=torch.bfloat16, max_seqs=32, max_blocks_per_seq=MB)
+    for pid, p in prefixes.items():
+        cache.register_seq(pid, MB)
+        for _ in range((p + BS - 1) // BS):
+            cache.alloc_block(pid, bm)
+        cache.store_kv(0, pid, to_dev(normal(rng, (p, Hkv, D), oracle.BF16)),
+                       to_dev(normal(rng, (p, Hkv, D), oracle.BF16)), 0, p)
+    ids = list(prefixes)
+    for pid, nf in nforks.items():
+        for j in range(nf):
+            cid = f"{pid}.{j}"
+            cache.fork_seq(pid, cid)
+            ids.append(cid)
+            for _ in range(1 + j % 4):  # fork-private tokens (copy-on-write of a partial tail)
+                st = cache.seq_state(cid)
+                if st.cached_tokens == len(st.block_ids) * BS:
+                    cache.alloc_block(cid, bm)
+                cache.append_kv(0, cid, to_dev(normal(rng, (1, Hkv, D), oracle.BF16)[0]),
+                                to_dev(normal(rng, (1, Hkv, D), oracle.BF16)[0]))
+    ids = [ids[i] for i in rng.permutation(len(ids))]
+    n = len(ids)
+    q = normal(rng, (n, H, D), oracle.BF16 if qdt == "bf16" else oracle.F32)
+    announce(f"shared-prefix decode G={G} D={D} q={qdt} mapping={mapping}")
+    out = to_host(cache.paged_decode(0, ids, to_dev(q), mapping=mapping))
+    cap = 32 // G
+
+    def chunks(m):
+        return m // cap + (1 if m % cap >= 2 else 0)
+    sg, pages = cache.decode_sharing()
+    assert sg == chunks(1 + nforks["pa"]) + chunks(1 + nforks["pb"])
+    kp, vp = to_host(cache.k_pool(0)), to_host(cache.v_pool(0))
+    bt = -np.ones((n, MB), np.int32)
+    lens = []
+    for i, sid in enumerate(ids):
+        st = cache.seq_state(sid)
+        bt[i, :len(st.block_ids)] = st.block_ids
+        lens.append(st.cached_tokens)
+    qf = as_f32(q, oracle.BF16) if qdt == "bf16" else q
+    ref = oracle.paged_decode(qf, kp, vp, oracle.BF16, bt, lens, Hkv, D, BS, np.float32(1 / math.sqrt(D)),
+                              mapping=oracle.GROUPED if mapping == "grouped" else oracle.MODULO)
+    got = as_f32(out, oracle.BF16) if qdt == "bf16" else out
+    assert max_abs_err(got, ref) <= 2e-2
+    for sid in ids:
+        cache.release_seq(sid)
+    assert bm.free_blocks == NB

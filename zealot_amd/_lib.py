@@ -80,6 +80,7 @@ SIGNATURES = {
                                 ctypes.POINTER(_SZ)]),
     "zk_cache_block_ids": (_I, [_P, _CP, ctypes.POINTER(_I64), ctypes.POINTER(_SZ)]),
     "zk_cache_paged_decode": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _I, _P, _I, _F, _I]),
+    "zk_cache_decode_sharing": (_I, [_P, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int64)]),
     "zk_timing_enable": (_I, [_I]),
     "zk_timing_reset": (_I, []),
     "zk_timing_query": (_I, [_CP, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),

@@ -21,6 +21,14 @@ HIPFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall",
     # packed-fp32 VALU ops stay off: hipcc must not emit v_pk_{add,mul,fma}_f32
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the decode kernels keep one wave per SIMD,
+    # so registers are plentiful, and loop-carried accumulators otherwise get
+    # copied between AGPRs and VGPRs on every page
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # the decode kernels claim work with a lane-0 atomic whose result is used
+    # one work item later; the wave-aggregating rewrite would wait for it at
+    # once and stall the page pipeline
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 

@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <cstring>
 #include <new>
 #include <string>
@@ -149,6 +150,8 @@ struct zk_kv_cache {
     uint64_t dec_epoch = ~0ull;
     size_t dec_stride = 0;
     std::vector<const SeqState *> dec_ids;
+    int last_sg = 0;          // prefix subgroups of the last paged_decode
+    int64_t last_sg_pages = 0;  // and the pages they shared (summed over subgroups)
 
     size_t block_bytes() const { return block_size * num_kv_heads * head_dim * zk::elt_size(dtype); }
     char *k_pool(size_t layer) const { return slab + (2 * layer) * pool_bytes; }
@@ -325,6 +328,62 @@ int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, cons
         s.block_offset = s.cached_tokens % bs;
     }
     return ZK_OK;
+}
+
+// Shared prefixes of a decode batch: sequences whose tables start with the
+// same blocks (fork_seq) read those pages once per subgroup.  A subgroup
+// holds at most `cap` members (32 query rows / G) and shares the longest
+// common run of leading blocks that every member has fully written at this
+// layer; runs shorter than kMinSharedPages are not worth a subgroup.
+constexpr size_t kMinSharedPages = 16;
+
+constexpr int kSgStride = 32;  // member slots per subgroup (the kernel's layout)
+
+struct SharePlan {
+    std::vector<int32_t> seq_pb, sg_members, sg_pages;  // sg_members: [nsg][kSgStride], -1 padded
+    long total_pages = 0;
+};
+
+void plan_sharing(const std::vector<const SeqState *> &seqs, size_t layer, size_t bs, int cap, SharePlan &out) {
+    const int n = (int)seqs.size();
+    out.seq_pb.assign(n, 0);
+    out.sg_members.clear();
+    out.sg_pages.clear();
+    out.total_pages = 0;
+    std::vector<size_t> full(n);
+    std::vector<std::pair<uint64_t, int>> keyed;
+    for (int i = 0; i < n; ++i) {
+        full[i] = std::min(seqs[i]->handles.size(), seqs[i]->layer_len[layer] / bs);
+        if (full[i] >= kMinSharedPages) keyed.emplace_back(seqs[i]->handles[0].block_id, i);
+    }
+    std::sort(keyed.begin(), keyed.end());
+    for (size_t a = 0; a < keyed.size();) {
+        size_t b = a;
+        while (b < keyed.size() && keyed[b].first == keyed[a].first) ++b;
+        for (size_t c0 = a; c0 + 1 < b; c0 += (size_t)cap) {  // chunks of <= cap members
+            const size_t c1 = std::min(b, c0 + (size_t)cap);
+            if (c1 - c0 < 2) break;
+            const SeqState *first = seqs[keyed[c0].second];
+            size_t S = SIZE_MAX;
+            for (size_t m = c0; m < c1; ++m) S = std::min(S, full[keyed[m].second]);
+            for (size_t m = c0 + 1; m < c1 && S > 0; ++m) {
+                const auto &h = seqs[keyed[m].second]->handles;
+                size_t j = 0;
+                while (j < S && h[j].block_id == first->handles[j].block_id) ++j;
+                S = j;
+            }
+            if (S < kMinSharedPages) continue;
+            const size_t base = out.sg_members.size();
+            out.sg_members.resize(base + kSgStride, -1);
+            for (size_t m = c0; m < c1; ++m) {
+                out.sg_members[base + (m - c0)] = keyed[m].second;
+                out.seq_pb[keyed[m].second] = (int32_t)S;
+            }
+            out.sg_pages.push_back((int32_t)S);
+            out.total_pages += (long)S;
+        }
+        a = b;
+    }
 }
 
 }  // namespace
@@ -649,9 +708,19 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
         c->dec_ids = seqs;
         c->dec_stride = stride;
     }
-    // Lengths at this layer, then (fp8) this layer's scales [2][n][H].
-    const size_t len_bytes = (((size_t)n * sizeof(int32_t)) + 255) & ~(size_t)255;
-    const size_t total = len_bytes + (fp8 ? 2 * (size_t)n * H * sizeof(float) : 0);
+    // Shared prefixes of forked sequences (bf16 MFMA shapes only).
+    SharePlan sp;
+    if (num_heads > 0 && num_heads % (int)H == 0 &&
+        zk::paged_decode_shares_prefixes(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads, (int)H))
+        plan_sharing(seqs, layer, c->block_size, 32 / (num_heads / (int)H), sp);
+    const int nsg = (int)sp.sg_pages.size();
+    // Lengths at this layer, (fp8) this layer's scales [2][n][H], (shared
+    // prefixes) seq_pb [n], sg_members [nsg][32], sg_pages [nsg].
+    auto a256 = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t len_bytes = a256((size_t)n * sizeof(int32_t));
+    const size_t sc_bytes = a256(fp8 ? 2 * (size_t)n * H * sizeof(float) : 0);
+    const size_t share_ints = nsg ? (size_t)n + sp.sg_members.size() + sp.sg_pages.size() : 0;
+    const size_t total = len_bytes + sc_bytes + share_ints * sizeof(int32_t);
     std::vector<char> host(total, 0);
     int32_t *lens = (int32_t *)host.data();
     float *sc = (float *)(host.data() + len_bytes);
@@ -662,16 +731,37 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
             std::memcpy(sc + (size_t)n * H + (size_t)i * H, seqs[i]->v_scales.data() + layer * H, H * sizeof(float));
         }
     }
+    int32_t *sh = (int32_t *)(host.data() + len_bytes + sc_bytes);
+    size_t o_pb = 0, o_mem = 0, o_pages = 0;
+    if (nsg) {
+        o_pb = 0;
+        o_mem = o_pb + (size_t)n;
+        o_pages = o_mem + sp.sg_members.size();
+        std::memcpy(sh + o_pb, sp.seq_pb.data(), (size_t)n * sizeof(int32_t));
+        std::memcpy(sh + o_mem, sp.sg_members.data(), sp.sg_members.size() * sizeof(int32_t));
+        std::memcpy(sh + o_pages, sp.sg_pages.data(), sp.sg_pages.size() * sizeof(int32_t));
+    }
     if (int rc = put(c, c->d_batch, host.data(), total, "KVCache decode batch")) return rc;
-    size_t ws = zk_paged_decode_workspace_size(n, num_heads, (int)c->head_dim, (int)stride, (int)c->block_size);
+    size_t ws = zk::paged_decode_workspace(n, num_heads, (int)c->head_dim, (int)stride, (int)c->block_size, nsg > 0);
     if (int rc = c->d_ws.ensure(ws, "KVCache decode workspace")) return rc;
     char *d = (char *)c->d_batch.dev.p;
     const float *dks = fp8 ? (const float *)(d + len_bytes) : nullptr;
     const float *dvs = fp8 ? dks + (size_t)n * H : nullptr;
-    return zk_paged_decode(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
-                           (const int32_t *)c->d_tbl.dev.p, (const int32_t *)d, n, num_heads, (int)H,
-                           (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
-                           mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream);
+    const int32_t *dsh = (const int32_t *)(d + len_bytes + sc_bytes);
+    zk::PrefixGroups pg{dsh + o_pb, dsh + o_mem, dsh + o_pages, nsg, sp.total_pages};
+    c->last_sg = nsg;
+    c->last_sg_pages = sp.total_pages;
+    return zk::paged_decode(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
+                            (const int32_t *)c->d_tbl.dev.p, (const int32_t *)d, n, num_heads, (int)H,
+                            (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
+                            mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr);
+}
+
+int zk_cache_decode_sharing(zk_kv_cache *c, int *subgroups, int64_t *shared_pages) {
+    if (!c) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache: NULL argument");
+    if (subgroups) *subgroups = c->last_sg;
+    if (shared_pages) *shared_pages = c->last_sg_pages;
+    return ZK_OK;
 }
 
 }  // extern "C"

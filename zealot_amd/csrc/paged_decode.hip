@@ -66,6 +66,8 @@ int min_part_pages(int head_dim, int block_size) {
     return e ? e : 16;
 }
 
+constexpr int kSgStride = 32;  // member slots per prefix subgroup (query rows of one shared item)
+
 struct Params {
     const void *q;
     const char *k_pool;
@@ -76,11 +78,23 @@ struct Params {
     const float *k_scales;
     const float *v_scales;
     int32_t *eff_len;     // [N] length after the page walk
-    int32_t *item_start;  // [N + 1] first work item of each sequence (MFMA path)
-    int2 *item_map;       // [N * MP] work item -> (sequence, partition) (MFMA path)
+    int4 *items;          // [N * MP] work-item descriptors, longest first (MFMA path):
+                          //   {n, part, first page, pages} of a sequence's own pages or
+                          //   {-1 - g, part, member 0, pages} of subgroup g's shared pages
     int32_t *work;        // [2] total items, queue head (MFMA path)
+    int num_waves;        // persistent grid: wave w starts with item w
     float2 *ml;   // [N][H][MP] (m, l), log2 domain
     float *po;    // [N][H][MP][D]
+    // Shared prefixes (MFMA bf16 path; all null when unused): sequence n's
+    // first seq_pb[n] pages are the same blocks as every other member of its
+    // prefix subgroup.  Subgroup g has members sg_members[g * kSgStride + i]
+    // (batch indices, at most 32 / G, padded with -1) and sg_pages[g] shared
+    // full pages.  Partial slots of a member: shared parts first, then its
+    // private parts.
+    const int32_t *seq_pb;
+    const int32_t *sg_members;
+    const int32_t *sg_pages;
+    int num_sg, shared_part_pages;
     int num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks, part_pages, max_parts;
     int64_t num_blocks;
     float scale_log2;  // softmax scale * log2(e)
@@ -104,6 +118,18 @@ __device__ __forceinline__ void store_out(const Params &p, size_t i, float x) {
 __device__ __forceinline__ int num_parts_for(const Params &p, int len) {
     int pages = (len + p.block_size - 1) / p.block_size;
     return (pages + p.part_pages - 1) / p.part_pages;
+}
+__device__ __forceinline__ int prefix_pages_of(const Params &p, int n) { return p.seq_pb ? p.seq_pb[n] : 0; }
+// Partitions of sequence n's shared prefix (computed by its subgroup's items).
+__device__ __forceinline__ int shared_parts_of(const Params &p, int n) {
+    const int pb = prefix_pages_of(p, n);
+    return pb > 0 ? (pb + p.shared_part_pages - 1) / p.shared_part_pages : 0;
+}
+// Partitions of the pages after the shared prefix (the sequence's own items).
+__device__ __forceinline__ int private_parts_of(const Params &p, int n) {
+    const int pages = (p.eff_len[n] + p.block_size - 1) / p.block_size;
+    const int rest = pages - prefix_pages_of(p, n);
+    return rest > 0 ? (rest + p.part_pages - 1) / p.part_pages : 0;
 }
 
 // ------------------------------------------------------------ seq info
@@ -166,35 +192,61 @@ __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2_t));
+}
+
+// Lazy-rescale slack of the shared-prefix softmax, in log2 units.
+constexpr float kRescaleSlack = 8.0f;
+
 // ------------------------------------------------------------ work plan
-// A work item is (sequence, partition, kv-head).  The host picks the
-// partition length (part_pages, up to kMaxItemPages) so the queue holds a few
-// items per wave; plan_kernel sizes pairs from the effective lengths of
-// seq_info_kernel and lists the (sequence, partition) pairs longest
-// first (counting sort on the page count) so that the persistent waves, which
-// take items in queue order, perform greedy longest-processing-time-first
-// scheduling.  Item i is pair i / Hkv, kv-head i % Hkv.  The kernel also
-// resets the queue head.
+// A work item is (sequence or prefix subgroup, partition, kv-head).  The host
+// picks the partition length (part_pages, up to kMaxItemPages) so the queue
+// holds a few items per wave; plan_kernel sizes pairs from the effective
+// lengths of seq_info_kernel and lists them longest first (counting sort on
+// the page count) as self-contained descriptors (first page and page count
+// included), so that the persistent waves, which take items in queue order,
+// perform greedy longest-processing-time-first scheduling and start an item
+// with one descriptor load.  Item i is pair i / Hkv, kv-head i % Hkv; wave w
+// takes item w first, then pulls from the queue, whose head the kernel sets.
 constexpr int kMaxItemPages = 1024;
 
+// Pages in flight per wave in the MFMA decode (LDS stages of K + V).
+#ifndef ZK_DECODE_STAGES
+#define ZK_DECODE_STAGES 2
+#endif
+constexpr int kStages = ZK_DECODE_STAGES;
+
 __device__ __forceinline__ int pair_pages(const Params &p, int n, int k) {
-    const int pages = (p.eff_len[n] + p.block_size - 1) / p.block_size;
+    const int pages = (p.eff_len[n] + p.block_size - 1) / p.block_size - prefix_pages_of(p, n);
     return max(0, min(p.part_pages, pages - k * p.part_pages));
+}
+// Items of sequence n: its private partitions; a sequence with neither shared
+// nor private pages still gets one (it writes the zero row).
+__device__ __forceinline__ int private_items_of(const Params &p, int n) {
+    const int np = private_parts_of(p, n);
+    return shared_parts_of(p, n) == 0 ? max(1, np) : np;
+}
+__device__ __forceinline__ int shared_pair_pages(const Params &p, int g, int k) {
+    return max(0, min(p.shared_part_pages, p.sg_pages[g] - k * p.shared_part_pages));
 }
 
 __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
-    constexpr int kBins = kMaxItemPages + 1;  // page counts 0 .. kMaxItemPages
-    __shared__ int hist[2048];                // bin j = kMaxItemPages - pages (longest first)
+    __shared__ int hist[2048];  // bin j = kMaxItemPages - pages (longest first)
     __shared__ int sums[1024];
     const int t = threadIdx.x;
     hist[2 * t] = 0;
     hist[2 * t + 1] = 0;
     __syncthreads();
-    int local = 0;
     for (int n = t; n < num_seqs; n += 1024) {
-        const int np = max(1, num_parts_for(p, p.eff_len[n]));
-        local += np;
+        const int np = private_items_of(p, n);
         for (int k = 0; k < np; ++k) atomicAdd(&hist[kMaxItemPages - pair_pages(p, n, k)], 1);
+    }
+    for (int g = t; g < p.num_sg; g += 1024) {
+        const int np = (p.sg_pages[g] + p.shared_part_pages - 1) / p.shared_part_pages;
+        for (int k = 0; k < np; ++k) atomicAdd(&hist[kMaxItemPages - shared_pair_pages(p, g, k)], 1);
     }
     __syncthreads();
     // exclusive scan of the bins, two per thread (block scan of the pair sums)
@@ -214,17 +266,27 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
     const int total_pairs = sums[1023];
     __syncthreads();
     for (int n = t; n < num_seqs; n += 1024) {
-        const int np = max(1, num_parts_for(p, p.eff_len[n]));
+        const int np = private_items_of(p, n);
         for (int k = 0; k < np; ++k) {
-            const int pos = atomicAdd(&hist[kMaxItemPages - pair_pages(p, n, k)], 1);
-            p.item_map[pos] = make_int2(n, k);
+            const int np = pair_pages(p, n, k);
+            const int pos = atomicAdd(&hist[kMaxItemPages - np], 1);
+            p.items[pos] = make_int4(n, k, prefix_pages_of(p, n) + k * p.part_pages, np);
         }
     }
-    (void)local;
-    (void)kBins;
+    for (int g = t; g < p.num_sg; g += 1024) {
+        const int np = (p.sg_pages[g] + p.shared_part_pages - 1) / p.shared_part_pages;
+        const int n0 = p.sg_members[(size_t)g * kSgStride];
+        // pages member 0's walk reaches (all unless its table is cut inside the prefix)
+        const int valid = min(p.sg_pages[g], p.eff_len[n0] / p.block_size);
+        for (int k = 0; k < np; ++k) {
+            const int pos = atomicAdd(&hist[kMaxItemPages - shared_pair_pages(p, g, k)], 1);
+            const int pages = max(0, min(p.shared_part_pages, valid - k * p.shared_part_pages));
+            p.items[pos] = make_int4(-1 - g, k, n0, pages);  // negative: subgroup item
+        }
+    }
     if (t == 0) {
         p.work[0] = total_pairs * p.num_kv_heads;  // total items
-        p.work[1] = 0;                             // queue head
+        p.work[1] = p.num_waves;                   // queue head: items below are taken statically
     }
 }
 
@@ -259,7 +321,7 @@ struct LdsVec<4> { typedef uint32_t T; };
 // Persistent split-K decode for bf16 / fp8 pools, D in {64, 128}, block_size 16,
 // G = H/Hkv in {1, 2, 4, 8}.  The grid holds a fixed number of one-wave
 // workgroups; each loops over work items.  Per item, the partition's pages
-// stream through two LDS stages per wave: every page (K and V, 16 rows of
+// stream through kStages LDS stages per wave: every page (K and V, 16 rows of
 // D elements each) arrives by global_load_lds_dwordx4, 1 KiB contiguous per
 // instruction, so the next page is in flight while this one is computed.
 //   K stage layout: 16-byte chunk c of row r sits at chunk slot
@@ -289,7 +351,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     constexpr int VBYTES = DV * ELT;     // V bytes per lane per token row
     static_assert(PAGE % 1024 == 0 && KBYTES % 16 == 0, "page shape");
     typedef typename LdsVec<VBYTES>::T vrow_t;
-    __shared__ __attribute__((aligned(16))) char lds[2][2][PAGE];  // [stage][K|V]
+    __shared__ __attribute__((aligned(16))) char lds[kStages][2][PAGE];  // [stage][K|V]
     __shared__ int32_t bids[kMaxItemPages];                         // this item's block ids
 
     const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
@@ -312,22 +374,241 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     }
     const uint32_t vl = (uint32_t)((4 * grp) * RB + col * VBYTES);  // + r * RB
 
+    // Wait until page pi of an np-page item has landed in LDS: the pages
+    // issued after it (up to kStages - 1) may still be in flight.
+    auto wait_page = [&](int pi, int np) {
+        const int ahead = min(kStages - 1, np - 1 - pi);
+        static_assert(kStages >= 2 && kStages <= 4, "pipeline depth");
+        if (ahead <= 0) wait_vmcnt<0>();
+        else if (ahead == 1) wait_vmcnt<LPP>();
+        else if (ahead == 2) wait_vmcnt<(kStages > 2 ? 2 * LPP : 0)>();
+        else wait_vmcnt<(kStages > 3 ? 3 * LPP : 0)>();
+    };
+
+    // Shared-prefix item (bf16 pools): the subgroup's members share the
+    // pages [0, sg_pages) (the same blocks in every member's table), so one
+    // wave reads each page once for all members: up to 32 query rows
+    // (member-major, G heads each) as two 16-column MFMA tiles.
+    //   QK^T  as in the per-sequence path, but every column is its own query
+    //         row; lane (grp, col) gets tokens 4*grp+i of row col.
+    //   softmax  one reference max per row shared by the 4 lane groups (so
+    //         the page's 16 tokens share a scale and PV can run on MFMA),
+    //         moved lazily (kRescaleSlack).
+    //   PV    O^T[dims x rows] += V^T[dims x 16 tokens] * P^T[16 tokens x rows]
+    //         on v_mfma_f32_16x16x16_bf16: P^T is the score fragment as is;
+    //         lane (grp, col) reads DT = D/16 consecutive dims of the 4 token
+    //         rows 4*grp+i and v_perm-transposes them into DT A operands, so
+    //         A row m of tile dt is dim DT*m + dt.
+    // Results are written as partials of every member; the reduce merges them
+    // with the members' private partitions.
+    int next = 0;
+    // Claims the next item; called right after the item's first page load is
+    // issued, so the atomic's round trip overlaps that page's.
+    auto claim_next = [&]() {
+        if (lane == 0) next = atomicAdd(&p.work[1], 1);
+    };
+
+    // Block ids of an item's pages into LDS (eight independent loads in flight
+    // per lane).  The LDS writes wait for their loads, which retires the
+    // item's earlier register loads (Q fragments) too, so the page loop starts
+    // with no register loads pending.  (An explicit s_waitcnt here makes the
+    // compiler's wait insertion drain vmcnt before every page's LDS reads.)
+    auto stage_bids = [&](const int32_t *row, int np) {
+        for (int i0 = 0; i0 < np; i0 += 8 * kWave) {
+            int32_t b[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave + lane;
+                b[j] = i < np ? row[i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave + lane;
+                if (i < np) bids[i] = b[j];
+            }
+        }
+        wait_lgkmcnt0();  // this wave's LDS writes are visible to its own reads
+    };
+
+    auto shared_item = [&](int sg, int part, int kvh, int n0, int np) {
+        if constexpr (KV == ZK_BF16) {
+            constexpr int DT = D / 16;
+            constexpr int T = 2;
+            typedef typename LdsVec<2 * DT>::T vtrow_t;
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            const int32_t *mem = p.sg_members + (size_t)sg * kSgStride;
+            const int page0 = part * p.shared_part_pages;
+
+            bf16x8 qf[T][KK];
+            int nm[T];  // member (batch index) of this lane's query row in tile t, or -1
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const int r = 16 * t + col;
+                nm[t] = mem[r / G];
+                if (nm[t] >= 0) {
+                    const size_t qb = ((size_t)nm[t] * H + qhead_of(p, kvh, r % G, G)) * D + (size_t)grp * DG;
+                    if (p.q_f32) {
+                        const float *qq = (const float *)p.q + qb;
+#pragma unroll
+                        for (int kk = 0; kk < KK; ++kk) {
+                            u32x4 w;
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(qq[8 * kk + 2 * j], qq[8 * kk + 2 * j + 1]);
+                            qf[t][kk] = __builtin_bit_cast(bf16x8, w);
+                        }
+                    } else {
+                        const uint16_t *qq = (const uint16_t *)p.q + qb;
+#pragma unroll
+                        for (int kk = 0; kk < KK; ++kk) qf[t][kk] = *reinterpret_cast<const bf16x8 *>(qq + 8 * kk);
+                    }
+                } else {
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk) qf[t][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+                }
+            }
+            stage_bids(p.bt + (size_t)n0 * p.max_blocks + page0, np);
+            const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
+            const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
+            const size_t block_bytes = (size_t)PAGE * Hkv;
+            auto issue = [&](int pi, int s) {
+                const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
+                const char *kp = kbase + (size_t)blk * block_bytes;
+                const char *vp = vbase + (size_t)blk * block_bytes;
+#pragma unroll
+                for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[s][0] + 1024 * j));
+#pragma unroll
+                for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[s][1] + 1024 * j));
+            };
+            f32x4 o[DT][T];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int t = 0; t < T; ++t) o[dt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            float m_run[T], l_run[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                m_run[t] = -INFINITY;
+                l_run[t] = 0.0f;
+            }
+            const float sl2 = p.scale_log2;
+            auto spage = [&](int pi, int s) {
+                wait_page(pi, np);
+                uint32_t kw[KBYTES / 4];
+#pragma unroll
+                for (int f = 0; f < KCH; ++f) {
+                    const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[s][0] + kl[f]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) kw[4 * f + j] = c4[j];
+                }
+                vtrow_t vt[4];  // token rows 4*grp+i, dims DT*col .. DT*col+DT-1
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    vt[i] = *reinterpret_cast<const vtrow_t *>(lds[s][1] + (4 * grp + i) * RB + col * (2 * DT));
+                wait_lgkmcnt0();
+                if (pi + kStages < np) issue(pi + kStages, s);
+
+                f32x4 sacc[T];
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk)
+                        sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, u32x4{kw[4 * kk], kw[4 * kk + 1], kw[4 * kk + 2], kw[4 * kk + 3]}),
+                            qf[t][kk], sacc[t], 0, 0, 0);
+                }
+                // V^T operands: element i of tile dt = V[4*grp+i][DT*col+dt]
+                s16x4 va[DT];
+                {
+                    uint32_t w[4][DT / 2];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) __builtin_memcpy(w[i], &vt[i], 2 * DT);
+#pragma unroll
+                    for (int j = 0; j < DT / 2; ++j) {
+                        const u32x2 lo{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x05040100u),
+                                       __builtin_amdgcn_perm(w[3][j], w[2][j], 0x05040100u)};
+                        const u32x2 hi{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x07060302u),
+                                       __builtin_amdgcn_perm(w[3][j], w[2][j], 0x07060302u)};
+                        va[2 * j] = __builtin_bit_cast(s16x4, lo);
+                        va[2 * j + 1] = __builtin_bit_cast(s16x4, hi);
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    float sc[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sc[i] = sacc[t][i] * sl2;
+                    const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                    // Lazy rescale: the row's reference max m_run only moves when
+                    // a score exceeds it by more than kRescaleSlack (always on the
+                    // first page), so weights stay <= 2^kRescaleSlack and most
+                    // pages leave the accumulators untouched.  The branch is
+                    // wave-uniform; the new reference is the row max over the
+                    // page's 16 tokens (all four lane groups).
+                    if (__builtin_amdgcn_ballot_w64(mx > m_run[t] + kRescaleSlack)) {
+                        float cm = fmaxf(mx, xor16(mx));
+                        cm = fmaxf(cm, xor32(cm));
+                        const float m_new = fmaxf(m_run[t], cm);  // shared pages are full: finite
+                        const float alpha = exp2_fast(m_run[t] - m_new);
+                        l_run[t] *= alpha;
+#pragma unroll
+                        for (int dt = 0; dt < DT; ++dt) o[dt][t] *= alpha;
+                        m_run[t] = m_new;
+                    }
+                    float pr[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) pr[i] = exp2_fast(sc[i] - m_run[t]);
+                    l_run[t] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+                    const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{bf16x2_rne(pr[0], pr[1]), bf16x2_rne(pr[2], pr[3])});
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt)
+                        o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt][t], 0, 0, 0);
+                }
+            };
+            for (int j = 0; j < kStages && j < np; ++j) issue(j, j);
+            claim_next();
+            // one page per iteration (a single loop-carried accumulator set
+            // stays in the MFMA registers)
+            for (int pi = 0, st = 0; pi < np; ++pi, st = (st + 1 == kStages ? 0 : st + 1)) spage(pi, st);
+            // every member's partial slot `part` of each of its G heads
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float l = l_run[t];
+                l += xor16(l);
+                l += xor32(l);
+                const int r = 16 * t + col;
+                if (nm[t] >= 0) {
+                    const size_t slot = ((size_t)nm[t] * H + qhead_of(p, kvh, r % G, G)) * p.max_parts + part;
+                    float *dst = p.po + slot * D;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float v[DT];
+#pragma unroll
+                        for (int dt = 0; dt < DT; ++dt) v[dt] = o[dt][t][i];
+                        __builtin_memcpy(dst + DT * (4 * grp + i), v, sizeof(v));
+                    }
+                    if (grp == 0) p.ml[slot] = make_float2(m_run[t], l);
+                }
+            }
+        }
+    };
+
     const int total = p.work[0];
-    int item = 0;
-    if (lane == 0) item = atomicAdd(&p.work[1], 1);
-    item = __builtin_amdgcn_readfirstlane(item);
+    int item = blockIdx.x;  // first item static, the rest from the queue
     while (item < total) {
-        int next = 0;
-        if (lane == 0) next = atomicAdd(&p.work[1], 1);  // older than this item's page loads
         const int kvh = item % Hkv;
-        const int2 np_pair = p.item_map[item / Hkv];
-        const int n = np_pair.x, part = np_pair.y;
+        const int4 desc = p.items[item / Hkv];
+        if constexpr (KV == ZK_BF16) {
+            if (desc.x < 0) {  // a shared-prefix partition of a subgroup
+                shared_item(-1 - desc.x, desc.y, kvh, desc.z, desc.w);
+                item = __builtin_amdgcn_readfirstlane(next);
+                continue;
+            }
+        }
+        const int n = desc.x, part = desc.y, page0 = desc.z, np = desc.w;
         const int len = p.eff_len[n];  // walk already cut at the first invalid entry
-        const int pages = (len + BS - 1) / BS;
-        const int nparts = (pages + p.part_pages - 1) / p.part_pages;
-        const int page0 = part * p.part_pages;
-        const int np = nparts > 0 ? min(p.part_pages, pages - page0) : 0;
-        const int32_t *row = p.bt + (size_t)n * p.max_blocks;
+        const int ns = shared_parts_of(p, n);   // partial slots before this sequence's own
+        const int nparts = private_parts_of(p, n);
 
         // Q fragment (B operand): column col -> head col % G
         bf16x8 qf[KK];
@@ -353,20 +634,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
             vscale = p.v_scales[(size_t)n * Hkv + kvh];
         }
-        for (int i0 = 0; i0 < np; i0 += 8 * kWave) {  // eight independent loads per lane per round
-            int32_t b[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + j * kWave + lane;
-                b[j] = i < np ? row[page0 + i] : 0;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + j * kWave + lane;
-                if (i < np) bids[i] = b[j];
-            }
-        }
-        wait_lgkmcnt0();  // this wave's LDS writes are visible to its own reads
+        stage_bids(p.bt + (size_t)n * p.max_blocks + page0, np);
         const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
         const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
         const size_t block_bytes = (size_t)PAGE * Hkv;
@@ -389,8 +657,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         float m_run = -INFINITY, l_run = 0.0f;
 
         auto page = [&](int pi, int s) {
-            if (pi + 1 < np) wait_vmcnt<LPP>();  // page pi landed, pi + 1 may still fly
-            else wait_vmcnt<0>();
+            wait_page(pi, np);
             uint32_t kw[KBYTES / 4];
 #pragma unroll
             for (int f = 0; f < KCH; ++f) {
@@ -402,7 +669,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) vr[r] = *reinterpret_cast<const vrow_t *>(lds[s][1] + vl + r * RB);
             wait_lgkmcnt0();
-            if (pi + 2 < np) issue(pi + 2, s);  // the stage is free again
+            if (pi + kStages < np) issue(pi + kStages, s);  // the stage is free again
 
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -477,11 +744,13 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             });
         };
 
-        if (np > 0) issue(0, 0);
-        if (np > 1) issue(1, 1);
-        for (int pi = 0; pi < np; pi += 2) {
-            page(pi, 0);
-            if (pi + 1 < np) page(pi + 1, 1);
+        for (int j = 0; j < kStages && j < np; ++j) issue(j, j);
+        claim_next();
+        for (int pi = 0; pi < np; pi += kStages) {
+            static_for<kStages>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                if (pi + j < np) page(pi + j, j);
+            });
         }
 
         // merge the four 16-lane rows
@@ -503,7 +772,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             }
         });
         // lanes 0..15 hold o[h][col*DV + d]; lane h < G holds (M, lsum) of head h
-        if (nparts <= 1) {
+        if (ns == 0 && nparts <= 1) {
             static_for<G>([&](auto hc) {
                 constexpr int h = decltype(hc)::value;
                 const float l_h = head_bcast<G, h>(lsum);
@@ -522,7 +791,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         } else {
             static_for<G>([&](auto hc) {
                 constexpr int h = decltype(hc)::value;
-                const size_t slot = ((size_t)n * H + qhead_of(p, kvh, h, G)) * p.max_parts + part;
+                const size_t slot = ((size_t)n * H + qhead_of(p, kvh, h, G)) * p.max_parts + ns + part;
                 if (grp == 0) {
                     float *dst = p.po + slot * D + (size_t)col * DV;
 #pragma unroll
@@ -670,9 +939,9 @@ __global__ void __launch_bounds__(kWave) decode_generic_kernel(Params p) {
 // the partitions eight at a time so 16 loads per lane are in flight.
 __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    const int len = p.eff_len[n];
-    const int nparts = num_parts_for(p, len);
-    if (nparts <= 1) return;
+    const int ns = shared_parts_of(p, n);
+    const int nparts = ns + private_parts_of(p, n);
+    if (ns == 0 && nparts <= 1) return;  // written by the partition kernel
     const int D = p.head_dim;
     const size_t base = ((size_t)n * p.num_heads + h) * p.max_parts;
     float M = -INFINITY;
@@ -721,8 +990,8 @@ WsLayout ws_layout(int num_seqs, int num_heads, int head_dim, int max_parts) {
     WsLayout w;
     w.eff = 0;
     w.items = align256(sizeof(int32_t) * (size_t)num_seqs);
-    w.map = w.items + align256(sizeof(int32_t) * ((size_t)num_seqs + 1));
-    w.work = w.map + align256(sizeof(int2) * (size_t)num_seqs * max_parts);
+    w.map = w.items;
+    w.work = w.map + align256(sizeof(int4) * (size_t)num_seqs * max_parts);
     w.ml = w.work + 256;
     size_t slots = (size_t)num_seqs * num_heads * max_parts;
     w.po = w.ml + align256(sizeof(float2) * slots);
@@ -803,24 +1072,43 @@ int check_launch(const char *what) {
     return ZK_OK;
 }
 
+// Pages per shared-prefix item: about one item per two waves over all
+// subgroups' pages, so half the waves stream the shared pages (two query-row
+// tiles each) while the rest run the sequences' own items; measured best on
+// forked-prefix batches.  ZEALOT_DECODE_SHARED_PART_PAGES (16..1024) overrides.
+int shared_part_pages_for(long total_shared_pages, int num_kv_heads) {
+    static const int env = [] {
+        const char *e = std::getenv("ZEALOT_DECODE_SHARED_PART_PAGES");
+        const int v = e ? std::atoi(e) : 0;
+        return v <= 0 ? 0 : (v < 16 ? 16 : (v > kMaxItemPages ? kMaxItemPages : v));
+    }();
+    if (env) return env;
+    const long half = persistent_grid() / 2;
+    long pp = (total_shared_pages * num_kv_heads + half - 1) / half;
+    pp = (pp + 15) / 16 * 16;
+    return (int)(pp < 16 ? 16 : (pp > kMaxItemPages ? kMaxItemPages : pp));
+}
+
 }  // namespace
 
-extern "C" {
-
-size_t zk_paged_decode_workspace_size(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq,
-                                      int block_size) {
+size_t zk::paged_decode_workspace(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq,
+                                  int block_size, bool shared) {
     if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0) return 256;
     return ws_layout(num_seqs, num_heads, head_dim,
-                     max_parts_for(max_blocks_per_seq, min_part_pages(head_dim, block_size)))
+                     max_parts_for(max_blocks_per_seq, min_part_pages(head_dim, block_size)) + (shared ? 1 : 0))
         .total;
 }
 
-int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool,
-                    zk_dtype kv_dtype, void *out, const int32_t *block_tables, const int32_t *seq_lens,
-                    int num_seqs, int num_heads, int num_kv_heads, int head_dim, int block_size,
-                    int max_blocks_per_seq, int64_t num_blocks, float scale, zk_gqa_mapping mapping,
-                    const float *k_scales, const float *v_scales, void *workspace, size_t workspace_bytes,
-                    void *stream) {
+bool zk::paged_decode_shares_prefixes(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads) {
+    return kv_dtype == ZK_BF16 && num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
+           mfma_supported(kv_dtype, head_dim, block_size, num_heads / num_kv_heads);
+}
+
+int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
+                     void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
+                     int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
+                     float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
+                     void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: q dtype must be f32 or bf16");
     if (!valid_dtype(kv_dtype))
@@ -849,7 +1137,15 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
     const bool use_mfma = mfma_supported(kv_dtype, head_dim, block_size, G);
     const int part_pages = use_mfma ? mfma_part_pages(num_seqs, num_kv_heads, max_blocks_per_seq)
                                     : part_pages_for(ZK_F32, head_dim, block_size);
-    const int max_parts = max_parts_for(max_blocks_per_seq, part_pages);
+    const bool shared = pg && pg->num_sg > 0 &&
+                        paged_decode_shares_prefixes(kv_dtype, head_dim, block_size, num_heads, num_kv_heads);
+    if (shared && (!pg->seq_pb || !pg->sg_members || !pg->sg_pages))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: paged decode: NULL prefix-group array");
+    const int shared_pages = shared ? shared_part_pages_for(pg->total_shared_pages, num_kv_heads) : 0;
+    // slot stride: a sequence's shared and private partitions together
+    const int max_parts =
+        shared ? max_parts_for(max_blocks_per_seq, min_part_pages(head_dim, block_size)) + 1
+               : max_parts_for(max_blocks_per_seq, part_pages);
     WsLayout w = ws_layout(num_seqs, num_heads, head_dim, max_parts);
     if (workspace_bytes < w.total || ((uintptr_t)workspace & 255u))
         return set_error(ZK_ERR_INVALID_ARGUMENT,
@@ -867,9 +1163,9 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
     p.v_scales = v_scales;
     char *ws = (char *)workspace;
     p.eff_len = (int32_t *)(ws + w.eff);
-    p.item_start = (int32_t *)(ws + w.items);
-    p.item_map = (int2 *)(ws + w.map);
+    p.items = (int4 *)(ws + w.map);
     p.work = (int32_t *)(ws + w.work);
+    p.num_waves = use_mfma ? persistent_grid() : 0;
     p.ml = (float2 *)(ws + w.ml);
     p.po = (float *)(ws + w.po);
     p.num_seqs = num_seqs;
@@ -881,6 +1177,11 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
     p.part_pages = part_pages;
     p.max_parts = max_parts;
     p.num_blocks = num_blocks;
+    p.seq_pb = shared ? pg->seq_pb : nullptr;
+    p.sg_members = shared ? pg->sg_members : nullptr;
+    p.sg_pages = shared ? pg->sg_pages : nullptr;
+    p.num_sg = shared ? pg->num_sg : 0;
+    p.shared_part_pages = shared ? shared_pages : 1;
     p.scale_log2 = scale * kLog2e;
     p.grouped = mapping == ZK_GQA_GROUPED ? 1 : 0;
     p.q_f32 = q_dtype == ZK_F32 ? 1 : 0;
@@ -898,7 +1199,7 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
         }
         if (int rc = check_launch("zk_paged_decode plan")) return rc;
         KernelTimer timer("decode_partials", s);
-        const int grid = persistent_grid();
+        const int grid = p.num_waves;
         if (kv_dtype == ZK_BF16) launch_mfma<ZK_BF16>(p, grid, s, G);
         else launch_mfma<ZK_FP8_E4M3>(p, grid, s, G);
     } else {
@@ -909,13 +1210,31 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
         else decode_generic_kernel<ZK_FP8_E4M3><<<grid, kWave, 0, s>>>(p);
     }
     if (int rc = check_launch("zk_paged_decode partials")) return rc;
-    if (max_parts > 1) {
+    if (max_parts > 1 || shared) {
         dim3 rgrid(num_heads, num_seqs);
         KernelTimer timer("decode_reduce", s);
         decode_reduce_kernel<<<rgrid, kWave, 0, s>>>(p);
         if (int rc = check_launch("zk_paged_decode reduce")) return rc;
     }
     return ZK_OK;
+}
+
+extern "C" {
+
+size_t zk_paged_decode_workspace_size(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq,
+                                      int block_size) {
+    return zk::paged_decode_workspace(num_seqs, num_heads, head_dim, max_blocks_per_seq, block_size, false);
+}
+
+int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool,
+                    zk_dtype kv_dtype, void *out, const int32_t *block_tables, const int32_t *seq_lens,
+                    int num_seqs, int num_heads, int num_kv_heads, int head_dim, int block_size,
+                    int max_blocks_per_seq, int64_t num_blocks, float scale, zk_gqa_mapping mapping,
+                    const float *k_scales, const float *v_scales, void *workspace, size_t workspace_bytes,
+                    void *stream) {
+    return zk::paged_decode(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, seq_lens, num_seqs,
+                            num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, num_blocks, scale,
+                            mapping, k_scales, v_scales, workspace, workspace_bytes, stream, nullptr);
 }
 
 }  // extern "C"

@@ -45,6 +45,28 @@ class KernelTimer {
 // apply a batch of block-table updates in one launch.
 int scatter_i32(int32_t *base, int64_t limit, const int2 *pairs, int n, hipStream_t stream);
 
+// Shared-prefix description for the paged decode (device arrays, see the
+// Params comment in paged_decode.hip); total_shared_pages is the host-side
+// sum of sg_pages, used to size the shared partitions.
+struct PrefixGroups {
+    const int32_t *seq_pb;      // [N] shared pages of each sequence (0: none)
+    const int32_t *sg_members;  // [num_sg][32] batch indices, padded with -1
+    const int32_t *sg_pages;
+    int num_sg;
+    long total_shared_pages;
+};
+// zk_paged_decode with optional shared prefixes (pg may be null).
+int paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
+                 void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
+                 int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
+                 float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
+                 void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg);
+size_t paged_decode_workspace(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq, int block_size,
+                              bool shared);
+// Whether paged_decode runs shared-prefix items for this shape (otherwise pg
+// is ignored and every sequence reads its whole table).
+bool paged_decode_shares_prefixes(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads);
+
 inline int elt_size(int dt) { return dt == ZK_F32 ? 4 : dt == ZK_BF16 ? 2 : 1; }
 inline bool valid_dtype(int dt) { return dt == ZK_F32 || dt == ZK_BF16 || dt == ZK_FP8_E4M3; }
 

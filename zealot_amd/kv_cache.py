@@ -187,6 +187,12 @@ class KVCache:
                                                     zk_dtype(q), _dev(out, "out"), h, float(scale), m))
         return out
 
+    def decode_sharing(self):
+        """(subgroups, shared pages) of the last paged_decode's prefix sharing."""
+        sg, pages = ctypes.c_int(), ctypes.c_int64()
+        _lib.check(_lib.lib().zk_cache_decode_sharing(self._h, ctypes.byref(sg), ctypes.byref(pages)))
+        return sg.value, pages.value
+
     # -- pool views ----------------------------------------------------------
     def _pool_view(self, ptr: int) -> torch.Tensor:
         """Device tensor aliasing a pool (shape [num_blocks, Hkv, bs, D])."""
