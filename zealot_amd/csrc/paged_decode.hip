@@ -328,19 +328,32 @@ struct LdsVec<4> { typedef uint32_t T; };
 //     r * CPR + (c ^ (r % CPR)), so the MFMA fragment reads (16 rows, same c)
 //     hit distinct LDS banks.
 //   V stage layout: natural [row][D].
-// Scores: QK^T on v_mfma_f32_16x16x32_bf16 with A = K rows (tokens), B = the G
-// query heads replicated over the 16 columns; lane l gets tokens 4*(l/16)+i of
-// head (l%16)%G.  PV: each lane accumulates D/16 dims of all G heads for the
-// four tokens 4*(l/16)+r, taking the other heads' weights by DPP/ds_swizzle
-// broadcasts; each 16-lane row keeps its own online-softmax state and the
-// rows merge once per item.
+// An item computes the query rows held in the columns of T 16-column MFMA
+// tiles: a sequence's own partition has the G heads of one kv-head (T = 1,
+// columns >= G idle); a prefix subgroup's shared partition has member-major
+// rows, G heads per member (T = 2, up to 32 rows), so one read of a shared
+// page serves every member.
+//   QK^T  v_mfma_f32_16x16x32_bf16, A = the page's 16 K rows (tokens), B = the
+//         tile's query rows; lane (grp, col) gets tokens 4*grp+i of row col.
+//   softmax  one reference max per row, shared by the 4 lane groups and moved
+//         lazily: only when a score exceeds it by kRescaleSlack (always on the
+//         first page), so weights stay <= 2^kRescaleSlack, the 16 tokens of a
+//         page share a scale, and most pages leave the accumulators alone.
+//   PV    O^T[dims x rows] += V^T[dims x 16 tokens] * P^T[16 tokens x rows] on
+//         v_mfma_f32_16x16x16_bf16: P^T is the score fragment in bf16; lane
+//         (grp, col) reads DT = D/16 consecutive dims of the token rows
+//         4*grp+i (fp8 pools: converted to bf16, exactly) and v_perm
+//         transposes them into DT A operands, so A row m of tile dt is dim
+//         DT*m + dt.
+// fp8 pools: the K scale folds into the softmax scale, the V scale into the
+// result.
 template <int KV, int D, int G>
 __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     constexpr int BS = 16;
     constexpr int ELT = KV == ZK_BF16 ? 2 : 1;
-    constexpr int DG = D / 4;            // head dims per 16-lane row in QK
+    constexpr int DG = D / 4;            // head dims per lane group in QK
     constexpr int KK = DG / 8;           // MFMA k-steps
-    constexpr int DV = D / 16;           // dims per lane in PV
+    constexpr int DT = D / 16;           // PV dim tiles = dims per lane per V row
     constexpr int RB = D * ELT;          // bytes per token row
     constexpr int CPR = RB / 16;         // 16-byte chunks per row
     constexpr int PAGE = BS * RB;        // bytes per (block, kv-head) page
@@ -348,15 +361,15 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     constexpr int LPP = 2 * LPK;         // per page, K and V
     constexpr int KBYTES = DG * ELT;     // K fragment bytes per lane per page
     constexpr int KCH = KBYTES / 16;     // ... in 16-byte chunks
-    constexpr int VBYTES = DV * ELT;     // V bytes per lane per token row
-    static_assert(PAGE % 1024 == 0 && KBYTES % 16 == 0, "page shape");
-    typedef typename LdsVec<VBYTES>::T vrow_t;
+    constexpr int VTB = DT * ELT;        // V bytes per lane per token row
+    static_assert(PAGE % 1024 == 0 && KBYTES % 16 == 0 && DT % 2 == 0, "page shape");
+    typedef typename LdsVec<VTB>::T vtrow_t;
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
     __shared__ __attribute__((aligned(16))) char lds[kStages][2][PAGE];  // [stage][K|V]
-    __shared__ int32_t bids[kMaxItemPages];                         // this item's block ids
+    __shared__ int32_t bids[kMaxItemPages];                              // this item's block ids
 
     const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
     const int H = p.num_heads, Hkv = p.num_kv_heads;
-    const int my_head = col % G;
 
     // per-lane byte offsets, fixed for the whole kernel
     uint32_t kg[LPK], vg[LPK];  // global offsets inside a page
@@ -372,7 +385,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         const int row = col, c = grp * KCH + f;
         kl[f] = (row * CPR + (c ^ (row % CPR))) * 16;
     }
-    const uint32_t vl = (uint32_t)((4 * grp) * RB + col * VBYTES);  // + r * RB
+    const uint32_t vt_off = (uint32_t)((4 * grp) * RB + col * VTB);  // + i * RB
 
     // Wait until page pi of an np-page item has landed in LDS: the pages
     // issued after it (up to kStages - 1) may still be in flight.
@@ -385,25 +398,9 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         else wait_vmcnt<(kStages > 3 ? 3 * LPP : 0)>();
     };
 
-    // Shared-prefix item (bf16 pools): the subgroup's members share the
-    // pages [0, sg_pages) (the same blocks in every member's table), so one
-    // wave reads each page once for all members: up to 32 query rows
-    // (member-major, G heads each) as two 16-column MFMA tiles.
-    //   QK^T  as in the per-sequence path, but every column is its own query
-    //         row; lane (grp, col) gets tokens 4*grp+i of row col.
-    //   softmax  one reference max per row shared by the 4 lane groups (so
-    //         the page's 16 tokens share a scale and PV can run on MFMA),
-    //         moved lazily (kRescaleSlack).
-    //   PV    O^T[dims x rows] += V^T[dims x 16 tokens] * P^T[16 tokens x rows]
-    //         on v_mfma_f32_16x16x16_bf16: P^T is the score fragment as is;
-    //         lane (grp, col) reads DT = D/16 consecutive dims of the 4 token
-    //         rows 4*grp+i and v_perm-transposes them into DT A operands, so
-    //         A row m of tile dt is dim DT*m + dt.
-    // Results are written as partials of every member; the reduce merges them
-    // with the members' private partitions.
     int next = 0;
-    // Claims the next item; called right after the item's first page load is
-    // issued, so the atomic's round trip overlaps that page's.
+    // Claims the next item; called right after the item's first page loads
+    // are issued, so the atomic's round trip overlaps theirs.
     auto claim_next = [&]() {
         if (lane == 0) next = atomicAdd(&p.work[1], 1);
     };
@@ -430,215 +427,35 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         wait_lgkmcnt0();  // this wave's LDS writes are visible to its own reads
     };
 
-    auto shared_item = [&](int sg, int part, int kvh, int n0, int np) {
-        if constexpr (KV == ZK_BF16) {
-            constexpr int DT = D / 16;
-            constexpr int T = 2;
-            typedef typename LdsVec<2 * DT>::T vtrow_t;
-            typedef short s16x4 __attribute__((ext_vector_type(4)));
-            const int32_t *mem = p.sg_members + (size_t)sg * kSgStride;
-            const int page0 = part * p.shared_part_pages;
-
-            bf16x8 qf[T][KK];
-            int nm[T];  // member (batch index) of this lane's query row in tile t, or -1
+    // B fragment of query row (n, qh): this lane group's DG dims as KK bf16x8.
+    auto load_q = [&](int n, int qh, bf16x8 *qf) {
+        const size_t qb = ((size_t)n * H + qh) * D + (size_t)grp * DG;
+        if (p.q_f32) {
+            const float *qq = (const float *)p.q + qb;
 #pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const int r = 16 * t + col;
-                nm[t] = mem[r / G];
-                if (nm[t] >= 0) {
-                    const size_t qb = ((size_t)nm[t] * H + qhead_of(p, kvh, r % G, G)) * D + (size_t)grp * DG;
-                    if (p.q_f32) {
-                        const float *qq = (const float *)p.q + qb;
+            for (int kk = 0; kk < KK; ++kk) {
+                u32x4 w;
 #pragma unroll
-                        for (int kk = 0; kk < KK; ++kk) {
-                            u32x4 w;
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(qq[8 * kk + 2 * j], qq[8 * kk + 2 * j + 1]);
-                            qf[t][kk] = __builtin_bit_cast(bf16x8, w);
-                        }
-                    } else {
-                        const uint16_t *qq = (const uint16_t *)p.q + qb;
-#pragma unroll
-                        for (int kk = 0; kk < KK; ++kk) qf[t][kk] = *reinterpret_cast<const bf16x8 *>(qq + 8 * kk);
-                    }
-                } else {
-#pragma unroll
-                    for (int kk = 0; kk < KK; ++kk) qf[t][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-                }
+                for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(qq[8 * kk + 2 * j], qq[8 * kk + 2 * j + 1]);
+                qf[kk] = __builtin_bit_cast(bf16x8, w);
             }
-            stage_bids(p.bt + (size_t)n0 * p.max_blocks + page0, np);
-            const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
-            const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
-            const size_t block_bytes = (size_t)PAGE * Hkv;
-            auto issue = [&](int pi, int s) {
-                const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
-                const char *kp = kbase + (size_t)blk * block_bytes;
-                const char *vp = vbase + (size_t)blk * block_bytes;
+        } else {
+            const uint16_t *qq = (const uint16_t *)p.q + qb;
 #pragma unroll
-                for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[s][0] + 1024 * j));
-#pragma unroll
-                for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[s][1] + 1024 * j));
-            };
-            f32x4 o[DT][T];
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int t = 0; t < T; ++t) o[dt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            float m_run[T], l_run[T];
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                m_run[t] = -INFINITY;
-                l_run[t] = 0.0f;
-            }
-            const float sl2 = p.scale_log2;
-            auto spage = [&](int pi, int s) {
-                wait_page(pi, np);
-                uint32_t kw[KBYTES / 4];
-#pragma unroll
-                for (int f = 0; f < KCH; ++f) {
-                    const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[s][0] + kl[f]);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) kw[4 * f + j] = c4[j];
-                }
-                vtrow_t vt[4];  // token rows 4*grp+i, dims DT*col .. DT*col+DT-1
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    vt[i] = *reinterpret_cast<const vtrow_t *>(lds[s][1] + (4 * grp + i) * RB + col * (2 * DT));
-                wait_lgkmcnt0();
-                if (pi + kStages < np) issue(pi + kStages, s);
-
-                f32x4 sacc[T];
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int kk = 0; kk < KK; ++kk)
-                        sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8, u32x4{kw[4 * kk], kw[4 * kk + 1], kw[4 * kk + 2], kw[4 * kk + 3]}),
-                            qf[t][kk], sacc[t], 0, 0, 0);
-                }
-                // V^T operands: element i of tile dt = V[4*grp+i][DT*col+dt]
-                s16x4 va[DT];
-                {
-                    uint32_t w[4][DT / 2];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) __builtin_memcpy(w[i], &vt[i], 2 * DT);
-#pragma unroll
-                    for (int j = 0; j < DT / 2; ++j) {
-                        const u32x2 lo{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x05040100u),
-                                       __builtin_amdgcn_perm(w[3][j], w[2][j], 0x05040100u)};
-                        const u32x2 hi{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x07060302u),
-                                       __builtin_amdgcn_perm(w[3][j], w[2][j], 0x07060302u)};
-                        va[2 * j] = __builtin_bit_cast(s16x4, lo);
-                        va[2 * j + 1] = __builtin_bit_cast(s16x4, hi);
-                    }
-                }
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    float sc[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) sc[i] = sacc[t][i] * sl2;
-                    const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-                    // Lazy rescale: the row's reference max m_run only moves when
-                    // a score exceeds it by more than kRescaleSlack (always on the
-                    // first page), so weights stay <= 2^kRescaleSlack and most
-                    // pages leave the accumulators untouched.  The branch is
-                    // wave-uniform; the new reference is the row max over the
-                    // page's 16 tokens (all four lane groups).
-                    if (__builtin_amdgcn_ballot_w64(mx > m_run[t] + kRescaleSlack)) {
-                        float cm = fmaxf(mx, xor16(mx));
-                        cm = fmaxf(cm, xor32(cm));
-                        const float m_new = fmaxf(m_run[t], cm);  // shared pages are full: finite
-                        const float alpha = exp2_fast(m_run[t] - m_new);
-                        l_run[t] *= alpha;
-#pragma unroll
-                        for (int dt = 0; dt < DT; ++dt) o[dt][t] *= alpha;
-                        m_run[t] = m_new;
-                    }
-                    float pr[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) pr[i] = exp2_fast(sc[i] - m_run[t]);
-                    l_run[t] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-                    const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{bf16x2_rne(pr[0], pr[1]), bf16x2_rne(pr[2], pr[3])});
-#pragma unroll
-                    for (int dt = 0; dt < DT; ++dt)
-                        o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt][t], 0, 0, 0);
-                }
-            };
-            for (int j = 0; j < kStages && j < np; ++j) issue(j, j);
-            claim_next();
-            // one page per iteration (a single loop-carried accumulator set
-            // stays in the MFMA registers)
-            for (int pi = 0, st = 0; pi < np; ++pi, st = (st + 1 == kStages ? 0 : st + 1)) spage(pi, st);
-            // every member's partial slot `part` of each of its G heads
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                float l = l_run[t];
-                l += xor16(l);
-                l += xor32(l);
-                const int r = 16 * t + col;
-                if (nm[t] >= 0) {
-                    const size_t slot = ((size_t)nm[t] * H + qhead_of(p, kvh, r % G, G)) * p.max_parts + part;
-                    float *dst = p.po + slot * D;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float v[DT];
-#pragma unroll
-                        for (int dt = 0; dt < DT; ++dt) v[dt] = o[dt][t][i];
-                        __builtin_memcpy(dst + DT * (4 * grp + i), v, sizeof(v));
-                    }
-                    if (grp == 0) p.ml[slot] = make_float2(m_run[t], l);
-                }
-            }
+            for (int kk = 0; kk < KK; ++kk) qf[kk] = *reinterpret_cast<const bf16x8 *>(qq + 8 * kk);
         }
     };
 
-    const int total = p.work[0];
-    int item = blockIdx.x;  // first item static, the rest from the queue
-    while (item < total) {
-        const int kvh = item % Hkv;
-        const int4 desc = p.items[item / Hkv];
-        if constexpr (KV == ZK_BF16) {
-            if (desc.x < 0) {  // a shared-prefix partition of a subgroup
-                shared_item(-1 - desc.x, desc.y, kvh, desc.z, desc.w);
-                item = __builtin_amdgcn_readfirstlane(next);
-                continue;
-            }
-        }
-        const int n = desc.x, part = desc.y, page0 = desc.z, np = desc.w;
-        const int len = p.eff_len[n];  // walk already cut at the first invalid entry
-        const int ns = shared_parts_of(p, n);   // partial slots before this sequence's own
-        const int nparts = private_parts_of(p, n);
-
-        // Q fragment (B operand): column col -> head col % G
-        bf16x8 qf[KK];
-        {
-            const size_t qb = ((size_t)n * H + qhead_of(p, kvh, my_head, G)) * D + (size_t)grp * DG;
-            if (p.q_f32) {
-                const float *qq = (const float *)p.q + qb;
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    u32x4 w;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(qq[8 * kk + 2 * j], qq[8 * kk + 2 * j + 1]);
-                    qf[kk] = __builtin_bit_cast(bf16x8, w);
-                }
-            } else {
-                const uint16_t *qq = (const uint16_t *)p.q + qb;
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) qf[kk] = *reinterpret_cast<const bf16x8 *>(qq + 8 * kk);
-            }
-        }
-        float sl2 = p.scale_log2, vscale = 1.0f;
-        if constexpr (KV == ZK_FP8_E4M3) {
-            sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
-            vscale = p.v_scales[(size_t)n * Hkv + kvh];
-        }
-        stage_bids(p.bt + (size_t)n * p.max_blocks + page0, np);
+    // Attention of T tiles of query rows (qf) over pages [page0, page0 + np)
+    // of table `trow` for kv-head kvh; tokens at positions >= len are masked.
+    // Leaves O^T (o), the rows' reference max (m) and sum (l, all 4 lane
+    // groups) for the caller to write.
+    auto attend = [&]<int T>(const bf16x8 (&qf)[T][KK], const int32_t *trow, int page0, int np, int len,
+                             int kvh, float sl2, f32x4 (&o)[DT][T], float (&m)[T], float (&l)[T]) {
+        stage_bids(trow + page0, np);
         const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
         const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
         const size_t block_bytes = (size_t)PAGE * Hkv;
-
         auto issue = [&](int pi, int s) {
             const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
             const char *kp = kbase + (size_t)blk * block_bytes;
@@ -648,14 +465,13 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
 #pragma unroll
             for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[s][1] + 1024 * j));
         };
-
-        float o[G][DV];
 #pragma unroll
-        for (int h = 0; h < G; ++h)
+        for (int t = 0; t < T; ++t) {
+            m[t] = -INFINITY;
+            l[t] = 0.0f;
 #pragma unroll
-            for (int d = 0; d < DV; ++d) o[h][d] = 0.0f;
-        float m_run = -INFINITY, l_run = 0.0f;
-
+            for (int dt = 0; dt < DT; ++dt) o[dt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
         auto page = [&](int pi, int s) {
             wait_page(pi, np);
             uint32_t kw[KBYTES / 4];
@@ -665,13 +481,15 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) kw[4 * f + j] = c4[j];
             }
-            vrow_t vr[4];
+            vtrow_t vt[4];  // token rows 4*grp+i, dims DT*col .. DT*col+DT-1
 #pragma unroll
-            for (int r = 0; r < 4; ++r) vr[r] = *reinterpret_cast<const vrow_t *>(lds[s][1] + vl + r * RB);
+            for (int i = 0; i < 4; ++i) vt[i] = *reinterpret_cast<const vtrow_t *>(lds[s][1] + vt_off + i * RB);
             wait_lgkmcnt0();
             if (pi + kStages < np) issue(pi + kStages, s);  // the stage is free again
 
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4 sacc[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
                 u32x4 w;
@@ -681,124 +499,178 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
                     const u32x2 lo2 = e4m3x4_to_bf16x4(kw[2 * kk]), hi2 = e4m3x4_to_bf16x4(kw[2 * kk + 1]);
                     w = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
                 }
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), qf[kk], acc, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), qf[t][kk],
+                                                                      sacc[t], 0, 0, 0);
+            }
+            // V rows as bf16 pairs: w[i][j] = dims (2j, 2j+1) of token row 4*grp+i
+            uint32_t w[4][DT / 2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (KV == ZK_BF16) {
+                    __builtin_memcpy(w[i], &vt[i], 2 * DT);
+                } else {
+                    uint32_t b8[DT / 4];
+                    __builtin_memcpy(b8, &vt[i], DT);
+#pragma unroll
+                    for (int j = 0; j < DT / 4; ++j) {
+                        const u32x2 c2 = e4m3x4_to_bf16x4(b8[j]);
+                        w[i][2 * j] = c2[0];
+                        w[i][2 * j + 1] = c2[1];
+                    }
+                }
             }
             const int tok0 = (page0 + pi) * BS + 4 * grp;
-            float sc[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < len) ? acc[i] * sl2 : -INFINITY;
-
-            float v[4][DV];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                uint32_t w[VBYTES / 4];
-                __builtin_memcpy(w, &vr[r], VBYTES);
-                if constexpr (KV == ZK_BF16) {
-#pragma unroll
-                    for (int j = 0; j < DV / 2; ++j) {
-                        v[r][2 * j] = bf16lo(w[j]);
-                        v[r][2 * j + 1] = bf16hi(w[j]);
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < DV / 4; ++j) e4m3x4_to_f32(w[j], &v[r][4 * j]);
-                }
-            }
             if (tok0 + 4 > len) {  // partial last page: stale rows must not reach O
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (tok0 + r >= len)
+                for (int i = 0; i < 4; ++i)
+                    if (tok0 + i >= len)
 #pragma unroll
-                        for (int d = 0; d < DV; ++d) v[r][d] = 0.0f;
+                        for (int j = 0; j < DT / 2; ++j) w[i][j] = 0u;
             }
-
-            const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-            const float m_new = fmaxf(m_run, mx);
-            float alpha, pr[4];
-            if (m_new == -INFINITY) {
-                alpha = 1.0f;
+            s16x4 va[DT];  // element i of tile dt = V[4*grp+i][DT*col+dt]
 #pragma unroll
-                for (int i = 0; i < 4; ++i) pr[i] = 0.0f;
-            } else {
-                alpha = exp2_fast(m_run - m_new);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) pr[i] = exp2_fast(sc[i] - m_new);
+            for (int j = 0; j < DT / 2; ++j) {
+                const u32x2 lo{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x05040100u),
+                               __builtin_amdgcn_perm(w[3][j], w[2][j], 0x05040100u)};
+                const u32x2 hi{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x07060302u),
+                               __builtin_amdgcn_perm(w[3][j], w[2][j], 0x07060302u)};
+                va[2 * j] = __builtin_bit_cast(s16x4, lo);
+                va[2 * j + 1] = __builtin_bit_cast(s16x4, hi);
             }
-            l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-            m_run = m_new;
-            static_for<G>([&](auto hc) {
-                constexpr int h = decltype(hc)::value;
-                const float a_h = head_bcast<G, h>(alpha);
-                float ph[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ph[r] = head_bcast<G, h>(pr[r]);
+            for (int t = 0; t < T; ++t) {
+                float sc[4];
 #pragma unroll
-                for (int d = 0; d < DV; ++d) {
-                    float x = o[h][d] * a_h;
-                    x = fmaf(ph[0], v[0][d], x);
-                    x = fmaf(ph[1], v[1][d], x);
-                    x = fmaf(ph[2], v[2][d], x);
-                    x = fmaf(ph[3], v[3][d], x);
-                    o[h][d] = x;
+                for (int i = 0; i < 4; ++i) sc[i] = tok0 + i < len ? sacc[t][i] * sl2 : -INFINITY;
+                const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                // lazy rescale (wave-uniform branch): the new reference is the
+                // row max over the page's 16 tokens (all four lane groups)
+                if (__builtin_amdgcn_ballot_w64(mx > m[t] + kRescaleSlack)) {
+                    float cm = fmaxf(mx, xor16(mx));
+                    cm = fmaxf(cm, xor32(cm));
+                    const float m_new = fmaxf(m[t], cm);
+                    const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[t] - m_new);
+                    l[t] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o[dt][t] *= alpha;
+                    m[t] = m_new;
                 }
-            });
+                float pr[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pr[i] = exp2_fast(sc[i] - m[t]);
+                l[t] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+                const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{bf16x2_rne(pr[0], pr[1]), bf16x2_rne(pr[2], pr[3])});
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+                    o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt][t], 0, 0, 0);
+            }
         };
-
         for (int j = 0; j < kStages && j < np; ++j) issue(j, j);
         claim_next();
-        for (int pi = 0; pi < np; pi += kStages) {
-            static_for<kStages>([&](auto jc) {
-                constexpr int j = decltype(jc)::value;
-                if (pi + j < np) page(pi + j, j);
-            });
+        // one page per iteration (a single loop-carried accumulator set)
+        for (int pi = 0, st = 0; pi < np; ++pi, st = (st + 1 == kStages ? 0 : st + 1)) page(pi, st);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            l[t] += xor16(l[t]);
+            l[t] += xor32(l[t]);
         }
+    };
 
-        // merge the four 16-lane rows
-        float M = fmaxf(m_run, xor16(m_run));
-        M = fmaxf(M, xor32(M));
-        const float f = (m_run == -INFINITY) ? 0.0f : exp2_fast(m_run - M);
-        float lsum = l_run * f;
-        lsum += xor16(lsum);
-        lsum += xor32(lsum);
-        static_for<G>([&](auto hc) {
-            constexpr int h = decltype(hc)::value;
-            const float f_h = head_bcast<G, h>(f);
+    // Lane (grp, col) holds dims DT*(4*grp+i)+dt, i < 4, dt < DT, of row col:
+    // four runs of DT consecutive floats.
+    auto store_row_f32 = [&](float *dst, const f32x4 (&o)[DT][2], int t, float scale) {
 #pragma unroll
-            for (int d = 0; d < DV; ++d) {
-                float x = o[h][d] * f_h;
-                x += xor16(x);
-                x += xor32(x);
-                o[h][d] = x * vscale;
+        for (int i = 0; i < 4; ++i) {
+            float v[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) v[dt] = o[dt][t][i] * scale;
+            __builtin_memcpy(dst + DT * (4 * grp + i), v, sizeof(v));
+        }
+    };
+
+    const int total = p.work[0];
+    int item = blockIdx.x;  // first item static, the rest from the queue
+    while (item < total) {
+        const int kvh = item % Hkv;
+        const int4 desc = p.items[item / Hkv];
+        if (KV == ZK_BF16 && desc.x < 0) {
+            // shared-prefix partition of subgroup sg: up to 32 rows, member-major
+            const int sg = -1 - desc.x, part = desc.y, n0 = desc.z, np = desc.w;
+            const int32_t *mem = p.sg_members + (size_t)sg * kSgStride;
+            bf16x8 qf[2][KK];
+            int nm[2];  // member (batch index) of this lane's row in tile t, or -1
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int r = 16 * t + col;
+                nm[t] = mem[r / G];
+                if (nm[t] >= 0) load_q(nm[t], qhead_of(p, kvh, r % G, G), qf[t]);
+                else
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk) qf[t][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
             }
-        });
-        // lanes 0..15 hold o[h][col*DV + d]; lane h < G holds (M, lsum) of head h
-        if (ns == 0 && nparts <= 1) {
-            static_for<G>([&](auto hc) {
-                constexpr int h = decltype(hc)::value;
-                const float l_h = head_bcast<G, h>(lsum);
-                const float inv = l_h > 0.0f ? 1.0f / l_h : 0.0f;
-                if (grp == 0) {
-                    const size_t ob = ((size_t)n * H + qhead_of(p, kvh, h, G)) * D + (size_t)col * DV;
-                    if (p.q_f32) {
+            f32x4 o[DT][2];
+            float m[2], l[2];
+            attend.template operator()<2>(qf, p.bt + (size_t)n0 * p.max_blocks, part * p.shared_part_pages, np,
+                                          0x7fffffff, kvh, p.scale_log2, o, m, l);
 #pragma unroll
-                        for (int d = 0; d < DV; ++d) ((float *)p.out)[ob + d] = o[h][d] * inv;
+            for (int t = 0; t < 2; ++t) {
+                const int r = 16 * t + col;
+                if (nm[t] >= 0) {
+                    const size_t slot = ((size_t)nm[t] * H + qhead_of(p, kvh, r % G, G)) * p.max_parts + part;
+                    store_row_f32(p.po + slot * D, o, t, 1.0f);
+                    if (grp == 0) p.ml[slot] = make_float2(m[t], l[t]);
+                }
+            }
+        } else {
+            // a sequence's own partition: rows 0..G-1 are its heads of kv-head kvh
+            const int n = desc.x, part = desc.y, page0 = desc.z, np = desc.w;
+            const int len = p.eff_len[n];  // walk already cut at the first invalid entry
+            const int ns = shared_parts_of(p, n);  // partial slots before this sequence's own
+            const int nparts = private_parts_of(p, n);
+            const int qh = qhead_of(p, kvh, col % G, G);
+            bf16x8 qf[1][KK];
+            if (col < G) load_q(n, qh, qf[0]);
+            else
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) qf[0][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+            float sl2 = p.scale_log2, vscale = 1.0f;
+            if constexpr (KV == ZK_FP8_E4M3) {
+                sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
+                vscale = p.v_scales[(size_t)n * Hkv + kvh];
+            }
+            f32x4 o[DT][1];
+            float m[1], l[1];
+            attend.template operator()<1>(qf, p.bt + (size_t)n * p.max_blocks, page0, np, len, kvh, sl2, o, m, l);
+            if (col < G) {
+                if (ns == 0 && nparts <= 1) {  // the whole context: write the output row
+                    const float inv = l[0] > 0.0f ? vscale / l[0] : 0.0f;
+                    const size_t ob = ((size_t)n * H + qh) * D;
+                    if (p.q_f32) {
+                        f32x4 o2[DT][2];
+#pragma unroll
+                        for (int dt = 0; dt < DT; ++dt) o2[dt][0] = o[dt][0];
+                        store_row_f32((float *)p.out + ob, o2, 0, inv);
                     } else {
 #pragma unroll
-                        for (int d = 0; d < DV; ++d) ((uint16_t *)p.out)[ob + d] = (uint16_t)f32_to_bf16_bits(o[h][d] * inv);
-                    }
-                }
-            });
-        } else {
-            static_for<G>([&](auto hc) {
-                constexpr int h = decltype(hc)::value;
-                const size_t slot = ((size_t)n * H + qhead_of(p, kvh, h, G)) * p.max_parts + ns + part;
-                if (grp == 0) {
-                    float *dst = p.po + slot * D + (size_t)col * DV;
+                        for (int i = 0; i < 4; ++i) {
+                            uint32_t v[DT / 2];
 #pragma unroll
-                    for (int d = 0; d < DV; ++d) dst[d] = o[h][d];
+                            for (int j = 0; j < DT / 2; ++j)
+                                v[j] = bf16x2_rne(o[2 * j][0][i] * inv, o[2 * j + 1][0][i] * inv);
+                            __builtin_memcpy((uint16_t *)p.out + ob + DT * (4 * grp + i), v, sizeof(v));
+                        }
+                    }
+                } else {
+                    const size_t slot = ((size_t)n * H + qh) * p.max_parts + ns + part;
+                    f32x4 o2[DT][2];
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o2[dt][0] = o[dt][0];
+                    store_row_f32(p.po + slot * D, o2, 0, vscale);
+                    if (grp == 0) p.ml[slot] = make_float2(m[0], l[0]);
                 }
-                if (lane == h) p.ml[slot] = make_float2(M, lsum);
-            });
+            }
         }
         item = __builtin_amdgcn_readfirstlane(next);
     }
