@@ -5,19 +5,21 @@
 // with one serial thread per workgroup).  The context of every (sequence,
 // kv-head) is cut into partitions of `part_pages` pages; one wavefront owns
 // one partition of one kv-head and serves all G = H/Hkv query heads that share
-// it, so every K/V byte is read from HBM exactly once.  Partials (running max
-// m, sum l, unnormalised o) of sequences with more than one partition are
-// merged by a log-sum-exp reduce kernel.
+// it, so every K/V byte is read from HBM exactly once.  Sequences forked from
+// one prefix (the KV cache passes their subgroups) read the shared pages once
+// per subgroup as well.  Partials (running max m, sum l, unnormalised o) of
+// sequences with more than one partition are merged by a log-sum-exp reduce.
 //
 // Kernels
 //   seq_info_kernel   effective length: the page walk stops at the first table
 //                     entry that is < 0 or >= num_blocks (paged_attention.cu:66-67)
-//   plan_kernel       prefix sums of partitions -> work items; resets the queue
+//   plan_kernel       partitions -> work-item descriptors, longest first;
+//                     resets the queue
 //   decode_mfma_kernel  bf16 / fp8 pools, D in {64,128}, G in {1,2,4,8}:
-//       persistent one-wave workgroups pull (sequence, partition, kv-head)
-//       items from an atomic queue (no tail of short waves), stream each page
-//       through LDS with global_load_lds, and run QK^T on MFMA, softmax and PV
-//       on the VALU with DPP broadcasts (details at the kernel).
+//       persistent one-wave workgroups take (sequence or subgroup, partition,
+//       kv-head) items from an atomic queue (no tail of short waves), stream
+//       each page through LDS with global_load_lds, and run QK^T and PV on
+//       MFMA with a lazily rescaled softmax (details at the kernel).
 //   decode_generic_kernel  any dtype / D <= 256 / G <= 16 (fp32 pools):
 //       one wavefront per (partition, kv-head, sequence); token-per-lane QK on
 //       the VALU, readlane-broadcast PV.
@@ -160,30 +162,6 @@ __global__ void __launch_bounds__(kWave) seq_info_kernel(Params p) {
 }
 
 // ------------------------------------------------------------ helpers
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-    [&]<int... I>(std::integer_sequence<int, I...>) {
-        (f(std::integral_constant<int, I>{}), ...);
-    }(std::make_integer_sequence<int, N>{});
-}
-
-// Value of head H's lane inside this lane's G-lane group of its 16-lane row.
-template <int G, int H>
-__device__ __forceinline__ float head_bcast(float v) {
-    if constexpr (G == 1) {
-        return v;
-    } else if constexpr (G == 2) {
-        constexpr int ctl = H == 0 ? 0xA0 : 0xF5;  // quad_perm [H,H,2+H,2+H]
-        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctl, 0xF, 0xF, false));
-    } else if constexpr (G == 4) {
-        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), H * 0x55, 0xF, 0xF, false));
-    } else {
-        static_assert(G == 8, "G must be 1, 2, 4 or 8");
-        // ds_swizzle bit mode inside 32-lane halves: src = (lane & 0x18) | H
-        return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (H << 5)));
-    }
-}
-
 __device__ __forceinline__ float xor16(float v) {
     // ds_swizzle bit mode: src = lane ^ 16 within 32-lane halves
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (0x10 << 10)));
