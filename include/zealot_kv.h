@@ -225,6 +225,30 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
  * pages they shared (sum over subgroups).  No reference counterpart. */
 int zk_cache_decode_sharing(zk_kv_cache *c, int *subgroups, int64_t *shared_pages);
 
+/* ================================================== chunked-prefill attention
+ * Replaces CudaAttention::forward_gpu (attention/cuda.rs:56-110, the tiled
+ * first-chunk kernel attention.cu:9-187) and the later-chunk paged_forward
+ * call of cuda_runner.rs:443-461, which computes only the chunk's first row.
+ * Sequence n's chunk has q rows cu_seqlens_q[n] .. cu_seqlens_q[n+1] (device,
+ * int64; total_q == cu_seqlens_q[num_seqs]) at absolute positions
+ * start_pos[n] + t (device, int32); its K/V are already in the pages (append
+ * first).  causal != 0: row t attends to positions [0, start + t]
+ * (attention.cu:117-121); causal == 0: to [0, start + len)
+ * (CpuAttention::forward, attention/mod.rs:64-98).  q, out: [total_q, H, D],
+ * f32 or bf16 (out has q's dtype).  The page walk stops at the first table
+ * entry < 0 or >= num_blocks, as in zk_paged_decode.  Shapes: bf16 or fp8
+ * pools, block_size 16, head_dim 64 or 128, H/Hkv in {1, 2, 4, 8},
+ * max_blocks_per_seq <= 2048.  workspace: caller-owned, 256-B aligned, at
+ * least zk_paged_prefill_workspace_size bytes.  Asynchronous on `stream`. */
+size_t zk_paged_prefill_workspace_size(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads);
+int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool,
+                     zk_dtype kv_dtype, void *out, const int32_t *block_tables,
+                     const int64_t *cu_seqlens_q, const int32_t *start_pos, int num_seqs,
+                     int64_t total_q, int num_heads, int num_kv_heads, int head_dim, int block_size,
+                     int max_blocks_per_seq, int64_t num_blocks, float scale, int causal,
+                     zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
+                     void *workspace, size_t workspace_bytes, void *stream);
+
 /* ======================================================= measurement
  * No reference counterpart (the reference's attention bench is a stub,
  * cuda_runner.rs:151-157).  When timing is on, every kernel this library
@@ -232,7 +256,8 @@ int zk_cache_decode_sharing(zk_kv_cache *c, int *subgroups, int64_t *shared_page
  * synchronises on the recorded events and returns the launch count and total
  * milliseconds of one kernel name since the last reset.  Kernel names:
  * "append", "fp8_scales", "gather", "copy_blocks", "decode_seq_info",
- * "decode_plan", "decode_partials", "decode_reduce", "stream_copy". */
+ * "decode_plan", "decode_partials", "decode_reduce", "prefill_plan",
+ * "prefill_attention", "stream_copy". */
 int zk_timing_enable(int on);
 int zk_timing_reset(void);
 int zk_timing_query(const char *kernel, int64_t *launches, double *total_ms);

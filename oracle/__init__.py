@@ -19,6 +19,11 @@ Parity status of each restated function (how it is pinned, see tests/):
       independent library routine), closed forms (ctx=1, constant K, dominant
       score, shift invariance) and both GQA mappings against
       or_repeat_interleave_kv + or_cpu_attention -- tests/test_oracle.py.
+  or_paged_prefill
+      pinned against or_paged_decode (a one-row chunk at position p is the
+      decode of p + 1 tokens), or_cpu_attention (a non-causal chunk from
+      position 0 is CpuAttention::forward on the gathered K/V) and torch's
+      causal scaled_dot_product_attention in float64 -- tests/test_oracle.py.
   or_cpu_attention / or_matmul / or_repeat_interleave_kv
       pinned by the reference's own unit tests (attention/mod.rs:121-189,
       model_runner_cpu.rs:153-195) restated as golden fixtures.
@@ -92,6 +97,9 @@ def _declare(L):
     L.or_paged_decode.restype = _I
     L.or_paged_decode.argtypes = [_P, _P, _P, _I, _P, _P, _P, _I64, _P, _I, _I, _I, _I, _I, _F,
                                   _I, _P, _I]
+    L.or_paged_prefill.restype = _I
+    L.or_paged_prefill.argtypes = [_P, _P, _P, _I, _P, _P, _P, _I64, _P, _P, _I, _I, _I, _I, _I, _F,
+                                   _I, _I, _P, _I]
     L.or_cpu_attention.restype = _I
     L.or_cpu_attention.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P]
     L.or_matmul.restype = None
@@ -198,6 +206,26 @@ def paged_decode(q, k_pool, v_pool, kv_dtype, block_tables, seq_lens, num_kv_hea
                                block_size, scale, mapping, _ptr(out), threads)
     if rc != 0:
         raise RuntimeError(f"or_paged_decode failed: {rc}")
+    return out
+
+
+def paged_prefill(q, k_pool, v_pool, kv_dtype, block_tables, cu_seqlens_q, start_pos, num_kv_heads,
+                  head_dim, block_size, scale, causal=True, mapping=GROUPED, k_scales=None, v_scales=None,
+                  threads=1):
+    """q [T, H, D] (f32 values) -> out [T, H, D] f32; see or_paged_prefill."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    t, h = q.shape[0], q.shape[1]
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    cu = np.ascontiguousarray(cu_seqlens_q, dtype=np.int64)
+    st = np.ascontiguousarray(start_pos, dtype=np.int32)
+    ks = None if k_scales is None else np.ascontiguousarray(k_scales, dtype=np.float32)
+    vs = None if v_scales is None else np.ascontiguousarray(v_scales, dtype=np.float32)
+    out = np.zeros((t, h, head_dim), dtype=np.float32)
+    rc = lib().or_paged_prefill(_ptr(q), _ptr(k_pool), _ptr(v_pool), kv_dtype, _ptr(ks), _ptr(vs),
+                                _ptr(bt), bt.shape[1], _ptr(cu), _ptr(st), len(st), h, num_kv_heads, head_dim,
+                                block_size, scale, mapping, int(bool(causal)), _ptr(out), threads)
+    if rc != 0:
+        raise RuntimeError(f"or_paged_prefill failed: {rc}")
     return out
 
 

@@ -283,6 +283,63 @@ int or_paged_decode(const float *q, const void *k_pool, const void *v_pool, int 
     return err;
 }
 
+/* Chunked-prefill attention over pages: sequence n's chunk has query rows
+ * cu_seqlens_q[n] .. cu_seqlens_q[n+1]; chunk row t sits at absolute position
+ * start_pos[n] + t, and the chunk's own K/V are already in the pages.  Causal:
+ * row t attends to positions [0, start + t] -- the per-element mask of
+ * attention.cu:117-121 (k_pos > q_pos is excluded) carried over to a chunk
+ * after `start` cached tokens.  Non-causal: every row attends to
+ * [0, start + len), like CpuAttention::forward (attention/mod.rs:64-98).  Each
+ * row is the decode row above with that many context tokens. */
+int or_paged_prefill(const float *q, const void *k_pool, const void *v_pool, int kv_dtype,
+                     const float *k_scales, const float *v_scales, const int32_t *block_tables,
+                     int64_t max_blocks, const int64_t *cu_seqlens_q, const int32_t *start_pos, int num_seqs,
+                     int num_heads, int num_kv_heads, int head_dim, int block_size, float scale, int mapping,
+                     int causal, float *out, int threads) {
+    if (num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return -1;
+    int64_t max_ctx = 0;
+    for (int n = 0; n < num_seqs; ++n) {
+        int64_t c = start_pos[n] + (cu_seqlens_q[n + 1] - cu_seqlens_q[n]);
+        if (c > max_ctx) max_ctx = c;
+    }
+    int group = num_heads / num_kv_heads;
+    int64_t rows = cu_seqlens_q[num_seqs] * num_heads;
+    int err = 0;
+#ifdef _OPENMP
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+#endif
+    {
+        float *scores = (float *)malloc(sizeof(float) * (size_t)(max_ctx + 1));
+        float *vbuf = (float *)malloc(sizeof(float) * (size_t)(max_ctx + 1) * head_dim);
+        if (!scores || !vbuf) {
+            err = -2;
+        } else {
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 4)
+#endif
+            for (int64_t r = 0; r < rows; ++r) {
+                int64_t tok = r / num_heads;
+                int h = (int)(r % num_heads);
+                int n = 0;
+                while (cu_seqlens_q[n + 1] <= tok) ++n;
+                int64_t t = tok - cu_seqlens_q[n];
+                int64_t len = cu_seqlens_q[n + 1] - cu_seqlens_q[n];
+                int64_t ctx = causal ? start_pos[n] + t + 1 : start_pos[n] + len;
+                int kvh = mapping == OR_GQA_GROUPED ? h / group : h % num_kv_heads;
+                float ks = k_scales ? k_scales[(int64_t)n * num_kv_heads + kvh] : 1.0f;
+                float vs = v_scales ? v_scales[(int64_t)n * num_kv_heads + kvh] : 1.0f;
+                decode_row(q + r * head_dim, k_pool, v_pool, kv_dtype, ks, vs,
+                           block_tables + (int64_t)n * max_blocks, max_blocks, ctx, kvh, num_kv_heads, head_dim,
+                           block_size, scale, out + r * head_dim, scores, vbuf);
+            }
+        }
+        free(scores);
+        free(vbuf);
+    }
+    (void)threads;
+    return err;
+}
+
 /* --------------------------------------------------- dense CPU attention */
 
 int or_cpu_attention(const float *query, const float *key, const float *value, int num_seqs,

@@ -63,6 +63,16 @@ int or_paged_decode(const float *q, const void *k_pool, const void *v_pool, int 
                     int num_kv_heads, int head_dim, int block_size, float scale, int mapping,
                     float *out, int threads);
 
+/* Chunked-prefill attention: row t of sequence n's chunk (q rows
+ * cu_seqlens_q[n] .. cu_seqlens_q[n+1], q/out [T, H, D] f32) sits at position
+ * start_pos[n] + t and sees positions [0, start + t] (causal) or
+ * [0, start + len) (not causal). */
+int or_paged_prefill(const float *q, const void *k_pool, const void *v_pool, int kv_dtype,
+                     const float *k_scales, const float *v_scales, const int32_t *block_tables,
+                     int64_t max_blocks, const int64_t *cu_seqlens_q, const int32_t *start_pos, int num_seqs,
+                     int num_heads, int num_kv_heads, int head_dim, int block_size, float scale, int mapping,
+                     int causal, float *out, int threads);
+
 /* Dense CPU attention, src/attention/mod.rs:31-103 verbatim semantics:
  * q, k, v, out are [S, H, n_pos, D] f32; non-causal softmax(QK^T*scale)V. */
 int or_cpu_attention(const float *q, const float *k, const float *v, int num_seqs, int num_heads,

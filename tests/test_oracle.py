@@ -336,3 +336,83 @@ def test_fp8_scales_and_quantised_append():
         assert np.all(err <= np.abs(x[t]) * 2 ** -4 + sc[row[t]][:, None] * 2 ** -10 + 1e-12)
         # the amax element maps to exactly +-448
     assert np.any(np.abs(deq) == 448.0)
+
+
+# ------------------------------------------------------------ chunked prefill
+
+def _prefill_case(rng, H, Hkv, D, BS, starts, chunks):
+    """Pages holding each sequence's start + chunk tokens; q for the chunk rows."""
+    lens = [s + c for s, c in zip(starts, chunks)]
+    _, kp, vp, bt = _paged_case(rng, len(lens), H, Hkv, D, BS, lens)
+    cu = np.concatenate([[0], np.cumsum(chunks)]).astype(np.int64)
+    q = rng.standard_normal((int(cu[-1]), H, D)).astype(np.float32)
+    return q, kp, vp, bt, cu, lens
+
+
+@pytest.mark.parametrize("mapping", [oracle.GROUPED, oracle.MODULO])
+@pytest.mark.parametrize("H,Hkv,D", [(4, 4, 32), (8, 2, 16), (32, 8, 64)])
+def test_prefill_causal_matches_torch_sdpa_float64(mapping, H, Hkv, D):
+    """Row t of a chunk after `start` cached tokens sees positions [0, start + t]:
+    torch SDPA in float64 with that explicit mask (an independent routine)."""
+    rng = np.random.default_rng(60 + H + D)
+    BS = 16
+    starts, chunks = [0, 5, 16, 33, 100], [7, 1, 16, 40, 19]
+    q, kp, vp, bt, cu, lens = _prefill_case(rng, H, Hkv, D, BS, starts, chunks)
+    scale = np.float32(1.0 / math.sqrt(D))
+    out = oracle.paged_prefill(q, kp, vp, oracle.F32, bt, cu, starts, Hkv, D, BS, scale, True, mapping)
+    heads = np.arange(H)
+    kvh = heads // (H // Hkv) if mapping == oracle.GROUPED else heads % Hkv
+    for n, (s, c) in enumerate(zip(starts, chunks)):
+        L = s + c
+        K = torch.from_numpy(_dense(kp, bt[n], L, BS)).double()[:, kvh, :].permute(1, 0, 2)  # [H, L, D]
+        V = torch.from_numpy(_dense(vp, bt[n], L, BS)).double()[:, kvh, :].permute(1, 0, 2)
+        Q = torch.from_numpy(q[cu[n]:cu[n + 1]]).double().permute(1, 0, 2)  # [H, c, D]
+        mask = torch.arange(L)[None, :] <= (s + torch.arange(c))[:, None]  # [c, L]
+        o = torch.nn.functional.scaled_dot_product_attention(Q, K, V, attn_mask=mask, scale=float(scale))
+        assert np.max(np.abs(out[cu[n]:cu[n + 1]] - o.permute(1, 0, 2).numpy())) < 2e-6, n
+
+
+def test_prefill_rows_are_decodes():
+    """A one-row chunk at position p is the decode of p + 1 tokens; a causal
+    chunk's row t equals the decode of start + t + 1 tokens."""
+    rng = np.random.default_rng(61)
+    H, Hkv, D, BS = 8, 2, 32, 16
+    starts, chunks = [0, 9, 31, 64], [1, 12, 1, 20]
+    q, kp, vp, bt, cu, lens = _prefill_case(rng, H, Hkv, D, BS, starts, chunks)
+    scale = np.float32(0.125)
+    out = oracle.paged_prefill(q, kp, vp, oracle.F32, bt, cu, starts, Hkv, D, BS, scale, True)
+    for n, (s, c) in enumerate(zip(starts, chunks)):
+        for t in range(c):
+            dec = oracle.paged_decode(q[cu[n] + t][None], kp, vp, oracle.F32, bt[n:n + 1], [s + t + 1],
+                                      Hkv, D, BS, scale)
+            assert np.array_equal(out[cu[n] + t], dec[0]), (n, t)
+
+
+def test_prefill_noncausal_first_chunk_is_reference_cpu_attention():
+    """Not causal, start 0: every row sees the whole chunk -- CpuAttention::forward
+    (attention/mod.rs:64-98) on the gathered K/V, MHA."""
+    rng = np.random.default_rng(62)
+    H, D, BS, L = 4, 16, 16, 37
+    q, kp, vp, bt, cu, lens = _prefill_case(rng, H, H, D, BS, [0], [L])
+    out = oracle.paged_prefill(q, kp, vp, oracle.F32, bt, cu, [0], H, D, BS, np.float32(1 / math.sqrt(D)), False)
+    K = np.ascontiguousarray(_dense(kp, bt[0], L, BS).transpose(1, 0, 2))  # [H, L, D]
+    V = np.ascontiguousarray(_dense(vp, bt[0], L, BS).transpose(1, 0, 2))
+    Q = np.ascontiguousarray(q.transpose(1, 0, 2))
+    dense = oracle.cpu_attention(Q, K, V, 1, H, D, L).reshape(H, L, D).transpose(1, 0, 2)
+    assert np.max(np.abs(out - dense)) < 1e-6
+
+
+def test_prefill_closed_forms():
+    """Causal row 0 of a first chunk is v_0; a chunk row after cached tokens with
+    constant K is the mean of V over its visible positions."""
+    rng = np.random.default_rng(63)
+    H, Hkv, D, BS = 2, 1, 8, 16
+    q, kp, vp, bt, cu, lens = _prefill_case(rng, H, Hkv, D, BS, [0, 10], [5, 6])
+    kp[:] = 0.5  # constant K: uniform weights
+    out = oracle.paged_prefill(q, kp, vp, oracle.F32, bt, cu, [0, 10], Hkv, D, BS, np.float32(0.3), True)
+    V0 = _dense(vp, bt[0], 5, BS)
+    V1 = _dense(vp, bt[1], 16, BS)
+    for h in range(H):
+        assert np.allclose(out[0, h], V0[0, 0], atol=1e-6)
+        for t in range(6):
+            assert np.allclose(out[5 + t, h], V1[: 10 + t + 1, 0].mean(axis=0), atol=1e-5)

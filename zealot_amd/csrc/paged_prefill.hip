@@ -1,0 +1,555 @@
+// paged_prefill.hip -- chunked-prefill attention over paged K/V for gfx950.
+//
+// A prompt chunk of C tokens of sequence n, whose K/V are already in the
+// pages behind start_pos[n] cached tokens, attends to its context: chunk row t
+// (absolute position start + t) sees positions [0, start + t] when causal --
+// the per-element mask of src/attention/kernels/attention.cu:117-121, there
+// applied to a first chunk held outside the pages -- or [0, start + C) when
+// not (CpuAttention::forward, src/attention/mod.rs:64-98).  This replaces the
+// reference's first-chunk tiled kernel (attention/cuda.rs:56-110) and its later
+// chunks, for which cuda_runner.rs:443-461 runs the one-query decode kernel.
+//
+// Kernels
+//   prefill_plan_kernel  one workgroup: effective context per sequence (the
+//       page walk stops at the first table entry < 0 or >= num_blocks, as in
+//       the decode), then work items (sequence, query tile, kv-head) listed
+//       longest first (counting sort on the pages a tile reads).
+//   prefill_mfma_kernel<KV, D, G>  bf16 / fp8 pools, D in {64, 128}, G in
+//       {1, 2, 4, 8}, block_size 16: persistent one-wave workgroups take items
+//       from an atomic queue.  An item holds 64 query rows -- TQ = 64/G chunk
+//       tokens x the G heads of one kv-head, token-major -- as four 16-column
+//       MFMA tiles, so each K/V page read serves all 64 rows.  Pages stream
+//       through LDS as in the decode (global_load_lds, two stages); QK^T and PV
+//       run on MFMA with a lazily rescaled softmax (see paged_decode.hip);
+//       every column carries its own visibility limit.
+// Rows write their outputs directly (no split over keys): an item reads the
+// pages up to its last row's limit, so the causal triangle costs half.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+#include "zk_common.h"
+
+using namespace zk;
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWave = 64;
+constexpr int kRows = 64;            // query rows per item (4 MFMA tiles)
+constexpr int kTiles = kRows / 16;
+constexpr int kMaxBins = 2048;       // page-count bins of the longest-first sort
+constexpr float kRescaleSlack = 8.0f;  // lazy-rescale slack, log2 units
+
+struct PParams {
+    const void *q;        // [T, H, D]
+    const char *k_pool;
+    const char *v_pool;
+    void *out;            // [T, H, D], dtype of q
+    const int32_t *bt;    // [N, max_blocks]
+    const int64_t *cu_q;  // [N + 1] chunk rows per sequence
+    const int32_t *start; // [N] cached tokens before each chunk
+    const float *k_scales;
+    const float *v_scales;
+    int32_t *eff;         // [N] context after the page walk
+    int4 *items;          // {n, query tile, pages, 0}, longest first
+    int32_t *work;        // [2] total items, queue head
+    int num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks, tq, num_waves, max_items;
+    int64_t num_blocks;
+    float scale_log2;
+    int grouped, q_f32, causal;
+};
+
+__device__ __forceinline__ int qhead_of(const PParams &p, int kvh, int j, int G) {
+    return p.grouped ? kvh * G + j : kvh + j * p.num_kv_heads;
+}
+
+// Pages a query tile reads: up to its last row's visibility limit.
+__device__ __forceinline__ int tile_pages(const PParams &p, int n, int qt) {
+    const int len = (int)(p.cu_q[n + 1] - p.cu_q[n]);
+    const int last = min(len, (qt + 1) * p.tq);  // rows of the tile end here
+    const int lim = p.causal ? p.start[n] + last : p.start[n] + len;
+    const int vis = min(lim, p.eff[n]);
+    return (vis + p.block_size - 1) / p.block_size;
+}
+
+__global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
+    __shared__ int hist[kMaxBins];
+    __shared__ int sums[1024];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    hist[2 * t] = 0;
+    hist[2 * t + 1] = 0;
+    // effective contexts: one wave per sequence, eight loads in flight per lane
+    for (int n = wave; n < p.num_seqs; n += 16) {
+        const int want = p.start[n] + (int)(p.cu_q[n + 1] - p.cu_q[n]);
+        const int cap = p.max_blocks * p.block_size;
+        const int len = max(0, min(want, cap));
+        const int pages = (len + p.block_size - 1) / p.block_size;
+        const int32_t *row = p.bt + (size_t)n * p.max_blocks;
+        int first_bad = pages;
+        for (int i0 = 0; i0 < pages && first_bad == pages; i0 += 8 * kWave) {
+            int32_t b[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave + lane;
+                b[j] = i < pages ? row[i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave + lane;
+                if (i < pages && (b[j] < 0 || (int64_t)b[j] >= p.num_blocks)) first_bad = min(first_bad, i);
+            }
+            for (int o = 32; o > 0; o >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, o));
+        }
+        if (lane == 0) p.eff[n] = min(len, first_bad * p.block_size);
+    }
+    __threadfence_block();
+    __syncthreads();
+    auto bin = [&](int pages) { return kMaxBins - 1 - min(pages, kMaxBins - 1); };  // longest first
+    for (int n = t; n < p.num_seqs; n += 1024) {
+        const int tiles = (int)((p.cu_q[n + 1] - p.cu_q[n] + p.tq - 1) / p.tq);
+        for (int qt = 0; qt < tiles; ++qt) atomicAdd(&hist[bin(tile_pages(p, n, qt))], 1);
+    }
+    __syncthreads();
+    const int a = hist[2 * t], b = hist[2 * t + 1];
+    sums[t] = a + b;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+        const int v = t >= o ? sums[t - o] : 0;
+        __syncthreads();
+        sums[t] += v;
+        __syncthreads();
+    }
+    const int base = sums[t] - (a + b);
+    __syncthreads();
+    hist[2 * t] = base;
+    hist[2 * t + 1] = base + a;
+    const int total = sums[1023];
+    __syncthreads();
+    for (int n = t; n < p.num_seqs; n += 1024) {
+        const int tiles = (int)((p.cu_q[n + 1] - p.cu_q[n] + p.tq - 1) / p.tq);
+        for (int qt = 0; qt < tiles; ++qt) {
+            const int pages = tile_pages(p, n, qt);
+            const int pos = atomicAdd(&hist[bin(pages)], 1);
+            if (pos < p.max_items) p.items[pos] = make_int4(n, qt, pages, 0);
+        }
+    }
+    if (t == 0) {
+        p.work[0] = min(total, p.max_items) * p.num_kv_heads;  // total items
+        p.work[1] = p.num_waves;                                // items below are taken statically
+    }
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kCachePolicyNT = 2;  // every K/V byte of a tile is streamed once
+__device__ __forceinline__ void g2l16(const void *g, lds_void *l) {
+    __builtin_amdgcn_global_load_lds(g, l, 16, 0, kCachePolicyNT);
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+__device__ __forceinline__ float xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (0x10 << 10)));
+}
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2_t));
+}
+template <int BYTES>
+struct LdsVec;
+template <>
+struct LdsVec<16> { typedef u32x4 T; };
+template <>
+struct LdsVec<8> { typedef u32x2 T; };
+template <>
+struct LdsVec<4> { typedef uint32_t T; };
+
+template <int KV, int D, int G>
+__global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
+    constexpr int BS = 16;
+    constexpr int ELT = KV == ZK_BF16 ? 2 : 1;
+    constexpr int DG = D / 4;         // head dims per lane group in QK
+    constexpr int KK = DG / 8;        // MFMA k-steps
+    constexpr int DT = D / 16;        // PV dim tiles = dims per lane per V row
+    constexpr int RB = D * ELT;       // bytes per token row
+    constexpr int CPR = RB / 16;      // 16-byte chunks per row
+    constexpr int PAGE = BS * RB;     // bytes per (block, kv-head) page
+    constexpr int LPK = PAGE / 1024;  // global_load_lds per page of K (or V)
+    constexpr int LPP = 2 * LPK;
+    constexpr int KBYTES = DG * ELT;
+    constexpr int KCH = KBYTES / 16;
+    constexpr int VTB = DT * ELT;
+    constexpr int T = kTiles;
+    static_assert(PAGE % 1024 == 0 && KBYTES % 16 == 0 && DT % 2 == 0, "page shape");
+    typedef typename LdsVec<VTB>::T vtrow_t;
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) char lds[2][2][PAGE];
+    __shared__ int32_t bids[kMaxBins];
+
+    const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+    const int H = p.num_heads, Hkv = p.num_kv_heads;
+    uint32_t kg[LPK], vg[LPK];
+#pragma unroll
+    for (int j = 0; j < LPK; ++j) {
+        const int q = 64 * j + lane, row = q / CPR, c = (q % CPR) ^ (row % CPR);
+        kg[j] = row * RB + c * 16;
+        vg[j] = q * 16;
+    }
+    uint32_t kl[KCH];
+#pragma unroll
+    for (int f = 0; f < KCH; ++f) {
+        const int row = col, c = grp * KCH + f;
+        kl[f] = (row * CPR + (c ^ (row % CPR))) * 16;
+    }
+    const uint32_t vt_off = (uint32_t)((4 * grp) * RB + col * VTB);
+
+    const int total = p.work[0];
+    int item = blockIdx.x;  // first item static, the rest from the queue
+    int next = 0;
+    while (item < total) {
+        const int kvh = item % Hkv;
+        const int4 desc = p.items[item / Hkv];
+        const int n = desc.x, qt = desc.y, np = desc.z;
+        const int len = (int)(p.cu_q[n + 1] - p.cu_q[n]), st = p.start[n], eff = p.eff[n];
+        const int64_t row0 = p.cu_q[n] + (int64_t)qt * p.tq;  // first q row of the tile
+
+        // rows: column col of tile t is row r = 16 t + col = token r / G, head r % G
+        bf16x8 qf[T][KK];
+        int lim[T];       // keys at positions < lim[t] are visible to this lane's row
+        bool real[T];     // the row is a chunk token (not padding past the chunk)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int r = 16 * t + col, tok = qt * p.tq + r / G;
+            real[t] = tok < len;
+            const int tok_c = min(tok, len - 1);  // padding rows see what the last row sees
+            lim[t] = min(p.causal ? st + tok_c + 1 : st + len, eff);
+            if (real[t]) {
+                const size_t qb = ((size_t)(row0 + r / G) * H + qhead_of(p, kvh, r % G, G)) * D + (size_t)grp * DG;
+                if (p.q_f32) {
+                    const float *qq = (const float *)p.q + qb;
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk) {
+                        u32x4 w;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(qq[8 * kk + 2 * j], qq[8 * kk + 2 * j + 1]);
+                        qf[t][kk] = __builtin_bit_cast(bf16x8, w);
+                    }
+                } else {
+                    const uint16_t *qq = (const uint16_t *)p.q + qb;
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk) qf[t][kk] = *reinterpret_cast<const bf16x8 *>(qq + 8 * kk);
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) qf[t][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+            }
+        }
+        float sl2 = p.scale_log2, vscale = 1.0f;
+        if constexpr (KV == ZK_FP8_E4M3) {
+            sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
+            vscale = p.v_scales[(size_t)n * Hkv + kvh];
+        }
+        // block ids of the tile's pages into LDS (the LDS writes wait for
+        // their loads, retiring the Q loads too)
+        const int32_t *trow = p.bt + (size_t)n * p.max_blocks;
+        for (int i0 = 0; i0 < np; i0 += 8 * kWave) {
+            int32_t b[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave + lane;
+                b[j] = i < np ? trow[i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave + lane;
+                if (i < np) bids[i] = b[j];
+            }
+        }
+        wait_lgkmcnt0();
+        const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
+        const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
+        const size_t block_bytes = (size_t)PAGE * Hkv;
+        auto issue = [&](int pi, int s) {
+            const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
+            const char *kp = kbase + (size_t)blk * block_bytes;
+            const char *vp = vbase + (size_t)blk * block_bytes;
+#pragma unroll
+            for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[s][0] + 1024 * j));
+#pragma unroll
+            for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[s][1] + 1024 * j));
+        };
+        f32x4 o[DT][T];
+        float m[T], l[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            m[t] = -INFINITY;
+            l[t] = 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        auto page = [&](int pi, int s) {
+            if (pi + 1 < np) wait_vmcnt<LPP>();
+            else wait_vmcnt<0>();
+            uint32_t kw[KBYTES / 4];
+#pragma unroll
+            for (int f = 0; f < KCH; ++f) {
+                const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[s][0] + kl[f]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kw[4 * f + j] = c4[j];
+            }
+            vtrow_t vt[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vt[i] = *reinterpret_cast<const vtrow_t *>(lds[s][1] + vt_off + i * RB);
+            wait_lgkmcnt0();
+            if (pi + 2 < np) issue(pi + 2, s);
+
+            f32x4 sacc[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                u32x4 w;
+                if constexpr (KV == ZK_BF16) {
+                    w = u32x4{kw[4 * kk], kw[4 * kk + 1], kw[4 * kk + 2], kw[4 * kk + 3]};
+                } else {
+                    const u32x2 lo2 = e4m3x4_to_bf16x4(kw[2 * kk]), hi2 = e4m3x4_to_bf16x4(kw[2 * kk + 1]);
+                    w = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+                }
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), qf[t][kk],
+                                                                      sacc[t], 0, 0, 0);
+            }
+            uint32_t w[4][DT / 2];  // V rows as bf16 pairs
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (KV == ZK_BF16) {
+                    __builtin_memcpy(w[i], &vt[i], 2 * DT);
+                } else {
+                    uint32_t b8[DT / 4];
+                    __builtin_memcpy(b8, &vt[i], DT);
+#pragma unroll
+                    for (int j = 0; j < DT / 4; ++j) {
+                        const u32x2 c2 = e4m3x4_to_bf16x4(b8[j]);
+                        w[i][2 * j] = c2[0];
+                        w[i][2 * j + 1] = c2[1];
+                    }
+                }
+            }
+            const int key0 = pi * BS + 4 * grp;  // position of this lane's first key
+            if (key0 + 4 > eff) {  // past the context: stale rows must not reach O
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (key0 + i >= eff)
+#pragma unroll
+                        for (int j = 0; j < DT / 2; ++j) w[i][j] = 0u;
+            }
+            s16x4 va[DT];
+#pragma unroll
+            for (int j = 0; j < DT / 2; ++j) {
+                const u32x2 lo{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x05040100u),
+                               __builtin_amdgcn_perm(w[3][j], w[2][j], 0x05040100u)};
+                const u32x2 hi{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x07060302u),
+                               __builtin_amdgcn_perm(w[3][j], w[2][j], 0x07060302u)};
+                va[2 * j] = __builtin_bit_cast(s16x4, lo);
+                va[2 * j + 1] = __builtin_bit_cast(s16x4, hi);
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float sc[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sc[i] = key0 + i < lim[t] ? sacc[t][i] * sl2 : -INFINITY;
+                const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                if (__builtin_amdgcn_ballot_w64(mx > m[t] + kRescaleSlack)) {
+                    float cm = fmaxf(mx, xor16(mx));
+                    cm = fmaxf(cm, xor32(cm));
+                    const float m_new = fmaxf(m[t], cm);
+                    const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[t] - m_new);
+                    l[t] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o[dt][t] *= alpha;
+                    m[t] = m_new;
+                }
+                float pr[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pr[i] = sc[i] == -INFINITY ? 0.0f : exp2_fast(sc[i] - m[t]);
+                l[t] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+                const s16x4 pb =
+                    __builtin_bit_cast(s16x4, u32x2{bf16x2_rne(pr[0], pr[1]), bf16x2_rne(pr[2], pr[3])});
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+                    o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt][t], 0, 0, 0);
+            }
+        };
+        if (np > 0) issue(0, 0);
+        if (lane == 0) next = atomicAdd(&p.work[1], 1);  // overlaps the first page's round trip
+        if (np > 1) issue(1, 1);
+        for (int pi = 0, s = 0; pi < np; ++pi, s ^= 1) page(pi, s);
+
+        // rows of this lane: dims DT*(4*grp+i)+dt of row 16 t + col
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float lt = l[t];
+            lt += xor16(lt);
+            lt += xor32(lt);
+            if (!real[t]) continue;
+            const int r = 16 * t + col;
+            const float inv = lt > 0.0f ? vscale / lt : 0.0f;
+            const size_t ob = ((size_t)(row0 + r / G) * H + qhead_of(p, kvh, r % G, G)) * D;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (p.q_f32) {
+                    float v[DT];
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) v[dt] = o[dt][t][i] * inv;
+                    __builtin_memcpy((float *)p.out + ob + DT * (4 * grp + i), v, sizeof(v));
+                } else {
+                    uint32_t v[DT / 2];
+#pragma unroll
+                    for (int j = 0; j < DT / 2; ++j) v[j] = bf16x2_rne(o[2 * j][t][i] * inv, o[2 * j + 1][t][i] * inv);
+                    __builtin_memcpy((uint16_t *)p.out + ob + DT * (4 * grp + i), v, sizeof(v));
+                }
+            }
+        }
+        item = __builtin_amdgcn_readfirstlane(next);
+    }
+}
+
+template <int KV, int D>
+bool launch_g(const PParams &p, hipStream_t s, int G) {
+    switch (G) {
+        case 1: prefill_mfma_kernel<KV, D, 1><<<p.num_waves, kWave, 0, s>>>(p); return true;
+        case 2: prefill_mfma_kernel<KV, D, 2><<<p.num_waves, kWave, 0, s>>>(p); return true;
+        case 4: prefill_mfma_kernel<KV, D, 4><<<p.num_waves, kWave, 0, s>>>(p); return true;
+        case 8: prefill_mfma_kernel<KV, D, 8><<<p.num_waves, kWave, 0, s>>>(p); return true;
+        default: return false;
+    }
+}
+
+int persistent_waves() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return cus * 4;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Workspace: eff[N] | work[2] | items[max_items] (int4).
+int max_items_for(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads) {
+    const int G = num_kv_heads > 0 ? std::max(1, num_heads / num_kv_heads) : 1;
+    const int tq = std::max(1, kRows / G);
+    const int64_t m = (total_q + tq - 1) / tq + num_seqs;
+    return (int)std::min<int64_t>(m, 0x3fffffff);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t zk_paged_prefill_workspace_size(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads) {
+    if (num_seqs <= 0 || total_q < 0) return 256;
+    return align256(sizeof(int32_t) * (size_t)num_seqs) + 256 +
+           align256(sizeof(int4) * (size_t)max_items_for(num_seqs, total_q, num_heads, num_kv_heads));
+}
+
+int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
+                     void *out, const int32_t *block_tables, const int64_t *cu_seqlens_q, const int32_t *start_pos,
+                     int num_seqs, int64_t total_q, int num_heads, int num_kv_heads, int head_dim, int block_size,
+                     int max_blocks_per_seq, int64_t num_blocks, float scale, int causal, zk_gqa_mapping mapping,
+                     const float *k_scales, const float *v_scales, void *workspace, size_t workspace_bytes,
+                     void *stream) {
+    if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: q dtype must be f32 or bf16");
+    if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+        max_blocks_per_seq <= 0 || num_blocks <= 0)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: bad shape");
+    if (num_heads % num_kv_heads != 0)
+        return set_error(ZK_ERR_INVALID_ARGUMENT,
+                         "Internal error: zk_paged_prefill: num_heads must be a multiple of num_kv_heads");
+    if (mapping != ZK_GQA_GROUPED && mapping != ZK_GQA_MODULO)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: bad gqa mapping");
+    const int G = num_heads / num_kv_heads;
+    if ((kv_dtype != ZK_BF16 && kv_dtype != ZK_FP8_E4M3) || block_size != 16 ||
+        (head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 8))
+        return set_error(ZK_ERR_INVALID_ARGUMENT,
+                         "Internal error: zk_paged_prefill: needs bf16 or fp8 pools, block_size 16, head_dim 64 "
+                         "or 128 and H/Hkv in {1, 2, 4, 8}");
+    if (max_blocks_per_seq > kMaxBins)  // an item stages its block ids in LDS
+        return set_error(ZK_ERR_INVALID_ARGUMENT,
+                         "Internal error: zk_paged_prefill: max_blocks_per_seq above " + std::to_string(kMaxBins));
+    if (num_seqs == 0 || total_q == 0) return ZK_OK;
+    if (!q || !k_pool || !v_pool || !out || !block_tables || !cu_seqlens_q || !start_pos || !workspace)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: NULL pointer");
+    const bool fp8 = kv_dtype == ZK_FP8_E4M3;
+    if (fp8 != (k_scales != nullptr && v_scales != nullptr))
+        return set_error(ZK_ERR_INVALID_ARGUMENT,
+                         "Internal error: zk_paged_prefill: fp8 pools need k/v scales, other pools none");
+    const size_t need = zk_paged_prefill_workspace_size(num_seqs, total_q, num_heads, num_kv_heads);
+    if (workspace_bytes < need || ((uintptr_t)workspace & 255u))
+        return set_error(ZK_ERR_INVALID_ARGUMENT,
+                         "Internal error: zk_paged_prefill: workspace too small or not 256-B aligned (need " +
+                             std::to_string(need) + " bytes)");
+    PParams p;
+    p.q = q;
+    p.k_pool = (const char *)k_pool;
+    p.v_pool = (const char *)v_pool;
+    p.out = out;
+    p.bt = block_tables;
+    p.cu_q = cu_seqlens_q;
+    p.start = start_pos;
+    p.k_scales = k_scales;
+    p.v_scales = v_scales;
+    char *ws = (char *)workspace;
+    p.eff = (int32_t *)ws;
+    p.work = (int32_t *)(ws + align256(sizeof(int32_t) * (size_t)num_seqs));
+    p.items = (int4 *)(ws + align256(sizeof(int32_t) * (size_t)num_seqs) + 256);
+    p.num_seqs = num_seqs;
+    p.num_heads = num_heads;
+    p.num_kv_heads = num_kv_heads;
+    p.head_dim = head_dim;
+    p.block_size = block_size;
+    p.max_blocks = max_blocks_per_seq;
+    p.tq = kRows / G;
+    p.num_waves = persistent_waves();
+    p.max_items = max_items_for(num_seqs, total_q, num_heads, num_kv_heads);
+    p.num_blocks = num_blocks;
+    p.scale_log2 = scale * kLog2e;
+    p.grouped = mapping == ZK_GQA_GROUPED ? 1 : 0;
+    p.q_f32 = q_dtype == ZK_F32 ? 1 : 0;
+    p.causal = causal ? 1 : 0;
+    hipStream_t s = (hipStream_t)stream;
+    {
+        KernelTimer timer("prefill_plan", s);
+        prefill_plan_kernel<<<1, 1024, 0, s>>>(p);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(ZK_ERR_HIP, std::string("Internal error: zk_paged_prefill plan: ") + hipGetErrorString(e));
+    {
+        KernelTimer timer("prefill_attention", s);
+        if (kv_dtype == ZK_BF16) {
+            if (head_dim == 128) launch_g<ZK_BF16, 128>(p, s, G);
+            else launch_g<ZK_BF16, 64>(p, s, G);
+        } else {
+            if (head_dim == 128) launch_g<ZK_FP8_E4M3, 128>(p, s, G);
+            else launch_g<ZK_FP8_E4M3, 64>(p, s, G);
+        }
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(ZK_ERR_HIP, std::string("Internal error: zk_paged_prefill: ") + hipGetErrorString(e));
+    return ZK_OK;
+}
+
+}  // extern "C"

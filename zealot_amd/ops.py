@@ -147,3 +147,39 @@ def paged_decode(q, k_pool, v_pool, block_tables, seq_lens, scale=None, mapping=
         _opt(v_scales, "v_scales", torch.float32), _dev(workspace, "workspace"),
         workspace.numel() * workspace.element_size(), _stream(stream)))
     return out
+
+
+def prefill_workspace_bytes(num_seqs, total_q, num_heads, num_kv_heads) -> int:
+    return int(_lib.lib().zk_paged_prefill_workspace_size(num_seqs, total_q, num_heads, num_kv_heads))
+
+
+def paged_prefill(q, k_pool, v_pool, block_tables, cu_seqlens_q, start_pos, causal=True, scale=None,
+                  mapping="grouped", k_scales=None, v_scales=None, out=None, workspace=None, stream=None):
+    """Chunked-prefill attention: q [T, H, D] (f32/bf16), sequence n's chunk is
+    rows cu_seqlens_q[n] .. cu_seqlens_q[n+1] (int64) after start_pos[n] (int32)
+    cached tokens; its K/V must already be in the pages.  Returns out [T, H, D]."""
+    nb, hkv, bs, d = _pool_shape(k_pool, v_pool)
+    if q.dim() != 3 or q.shape[2] != d:
+        raise ValueError(f"q must be [T, H, {d}]")
+    t, h, _ = q.shape
+    n = start_pos.shape[0]
+    if block_tables.dim() != 2 or block_tables.shape[0] != n or cu_seqlens_q.shape != (n + 1,):
+        raise ValueError("block_tables must be [N, max_blocks], cu_seqlens_q [N + 1] and start_pos [N]")
+    mb = block_tables.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q")
+    need = prefill_workspace_bytes(n, t, h, hkv)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _lib.check(_lib.lib().zk_paged_prefill(
+        _dev(q, "q"), zk_dtype(q), _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool"), zk_dtype(k_pool),
+        _dev(out, "out"), _dev(block_tables, "block_tables", torch.int32),
+        _dev(cu_seqlens_q, "cu_seqlens_q", torch.int64), _dev(start_pos, "start_pos", torch.int32), n, t, h, hkv,
+        d, bs, mb, nb, float(scale), int(bool(causal)), _MAPPINGS[mapping],
+        _opt(k_scales, "k_scales", torch.float32), _opt(v_scales, "v_scales", torch.float32),
+        _dev(workspace, "workspace"), workspace.numel() * workspace.element_size(), _stream(stream)))
+    return out
