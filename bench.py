@@ -8,7 +8,8 @@ also measures the chunked-prefill KV append (C3: 64 x 512 tokens at
 non-aligned offsets, bf16), the fp8-KV decode (C5: 512 sequences, context
 U[1024, 16384]) and prefix sharing with copy-on-write through the stateful
 KVCache (C4: 16 prefixes x 2048+r tokens x 32 layers, 128 forks, 64 decode
-steps) and reports them as extra fields.
+steps) and the causal chunked-prefill attention of C3's chunks, and reports
+them as extra fields.
 
 Algorithmic bytes (unique bytes that must cross HBM):
   decode  sum(ctx) * 2 * Hkv * D * elt  + Q + O + block-table entries + seq_lens
@@ -412,6 +413,65 @@ def bench_c4(args, torch, lib):
     return res
 
 
+# ---------------------------------------------------------------- prefill attention
+
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def bench_prefill(args, torch, ops, lib):
+    """Causal chunked-prefill attention of C3's chunks: 64 sequences x 512 new
+    tokens at unaligned offsets < 4096 (their K/V already in the pages), 32/8
+    heads, D = 128, bf16.  Compute-bound: 4 * D flops per (query row, head,
+    visible key)."""
+    N, C, H, Hkv, D, BS = 64, 512, 32, 8, 128, 16
+    rng = np.random.default_rng(SEED + 1)
+    starts = rng.integers(0, 4096, N)
+    starts[starts % BS == 0] += 1
+    lens = starts + C
+    bt, nb, _ = paged_tables(rng, lens, BS)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(SEED + 6)
+    kp = torch.randn((nb, Hkv, BS, D), generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn((nb, Hkv, BS, D), generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn((N * C, H, D), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    btd = torch.from_numpy(bt).to(dev)
+    cu = torch.arange(0, N * C + 1, C, dtype=torch.int64, device=dev)
+    st = torch.from_numpy(starts.astype(np.int32)).to(dev)
+    ws = torch.empty(ops.prefill_workspace_bytes(N, N * C, H, Hkv), dtype=torch.uint8, device=dev)
+    log(f"prefill: N={N} chunk={C} context {int(lens.min())}..{int(lens.max())} blocks={nb}")
+
+    def step(_):
+        ops.paged_prefill(q, kp, vp, btd, cu, st, causal=True, out=out, workspace=ws)
+
+    ms = timed(step, args.steps, args.warmup, torch)
+    lib.zk_timing_reset()
+    lib.zk_timing_enable(1)
+    timed(step, args.steps, 0, torch)
+    lib.zk_timing_enable(0)
+    k_ms, k_n = kernel_ms(lib, "prefill_attention")
+    p_ms, _ = kernel_ms(lib, "prefill_plan")
+    lib.zk_timing_reset()
+    keys = int(sum(int(s) * C + C * (C + 1) // 2 for s in starts))  # visible keys over all rows
+    flops = 4 * D * H * keys
+    tflops = flops / (ms * 1e-3) / 1e12
+    k_tflops = flops / (k_ms * 1e-3) / 1e12
+    # K/V bytes the kernel streams: every (tile, kv-head) reads its pages once
+    tq = 64 // (H // Hkv)
+    kv_bytes = sum(((int(s) + min(C, (t + 1) * tq) + BS - 1) // BS) * BS * 2 * D * 2 * Hkv
+                   for s in starts for t in range((C + tq - 1) // tq))
+    res = {"ms_per_step": ms, "tflops": tflops, "frac_of_peak": tflops / PEAK_BF16_TFLOPS,
+           "tokens_per_s": N * C / (ms * 1e-3), "flops": flops, "visible_keys": keys,
+           "kernel_ms": {"prefill_attention": k_ms, "prefill_plan": p_ms},
+           "kv_bytes_streamed": kv_bytes, "kv_gbps_streamed": kv_bytes / (k_ms * 1e-3) / 1e9,
+           "roofline": {"bound": "mfma", "achieved": k_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": k_tflops / PEAK_BF16_TFLOPS, "traffic": None, "kernel": "prefill_attention",
+                        "kernel_flops_per_launch": flops, "launches": k_n}}
+    del kp, vp, q, out, ws
+    torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 def cpu_model() -> str:
@@ -456,7 +516,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4"], default=None,
+    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4", "prefill"], default=None,
                     help="run one workload (for profiler passes)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
@@ -475,7 +535,7 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     result = {}
-    dec = lens = app = fp8 = c4 = None
+    dec = lens = app = fp8 = c4 = pre = None
     if args.only in (None, "decode"):
         dec, lens = bench_decode(args, torch, ops, lib, "bf16")
         log(f"decode bf16: {dec['ms_per_step']:.4f} ms {dec['gbps']:.1f} GB/s")
@@ -489,14 +549,20 @@ def main() -> int:
         c4 = bench_c4(args, torch, lib)
         log(f"c4: cow {c4['cow']['gbps']:.1f} GB/s; step {c4['decode_step']['ms_per_step']:.3f} ms, "
             f"logical {c4['decode_step']['logical_gbps']:.1f} GB/s, unique {c4['decode_step']['unique_gbps']:.1f} GB/s")
+    if args.only in (None, "prefill"):
+        pre = bench_prefill(args, torch, ops, lib)
+        log(f"prefill: {pre['ms_per_step']:.3f} ms {pre['tflops']:.1f} TFLOP/s "
+            f"(kernel {pre['roofline']['achieved']:.1f} TFLOP/s)")
     cpu = None
     if args.only is None and not args.no_cpu_baseline:
         cpu = cpu_baseline(lens, args.cpu_sample_seqs)
         log(f"cpu baseline: {cpu['value']:.3f} GB/s (1 core), {cpu['omp_value']:.2f} GB/s ({cpu['omp_cores']} cores)")
     head = next((x for x in (dec, app, fp8) if x is not None), None)
-    if head is None:  # --only c4
+    if head is None and c4 is not None:  # --only c4
         head = {"gbps": c4["decode_step"]["logical_gbps"], "ms_per_step": c4["decode_step"]["ms_per_step"],
                 "roofline": None}
+    if head is None:  # --only prefill
+        head = {"gbps": pre["tflops"], "ms_per_step": pre["ms_per_step"], "roofline": pre["roofline"]}
     result = {
         "metric": METRIC,
         "value": round(head["gbps"], 2),
@@ -520,6 +586,7 @@ def main() -> int:
         "append_bf16": app,
         "decode_fp8": fp8,
         "prefix_cow_c4": c4,
+        "prefill_attention": pre,
         "gpu": torch.cuda.get_device_name(0),
     }
     if args.only is not None:
