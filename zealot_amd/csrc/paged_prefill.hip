@@ -302,7 +302,10 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
             for (int dt = 0; dt < DT; ++dt) o[dt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
         const s16x4 ones = __builtin_bit_cast(s16x4, u32x2{0x3f803f80u, 0x3f803f80u});  // bf16 1.0 x 4
-        auto page = [&](int pi, int s) {
+        // MASK: the page holds keys some row of the tile may not see (the
+        // diagonal pages, or stale rows past the context); the pages before
+        // run without the per-element compares.
+        auto page = [&]<bool MASK>(int pi, int s) {
             if (pi + 1 < np) wait_vmcnt<LPP>();
             else wait_vmcnt<0>();
             uint32_t kw[KBYTES / 4];
@@ -352,7 +355,7 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
                 }
             }
             const int key0 = pi * BS + 4 * grp;  // position of this lane's first key
-            if (key0 + 4 > eff) {  // past the context: stale rows must not reach O
+            if (MASK && key0 + 4 > eff) {  // past the context: stale rows must not reach O
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     if (key0 + i >= eff)
@@ -373,7 +376,7 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
             for (int t = 0; t < T; ++t) {
                 float sc[4];  // raw scores; the scale is applied inside the exponent
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sc[i] = key0 + i < lim[t] ? sacc[t][i] : -INFINITY;
+                for (int i = 0; i < 4; ++i) sc[i] = !MASK || key0 + i < lim[t] ? sacc[t][i] : -INFINITY;
                 const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])) * sl2;
                 if (__builtin_amdgcn_ballot_w64(mx > m[t] + kRescaleSlack)) {
                     float cm = fmaxf(mx, xor16(mx));
@@ -399,7 +402,12 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
         if (np > 0) issue(0, 0);
         if (lane == 0) next = atomicAdd(&p.work[1], 1);  // overlaps the first page's round trip
         if (np > 1) issue(1, 1);
-        for (int pi = 0, s = 0; pi < np; ++pi, s ^= 1) page(pi, s);
+        // pages every row sees whole: below the first row's limit (rows are
+        // token-major, limits grow with the row)
+        const int open = min(p.causal ? st + qt * p.tq + 1 : st + len, eff) / BS;
+        int pi = 0, s = 0;
+        for (; pi < min(open, np); ++pi, s ^= 1) page.template operator()<false>(pi, s);
+        for (; pi < np; ++pi, s ^= 1) page.template operator()<true>(pi, s);
 
         // rows of this lane: dims DT*(4*grp+i)+dt of row 16 t + col
 #pragma unroll
