@@ -198,6 +198,17 @@ int zk_cache_append_kv(zk_kv_cache *c, size_t layer, const char *id, const void 
  * (kv_cache.rs:281-356) for a runner that steps all sequences together. */
 int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *ids, int n,
                              const void *k, const void *v, zk_dtype src_dtype);
+/* Batched write for one layer of a mixed prefill / decode step: sequence
+ * ids[i] receives num_tokens[i] tokens (0 allowed) at its cached_tokens
+ * position, packed in batch order in k/v ([sum num_tokens, Hkv, D]);
+ * copy-on-write first where a target block is shared; one launch for the whole
+ * batch.  Writing the last layer advances each sequence by its num_tokens[i].
+ * Replaces the per-sequence store_kv / append_kv calls of the runner's step
+ * (cuda_runner.rs:274-406, kv_cache.rs:206-356).  Fails before writing
+ * anything if a position has no block (kv_cache.rs:234-239) or an id repeats. */
+int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids,
+                         const int32_t *num_tokens, int n, const void *k, const void *v,
+                         zk_dtype src_dtype);
 /* fp8 pools: set the per-(layer, kv_head) dequant scales of a sequence
  * (k_scales/v_scales: host arrays of num_layers * Hkv floats). */
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales,
@@ -221,6 +232,18 @@ int zk_cache_block_ids(zk_kv_cache *c, const char *id, int64_t *ids, size_t *n);
 int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, int n,
                           const void *q, zk_dtype q_dtype, void *out, int num_heads, float scale,
                           zk_gqa_mapping mapping);
+/* Batched attention for one layer of a mixed step, after zk_cache_write_batch
+ * wrote the step's tokens: the num_tokens[i] query rows of sequence ids[i]
+ * (packed in batch order in q / out, [sum num_tokens, H, D]) are its last
+ * num_tokens[i] tokens at this layer, attended causally over its pages (row t
+ * sees positions [0, layer_len - num_tokens[i] + t], attention.cu:117-121).
+ * One-row entries run as one paged decode (with prefix sharing), longer ones
+ * as one chunked-prefill launch (zk_paged_prefill); shapes outside the
+ * prefill kernel's run every chunk row as a decode.  Replaces the runner's
+ * per-sequence paged_forward (cuda_runner.rs:438-461). */
+int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *ids,
+                             const int32_t *num_tokens, int n, const void *q, zk_dtype q_dtype,
+                             void *out, int num_heads, float scale, zk_gqa_mapping mapping);
 /* Prefix sharing of the last zk_cache_paged_decode: subgroups formed and the
  * pages they shared (sum over subgroups).  No reference counterpart. */
 int zk_cache_decode_sharing(zk_kv_cache *c, int *subgroups, int64_t *shared_pages);

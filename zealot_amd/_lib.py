@@ -74,6 +74,7 @@ SIGNATURES = {
     "zk_cache_store_kv": (_I, [_P, _SZ, _CP, _P, _P, _I, _SZ, _SZ]),
     "zk_cache_append_kv": (_I, [_P, _SZ, _CP, _P, _P, _I]),
     "zk_cache_append_kv_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _P, _I]),
+    "zk_cache_write_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _P, _I]),
     "zk_cache_set_fp8_scales": (_I, [_P, _CP, _P, _P]),
     "zk_cache_block_table_ptr": (_I, [_P, _CP, ctypes.POINTER(_P)]),
     "zk_cache_k_pool_ptr": (_P, [_P, _SZ]),
@@ -83,6 +84,7 @@ SIGNATURES = {
                                 ctypes.POINTER(_SZ)]),
     "zk_cache_block_ids": (_I, [_P, _CP, ctypes.POINTER(_I64), ctypes.POINTER(_SZ)]),
     "zk_cache_paged_decode": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _I, _P, _I, _F, _I]),
+    "zk_cache_attention_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _I, _P, _I, _F, _I]),
     "zk_cache_decode_sharing": (_I, [_P, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int64)]),
     "zk_timing_enable": (_I, [_I]),
     "zk_timing_reset": (_I, []),

@@ -139,6 +139,8 @@ struct zk_kv_cache {
     DevBuf d_tblupd;   // block-table updates (offset, value)
     CachedBuf d_tbl;   // decode batch block tables [n][stride]
     CachedBuf d_batch; // decode batch lengths + scales
+    CachedBuf d_pre;   // prefill batch tables, row offsets, lengths, starts, scales
+    DevBuf d_pws;      // prefill workspace
     DevBuf d_ws;     // decode workspace
     static constexpr int kStages = 16;
     Staging stage[kStages];
@@ -543,55 +545,69 @@ int zk_cache_append_kv(zk_kv_cache *c, size_t layer, const char *id, const void 
     return write_tokens(c, layer, *s, id, k, v, src_dtype, s->cached_tokens, 1, "append_kv");
 }
 
-int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *k,
-                             const void *v, zk_dtype src_dtype) {
-    if (!c || (n > 0 && !ids)) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache append batch: NULL argument");
+int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,
+                         const void *k, const void *v, zk_dtype src_dtype) {
+    if (!c || (n > 0 && (!ids || !num_tokens)))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: NULL argument");
     if (layer >= c->num_layers)
-        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache append batch: layer out of range");
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: layer out of range");
     if (src_dtype != ZK_F32 && src_dtype != ZK_BF16)
-        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache append batch: bad src dtype");
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: bad src dtype");
     if (n <= 0) return ZK_OK;
-    if (!k || !v) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache append batch: NULL k/v");
     DeviceGuard g(c->device);
     const size_t bs = c->block_size, H = c->num_kv_heads;
     const bool fp8 = c->dtype == ZK_FP8_E4M3;
     std::vector<SeqState *> seqs((size_t)n);
+    size_t T = 0;
     for (int i = 0; i < n; ++i) {
         if (int rc = find_seq(c, ids[i], &seqs[i])) return rc;
         for (int j = 0; j < i; ++j)
             if (seqs[j] == seqs[i])
                 return set_error(ZK_ERR_INVALID_ARGUMENT,
-                                 std::string("Internal error: KVCache append batch: seq ") + ids[i] + " twice");
+                                 std::string("Internal error: KVCache write batch: seq ") + ids[i] + " twice");
+        if (num_tokens[i] < 0)
+            return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: negative token count");
         const SeqState &s = *seqs[i];
-        const size_t idx = s.cached_tokens / bs;
-        if (idx >= s.handles.size())  // kv_cache.rs:307-312
-            return set_error(ZK_ERR_INTERNAL, "Internal error: KVCache append_kv: block_idx " + std::to_string(idx) +
-                                                  " OOB (have " + std::to_string(s.handles.size()) + " blocks)");
+        if (num_tokens[i] > 0) {
+            const size_t last = (s.cached_tokens + (size_t)num_tokens[i] - 1) / bs;
+            if (last >= s.handles.size())  // kv_cache.rs:234-239
+                return set_error(ZK_ERR_INTERNAL, "Internal error: KVCache append_kv: block_idx " +
+                                                      std::to_string(last) + " OOB (have " +
+                                                      std::to_string(s.handles.size()) + " blocks)");
+        }
         if (fp8 && s.k_scales.empty())
             return set_error(ZK_ERR_FAILED_PRECONDITION,
                              std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
+        T += (size_t)num_tokens[i];
     }
-    std::vector<std::pair<SeqState *, size_t>> shared;  // copy-on-write of shared targets
+    if (T == 0) return ZK_OK;
+    if (!k || !v) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: NULL k/v");
+    std::vector<std::pair<SeqState *, size_t>> shared;  // copy-on-write of every shared target
     for (int i = 0; i < n; ++i) {
         SeqState &s = *seqs[i];
-        const size_t idx = s.cached_tokens / bs;
-        if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1) shared.emplace_back(&s, idx);
+        if (num_tokens[i] == 0) continue;
+        for (size_t idx = s.cached_tokens / bs; idx <= (s.cached_tokens + (size_t)num_tokens[i] - 1) / bs; ++idx)
+            if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1) shared.emplace_back(&s, idx);
     }
     if (int rc = cow_blocks(c, shared)) return rc;
-    const size_t slots_bytes = (size_t)n * sizeof(int64_t);
-    const size_t rows_bytes = fp8 ? (size_t)n * sizeof(int32_t) : 0;
+    const size_t slots_bytes = T * sizeof(int64_t);
+    const size_t rows_bytes = fp8 ? T * sizeof(int32_t) : 0;
     const size_t scale_bytes = fp8 ? 2 * (size_t)n * H * sizeof(float) : 0;
     std::vector<char> host(slots_bytes + rows_bytes + scale_bytes);
     int64_t *slots = (int64_t *)host.data();
+    int32_t *rows = fp8 ? (int32_t *)(host.data() + slots_bytes) : nullptr;
+    size_t t = 0;
     for (int i = 0; i < n; ++i) {
         const SeqState &s = *seqs[i];
-        slots[i] = (int64_t)s.handles[s.cached_tokens / bs].block_id * (int64_t)bs + (int64_t)(s.cached_tokens % bs);
+        for (int j = 0; j < num_tokens[i]; ++j, ++t) {
+            const size_t pos = s.cached_tokens + (size_t)j;
+            slots[t] = (int64_t)s.handles[pos / bs].block_id * (int64_t)bs + (int64_t)(pos % bs);
+            if (fp8) rows[t] = i;
+        }
     }
     if (fp8) {
-        int32_t *rows = (int32_t *)(host.data() + slots_bytes);
         float *sc = (float *)(host.data() + slots_bytes + rows_bytes);
         for (int i = 0; i < n; ++i) {
-            rows[i] = i;
             std::memcpy(sc + (size_t)i * H, seqs[i]->k_scales.data() + layer * H, H * sizeof(float));
             std::memcpy(sc + (size_t)n * H + (size_t)i * H, seqs[i]->v_scales.data() + layer * H, H * sizeof(float));
         }
@@ -602,19 +618,25 @@ int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *id
     const float *d_ks = fp8 ? (const float *)(d + slots_bytes + rows_bytes) : nullptr;
     const float *d_vs = fp8 ? d_ks + (size_t)n * H : nullptr;
     if (int rc = zk_append(c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, k, v, src_dtype,
-                           (const int64_t *)d, (int64_t)n, (int)H, (int)c->head_dim, (int)bs,
+                           (const int64_t *)d, (int64_t)T, (int)H, (int)c->head_dim, (int)bs,
                            (int64_t)c->num_blocks, d_ks, d_vs, d_rows, c->stream))
         return rc;
     for (int i = 0; i < n; ++i) {
         SeqState &s = *seqs[i];
-        s.layer_len[layer] = std::max(s.layer_len[layer], s.cached_tokens + 1);
+        s.layer_len[layer] = std::max(s.layer_len[layer], s.cached_tokens + (size_t)num_tokens[i]);
     }
     if (layer + 1 == c->num_layers)
         for (int i = 0; i < n; ++i) {
-            seqs[i]->cached_tokens += 1;
+            seqs[i]->cached_tokens += (size_t)num_tokens[i];
             seqs[i]->block_offset = seqs[i]->cached_tokens % bs;
         }
     return ZK_OK;
+}
+
+int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *k,
+                             const void *v, zk_dtype src_dtype) {
+    std::vector<int32_t> ones(n > 0 ? (size_t)n : 0, 1);
+    return zk_cache_write_batch(c, layer, ids, ones.data(), n, k, v, src_dtype);
 }
 
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales, const float *v_scales) {
@@ -675,26 +697,23 @@ int zk_cache_block_ids(zk_kv_cache *c, const char *id, int64_t *ids, size_t *n) 
     return ZK_OK;
 }
 
-int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *q,
-                          zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping) {
-    if (!c || (n > 0 && !ids)) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode: NULL argument");
-    if (layer >= c->num_layers)
-        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode: layer out of range");
+}  // extern "C"
+
+namespace {
+
+// Decode at `layer` of entries seqs[i] (a sequence may appear more than once)
+// with context lens[i] (default: the tokens written at the layer) and q / out
+// row q_rows[i] (default: i); forked prefixes are shared when `share` holds
+// and the lengths are the layer's.
+int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState *> &seqs,
+                 const std::vector<int32_t> *lens_in, const std::vector<int32_t> *q_rows, const void *q,
+                 zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping, bool share) {
+    const int n = (int)seqs.size();
     if (n <= 0) return ZK_OK;
-    DeviceGuard g(c->device);
     const size_t H = c->num_kv_heads;
     const bool fp8 = c->dtype == ZK_FP8_E4M3;
-    std::vector<const SeqState *> seqs((size_t)n);
     size_t stride = 1;
-    for (int i = 0; i < n; ++i) {
-        SeqState *s;
-        if (int rc = find_seq(c, ids[i], &s)) return rc;
-        if (fp8 && s->k_scales.empty())
-            return set_error(ZK_ERR_FAILED_PRECONDITION,
-                             std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
-        seqs[i] = s;
-        stride = std::max(stride, s->handles.size());
-    }
+    for (const SeqState *s : seqs) stride = std::max(stride, s->handles.size());
     // Block tables [n][stride]: re-uploaded only when some table changed or
     // the batch differs from the previous call's.
     if (c->dec_epoch != c->epoch || c->dec_ids != seqs || c->dec_stride != stride) {
@@ -710,7 +729,7 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
     }
     // Shared prefixes of forked sequences (bf16 MFMA shapes only).
     SharePlan sp;
-    if (num_heads > 0 && num_heads % (int)H == 0 &&
+    if (share && !lens_in && num_heads > 0 && num_heads % (int)H == 0 &&
         zk::paged_decode_shares_prefixes(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads, (int)H))
         plan_sharing(seqs, layer, c->block_size, 32 / (num_heads / (int)H), sp);
     const int nsg = (int)sp.sg_pages.size();
@@ -720,12 +739,14 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
     const size_t len_bytes = a256((size_t)n * sizeof(int32_t));
     const size_t sc_bytes = a256(fp8 ? 2 * (size_t)n * H * sizeof(float) : 0);
     const size_t share_ints = nsg ? (size_t)n + sp.sg_members.size() + sp.sg_pages.size() : 0;
-    const size_t total = len_bytes + sc_bytes + share_ints * sizeof(int32_t);
+    const size_t share_bytes = a256(share_ints * sizeof(int32_t));
+    const size_t rows_bytes = q_rows ? (size_t)n * sizeof(int32_t) : 0;
+    const size_t total = len_bytes + sc_bytes + share_bytes + rows_bytes;
     std::vector<char> host(total, 0);
     int32_t *lens = (int32_t *)host.data();
     float *sc = (float *)(host.data() + len_bytes);
     for (int i = 0; i < n; ++i) {
-        lens[i] = (int32_t)seqs[i]->layer_len[layer];
+        lens[i] = lens_in ? (*lens_in)[i] : (int32_t)seqs[i]->layer_len[layer];
         if (fp8) {
             std::memcpy(sc + (size_t)i * H, seqs[i]->k_scales.data() + layer * H, H * sizeof(float));
             std::memcpy(sc + (size_t)n * H + (size_t)i * H, seqs[i]->v_scales.data() + layer * H, H * sizeof(float));
@@ -741,6 +762,7 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
         std::memcpy(sh + o_mem, sp.sg_members.data(), sp.sg_members.size() * sizeof(int32_t));
         std::memcpy(sh + o_pages, sp.sg_pages.data(), sp.sg_pages.size() * sizeof(int32_t));
     }
+    if (q_rows) std::memcpy(host.data() + len_bytes + sc_bytes + share_bytes, q_rows->data(), rows_bytes);
     if (int rc = put(c, c->d_batch, host.data(), total, "KVCache decode batch")) return rc;
     size_t ws = zk::paged_decode_workspace(n, num_heads, (int)c->head_dim, (int)stride, (int)c->block_size, nsg > 0);
     if (int rc = c->d_ws.ensure(ws, "KVCache decode workspace")) return rc;
@@ -751,10 +773,151 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
     zk::PrefixGroups pg{dsh + o_pb, dsh + o_mem, dsh + o_pages, nsg, sp.total_pages};
     c->last_sg = nsg;
     c->last_sg_pages = sp.total_pages;
+    const int32_t *drows = q_rows ? (const int32_t *)(d + len_bytes + sc_bytes + share_bytes) : nullptr;
     return zk::paged_decode(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
                             (const int32_t *)c->d_tbl.dev.p, (const int32_t *)d, n, num_heads, (int)H,
                             (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
-                            mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr);
+                            mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr, drows);
+}
+
+// Looks up ids[0..n) (each must be registered; fp8 caches need scales).
+int find_seqs(zk_kv_cache *c, const char *const *ids, int n, std::vector<const SeqState *> &out) {
+    out.resize(n > 0 ? (size_t)n : 0);
+    for (int i = 0; i < n; ++i) {
+        SeqState *s;
+        if (int rc = find_seq(c, ids[i], &s)) return rc;
+        if (c->dtype == ZK_FP8_E4M3 && s->k_scales.empty())
+            return set_error(ZK_ERR_FAILED_PRECONDITION,
+                             std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
+        out[i] = s;
+    }
+    return ZK_OK;
+}
+
+// Causal chunked-prefill attention of chunk rows through zk_paged_prefill:
+// entry i is seqs[i]'s last len[i] tokens at the layer, at q / out rows
+// off[i] .. off[i] + len[i].
+int prefill_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState *> &seqs,
+                  const std::vector<int32_t> &len, const std::vector<int64_t> &off, int64_t total_rows, const void *q,
+                  zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping) {
+    const int n = (int)seqs.size();
+    if (n <= 0) return ZK_OK;
+    const size_t H = c->num_kv_heads;
+    const bool fp8 = c->dtype == ZK_FP8_E4M3;
+    size_t stride = 1;
+    for (const SeqState *s : seqs) stride = std::max(stride, s->handles.size());
+    auto a256 = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t tbl_bytes = a256((size_t)n * stride * sizeof(int32_t));
+    const size_t off_bytes = a256((size_t)n * sizeof(int64_t));
+    const size_t i32_bytes = a256((size_t)n * sizeof(int32_t));
+    const size_t sc_bytes = fp8 ? 2 * (size_t)n * H * sizeof(float) : 0;
+    std::vector<char> host(tbl_bytes + off_bytes + 2 * i32_bytes + sc_bytes, 0);
+    int32_t *tbl = (int32_t *)host.data();
+    int64_t *qo = (int64_t *)(host.data() + tbl_bytes);
+    int32_t *ql = (int32_t *)(host.data() + tbl_bytes + off_bytes);
+    int32_t *st = (int32_t *)(host.data() + tbl_bytes + off_bytes + i32_bytes);
+    float *sc = (float *)(host.data() + tbl_bytes + off_bytes + 2 * i32_bytes);
+    for (int i = 0; i < n; ++i) {
+        for (size_t j = 0; j < stride; ++j)
+            tbl[(size_t)i * stride + j] = j < seqs[i]->handles.size() ? (int32_t)seqs[i]->handles[j].block_id : -1;
+        qo[i] = off[i];
+        ql[i] = len[i];
+        st[i] = (int32_t)seqs[i]->layer_len[layer] - len[i];
+        if (fp8) {
+            std::memcpy(sc + (size_t)i * H, seqs[i]->k_scales.data() + layer * H, H * sizeof(float));
+            std::memcpy(sc + (size_t)n * H + (size_t)i * H, seqs[i]->v_scales.data() + layer * H, H * sizeof(float));
+        }
+    }
+    if (int rc = put(c, c->d_pre, host.data(), host.size(), "KVCache prefill batch")) return rc;
+    const size_t ws = zk_paged_prefill_workspace_size(n, total_rows, num_heads, (int)H);
+    if (int rc = c->d_pws.ensure(ws, "KVCache prefill workspace")) return rc;
+    char *d = (char *)c->d_pre.dev.p;
+    const float *dks = fp8 ? (const float *)(d + tbl_bytes + off_bytes + 2 * i32_bytes) : nullptr;
+    const float *dvs = fp8 ? dks + (size_t)n * H : nullptr;
+    return zk::paged_prefill_rows(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
+                                  (const int32_t *)d, (const int64_t *)(d + tbl_bytes),
+                                  (const int32_t *)(d + tbl_bytes + off_bytes),
+                                  (const int32_t *)(d + tbl_bytes + off_bytes + i32_bytes), n, total_rows, num_heads,
+                                  (int)H, (int)c->head_dim, (int)c->block_size, (int)stride,
+                                  (int64_t)c->num_blocks, scale, 1, mapping, dks, dvs, c->d_pws.p, c->d_pws.cap,
+                                  c->stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *q,
+                          zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping) {
+    if (!c || (n > 0 && !ids)) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode: NULL argument");
+    if (layer >= c->num_layers)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode: layer out of range");
+    if (n <= 0) return ZK_OK;
+    DeviceGuard g(c->device);
+    std::vector<const SeqState *> seqs;
+    if (int rc = find_seqs(c, ids, n, seqs)) return rc;
+    return decode_batch(c, layer, seqs, nullptr, nullptr, q, q_dtype, out, num_heads, scale, mapping, true);
+}
+
+int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,
+                             const void *q, zk_dtype q_dtype, void *out, int num_heads, float scale,
+                             zk_gqa_mapping mapping) {
+    if (!c || (n > 0 && (!ids || !num_tokens)))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache attention batch: NULL argument");
+    if (layer >= c->num_layers)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache attention batch: layer out of range");
+    if (n <= 0) return ZK_OK;
+    DeviceGuard g(c->device);
+    std::vector<const SeqState *> seqs;
+    if (int rc = find_seqs(c, ids, n, seqs)) return rc;
+    // rows of entry i: off .. off + num_tokens[i], packed in batch order
+    std::vector<const SeqState *> dec, pre;
+    std::vector<int32_t> dec_rows, pre_len;
+    std::vector<int64_t> pre_off;
+    int64_t row = 0;
+    for (int i = 0; i < n; ++i) {
+        const int nt = num_tokens[i];
+        if (nt < 0 || (size_t)nt > seqs[i]->layer_len[layer])
+            return set_error(ZK_ERR_INVALID_ARGUMENT,
+                             std::string("Internal error: KVCache attention batch: seq ") + ids[i] +
+                                 " has fewer tokens at this layer than its rows (write the layer first)");
+        if (nt == 1) {
+            dec.push_back(seqs[i]);
+            dec_rows.push_back((int32_t)row);
+        } else if (nt > 1) {
+            pre.push_back(seqs[i]);
+            pre_len.push_back(nt);
+            pre_off.push_back(row);
+        }
+        row += nt;
+    }
+    if (row > 0x7fffffff)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache attention batch: too many rows");
+    if (!q || !out) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache attention batch: NULL q/out");
+    const bool identity = dec.size() == (size_t)n;  // all decode rows, in batch order
+    if (int rc = decode_batch(c, layer, dec, nullptr, identity ? nullptr : &dec_rows, q, q_dtype, out, num_heads,
+                              scale, mapping, true))
+        return rc;
+    if (pre.empty()) return ZK_OK;
+    size_t pre_pages = 0;
+    for (const SeqState *s : pre) pre_pages = std::max(pre_pages, s->handles.size());
+    if (zk::paged_prefill_supported(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads,
+                                    (int)c->num_kv_heads) &&
+        pre_pages <= (size_t)zk::kPrefillMaxPages)
+        return prefill_batch(c, layer, pre, pre_len, pre_off, row, q, q_dtype, out, num_heads, scale, mapping);
+    // shapes without the MFMA prefill: every chunk row is a decode of its
+    // causal context (start + t + 1 tokens)
+    std::vector<const SeqState *> ex;
+    std::vector<int32_t> ex_len, ex_rows;
+    for (size_t i = 0; i < pre.size(); ++i) {
+        const int32_t start = (int32_t)pre[i]->layer_len[layer] - pre_len[i];
+        for (int t = 0; t < pre_len[i]; ++t) {
+            ex.push_back(pre[i]);
+            ex_len.push_back(start + t + 1);
+            ex_rows.push_back((int32_t)(pre_off[i] + t));
+        }
+    }
+    return decode_batch(c, layer, ex, &ex_len, &ex_rows, q, q_dtype, out, num_heads, scale, mapping, false);
 }
 
 int zk_cache_decode_sharing(zk_kv_cache *c, int *subgroups, int64_t *shared_pages) {

@@ -71,7 +71,7 @@ int min_part_pages(int head_dim, int block_size) {
 constexpr int kSgStride = 32;  // member slots per prefix subgroup (query rows of one shared item)
 
 struct Params {
-    const void *q;
+    const void *q;        // [rows, H, D]; sequence n's row is q_rows[n] (n when q_rows is null)
     const char *k_pool;
     const char *v_pool;
     void *out;
@@ -79,6 +79,7 @@ struct Params {
     const int32_t *seq_lens;
     const float *k_scales;
     const float *v_scales;
+    const int32_t *q_rows;  // optional: q / out row of each sequence
     int32_t *eff_len;     // [N] length after the page walk
     int4 *items;          // [N * MP] work-item descriptors, longest first (MFMA path):
                           //   {n, part, first page, pages} of a sequence's own pages or
@@ -103,6 +104,8 @@ struct Params {
     int grouped;       // 1: kv = h / G, 0: kv = h % Hkv
     int q_f32;         // Q / out dtype: 1 f32, 0 bf16
 };
+
+__device__ __forceinline__ size_t qrow(const Params &p, int n) { return p.q_rows ? (size_t)p.q_rows[n] : (size_t)n; }
 
 __device__ __forceinline__ int qhead_of(const Params &p, int kvh, int j, int G) {
     return p.grouped ? kvh * G + j : kvh + j * p.num_kv_heads;
@@ -407,7 +410,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
 
     // B fragment of query row (n, qh): this lane group's DG dims as KK bf16x8.
     auto load_q = [&](int n, int qh, bf16x8 *qf) {
-        const size_t qb = ((size_t)n * H + qh) * D + (size_t)grp * DG;
+        const size_t qb = (qrow(p, n) * H + qh) * D + (size_t)grp * DG;
         if (p.q_f32) {
             const float *qq = (const float *)p.q + qb;
 #pragma unroll
@@ -624,7 +627,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             if (col < G) {
                 if (ns == 0 && nparts <= 1) {  // the whole context: write the output row
                     const float inv = l[0] > 0.0f ? vscale / l[0] : 0.0f;
-                    const size_t ob = ((size_t)n * H + qh) * D;
+                    const size_t ob = (qrow(p, n) * H + qh) * D;
                     if (p.q_f32) {
                         f32x4 o2[DT][2];
 #pragma unroll
@@ -683,7 +686,7 @@ __global__ void __launch_bounds__(kWave) decode_generic_kernel(Params p) {
 
     for (int i = lane; i < G * D; i += kWave) {
         int j = i / D, d = i % D;
-        q_s[i] = load_q(p, ((size_t)n * H + qhead_of(p, kvh, j, G)) * D + d);
+        q_s[i] = load_q(p, (qrow(p, n) * H + qhead_of(p, kvh, j, G)) * D + d);
     }
     __syncthreads();
     float ks = 1.0f, vs = 1.0f;
@@ -769,7 +772,7 @@ __global__ void __launch_bounds__(kWave) decode_generic_kernel(Params p) {
 #pragma unroll
             for (int c = 0; c < kMaxDSlots; ++c) {
                 int d = lane + c * kWave;
-                if (d < D) store_out(p, ((size_t)n * H + qh) * D + d, o[j][c] * vs * inv);
+                if (d < D) store_out(p, (qrow(p, n) * H + qh) * D + d, o[j][c] * vs * inv);
             }
         } else {
             const size_t slot = ((size_t)n * H + qh) * p.max_parts + part;
@@ -828,7 +831,7 @@ __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-        if (lane + 64 * c < D) store_out(p, ((size_t)n * p.num_heads + h) * D + lane + 64 * c, acc[c] * inv);
+        if (lane + 64 * c < D) store_out(p, (qrow(p, n) * p.num_heads + h) * D + lane + 64 * c, acc[c] * inv);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -958,7 +961,8 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                      void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
                      int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                      float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                     void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg) {
+                     void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
+                     const int32_t *q_rows) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: q dtype must be f32 or bf16");
     if (!valid_dtype(kv_dtype))
@@ -1011,6 +1015,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.seq_lens = seq_lens;
     p.k_scales = k_scales;
     p.v_scales = v_scales;
+    p.q_rows = q_rows;
     char *ws = (char *)workspace;
     p.eff_len = (int32_t *)(ws + w.eff);
     p.items = (int4 *)(ws + w.map);
@@ -1084,7 +1089,7 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
                     void *stream) {
     return zk::paged_decode(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, seq_lens, num_seqs,
                             num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, num_blocks, scale,
-                            mapping, k_scales, v_scales, workspace, workspace_bytes, stream, nullptr);
+                            mapping, k_scales, v_scales, workspace, workspace_bytes, stream, nullptr, nullptr);
 }
 
 }  // extern "C"

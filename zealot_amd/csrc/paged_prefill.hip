@@ -42,7 +42,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWave = 64;
 constexpr int kRows = 64;            // query rows per item (4 MFMA tiles)
 constexpr int kTiles = kRows / 16;
-constexpr int kMaxBins = 2048;       // page-count bins of the longest-first sort
+constexpr int kMaxBins = zk::kPrefillMaxPages;  // page-count bins of the longest-first sort
 constexpr float kRescaleSlack = 8.0f;  // lazy-rescale slack, log2 units
 
 struct PParams {
@@ -51,7 +51,9 @@ struct PParams {
     const char *v_pool;
     void *out;            // [T, H, D], dtype of q
     const int32_t *bt;    // [N, max_blocks]
-    const int64_t *cu_q;  // [N + 1] chunk rows per sequence
+    const int64_t *cu_q;  // [N + 1] chunk rows per sequence (or, when q_off is set,
+    const int64_t *q_off; //  sequence n's rows are q_off[n] .. q_off[n] + q_len[n])
+    const int32_t *q_len;
     const int32_t *start; // [N] cached tokens before each chunk
     const float *k_scales;
     const float *v_scales;
@@ -64,13 +66,18 @@ struct PParams {
     int grouped, q_f32, causal;
 };
 
+__device__ __forceinline__ int chunk_len(const PParams &p, int n) {
+    return p.q_off ? p.q_len[n] : (int)(p.cu_q[n + 1] - p.cu_q[n]);
+}
+__device__ __forceinline__ int64_t chunk_row0(const PParams &p, int n) { return p.q_off ? p.q_off[n] : p.cu_q[n]; }
+
 __device__ __forceinline__ int qhead_of(const PParams &p, int kvh, int j, int G) {
     return p.grouped ? kvh * G + j : kvh + j * p.num_kv_heads;
 }
 
 // Pages a query tile reads: up to its last row's visibility limit.
 __device__ __forceinline__ int tile_pages(const PParams &p, int n, int qt) {
-    const int len = (int)(p.cu_q[n + 1] - p.cu_q[n]);
+    const int len = chunk_len(p, n);
     const int last = min(len, (qt + 1) * p.tq);  // rows of the tile end here
     const int lim = p.causal ? p.start[n] + last : p.start[n] + len;
     const int vis = min(lim, p.eff[n]);
@@ -85,7 +92,7 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
     hist[2 * t + 1] = 0;
     // effective contexts: one wave per sequence, eight loads in flight per lane
     for (int n = wave; n < p.num_seqs; n += 16) {
-        const int want = p.start[n] + (int)(p.cu_q[n + 1] - p.cu_q[n]);
+        const int want = p.start[n] + chunk_len(p, n);
         const int cap = p.max_blocks * p.block_size;
         const int len = max(0, min(want, cap));
         const int pages = (len + p.block_size - 1) / p.block_size;
@@ -111,7 +118,7 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
     __syncthreads();
     auto bin = [&](int pages) { return kMaxBins - 1 - min(pages, kMaxBins - 1); };  // longest first
     for (int n = t; n < p.num_seqs; n += 1024) {
-        const int tiles = (int)((p.cu_q[n + 1] - p.cu_q[n] + p.tq - 1) / p.tq);
+        const int tiles = (chunk_len(p, n) + p.tq - 1) / p.tq;
         for (int qt = 0; qt < tiles; ++qt) atomicAdd(&hist[bin(tile_pages(p, n, qt))], 1);
     }
     __syncthreads();
@@ -131,7 +138,7 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
     const int total = sums[1023];
     __syncthreads();
     for (int n = t; n < p.num_seqs; n += 1024) {
-        const int tiles = (int)((p.cu_q[n + 1] - p.cu_q[n] + p.tq - 1) / p.tq);
+        const int tiles = (chunk_len(p, n) + p.tq - 1) / p.tq;
         for (int qt = 0; qt < tiles; ++qt) {
             const int pages = tile_pages(p, n, qt);
             const int pos = atomicAdd(&hist[bin(pages)], 1);
@@ -221,8 +228,8 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
         const int kvh = item % Hkv;
         const int4 desc = p.items[item / Hkv];
         const int n = desc.x, qt = desc.y, np = desc.z;
-        const int len = (int)(p.cu_q[n + 1] - p.cu_q[n]), st = p.start[n], eff = p.eff[n];
-        const int64_t row0 = p.cu_q[n] + (int64_t)qt * p.tq;  // first q row of the tile
+        const int len = chunk_len(p, n), st = p.start[n], eff = p.eff[n];
+        const int64_t row0 = chunk_row0(p, n) + (int64_t)qt * p.tq;  // first q row of the tile
 
         // rows: column col of tile t is row r = 16 t + col = token r / G, head r % G
         bf16x8 qf[T][KK];
@@ -465,7 +472,28 @@ int max_items_for(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads
     return (int)std::min<int64_t>(m, 0x3fffffff);
 }
 
+int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
+                 void *out, const int32_t *block_tables, const int64_t *cu_seqlens_q, const int64_t *q_off,
+                 const int32_t *q_len, const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads,
+                 int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
+                 float scale, int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
+                 void *workspace, size_t workspace_bytes, void *stream);
+
 }  // namespace
+
+int zk::paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool,
+                           zk_dtype kv_dtype, void *out, const int32_t *block_tables, const int64_t *q_off,
+                           const int32_t *q_len, const int32_t *start_pos, int num_seqs, int64_t total_q,
+                           int num_heads, int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq,
+                           int64_t num_blocks, float scale, int causal, zk_gqa_mapping mapping,
+                           const float *k_scales, const float *v_scales, void *workspace, size_t workspace_bytes,
+                           void *stream) {
+    if (!q_off || !q_len)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: paged prefill: NULL row offsets");
+    return prefill_impl(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, nullptr, q_off, q_len, start_pos,
+                        num_seqs, total_q, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq,
+                        num_blocks, scale, causal, mapping, k_scales, v_scales, workspace, workspace_bytes, stream);
+}
 
 extern "C" {
 
@@ -481,6 +509,24 @@ int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                      int max_blocks_per_seq, int64_t num_blocks, float scale, int causal, zk_gqa_mapping mapping,
                      const float *k_scales, const float *v_scales, void *workspace, size_t workspace_bytes,
                      void *stream) {
+    if (num_seqs > 0 && total_q > 0 && !cu_seqlens_q)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: NULL pointer");
+    return prefill_impl(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, cu_seqlens_q, nullptr, nullptr,
+                        start_pos, num_seqs, total_q, num_heads, num_kv_heads, head_dim, block_size,
+                        max_blocks_per_seq, num_blocks, scale, causal, mapping, k_scales, v_scales, workspace,
+                        workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
+                 void *out, const int32_t *block_tables, const int64_t *cu_seqlens_q, const int64_t *q_off,
+                 const int32_t *q_len, const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads,
+                 int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
+                 float scale, int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
+                 void *workspace, size_t workspace_bytes, void *stream) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: q dtype must be f32 or bf16");
     if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
@@ -492,8 +538,7 @@ int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     if (mapping != ZK_GQA_GROUPED && mapping != ZK_GQA_MODULO)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: bad gqa mapping");
     const int G = num_heads / num_kv_heads;
-    if ((kv_dtype != ZK_BF16 && kv_dtype != ZK_FP8_E4M3) || block_size != 16 ||
-        (head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 8))
+    if (!zk::paged_prefill_supported(kv_dtype, head_dim, block_size, num_heads, num_kv_heads))
         return set_error(ZK_ERR_INVALID_ARGUMENT,
                          "Internal error: zk_paged_prefill: needs bf16 or fp8 pools, block_size 16, head_dim 64 "
                          "or 128 and H/Hkv in {1, 2, 4, 8}");
@@ -501,7 +546,7 @@ int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const 
         return set_error(ZK_ERR_INVALID_ARGUMENT,
                          "Internal error: zk_paged_prefill: max_blocks_per_seq above " + std::to_string(kMaxBins));
     if (num_seqs == 0 || total_q == 0) return ZK_OK;
-    if (!q || !k_pool || !v_pool || !out || !block_tables || !cu_seqlens_q || !start_pos || !workspace)
+    if (!q || !k_pool || !v_pool || !out || !block_tables || !start_pos || !workspace)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: NULL pointer");
     const bool fp8 = kv_dtype == ZK_FP8_E4M3;
     if (fp8 != (k_scales != nullptr && v_scales != nullptr))
@@ -519,6 +564,8 @@ int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.out = out;
     p.bt = block_tables;
     p.cu_q = cu_seqlens_q;
+    p.q_off = q_off;
+    p.q_len = q_len;
     p.start = start_pos;
     p.k_scales = k_scales;
     p.v_scales = v_scales;
@@ -564,4 +611,11 @@ int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     return ZK_OK;
 }
 
-}  // extern "C"
+}  // namespace
+
+bool zk::paged_prefill_supported(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads) {
+    if (num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return false;
+    const int G = num_heads / num_kv_heads;
+    return (kv_dtype == ZK_BF16 || kv_dtype == ZK_FP8_E4M3) && block_size == 16 &&
+           (head_dim == 64 || head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
+}

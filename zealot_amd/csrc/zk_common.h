@@ -55,17 +55,33 @@ struct PrefixGroups {
     int num_sg;
     long total_shared_pages;
 };
-// zk_paged_decode with optional shared prefixes (pg may be null).
+// zk_paged_decode with optional shared prefixes (pg may be null) and an
+// optional device map from sequence to q / out row (q_rows may be null).
 int paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
                  void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                  float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                 void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg);
+                 void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
+                 const int32_t *q_rows);
+// zk_paged_prefill with the chunk rows of sequence n given as a device
+// offset and length (q_off[n], q_len[n]) instead of cu_seqlens_q; total_q is
+// an upper bound of the rows.
+int paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
+                       void *out, const int32_t *block_tables, const int64_t *q_off, const int32_t *q_len,
+                       const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads, int num_kv_heads,
+                       int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks, float scale,
+                       int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
+                       void *workspace, size_t workspace_bytes, void *stream);
 size_t paged_decode_workspace(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq, int block_size,
                               bool shared);
 // Whether paged_decode runs shared-prefix items for this shape (otherwise pg
 // is ignored and every sequence reads its whole table).
 bool paged_decode_shares_prefixes(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads);
+// Whether paged_prefill / paged_prefill_rows run this shape (the MFMA kernel's
+// shapes: bf16 or fp8 pools, block_size 16, head_dim 64 or 128, H/Hkv in {1,2,4,8}).
+// Longest block table (pages per sequence) paged_prefill accepts.
+constexpr int kPrefillMaxPages = 2048;
+bool paged_prefill_supported(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads);
 
 inline int elt_size(int dt) { return dt == ZK_F32 ? 4 : dt == ZK_BF16 ? 2 : 1; }
 inline bool valid_dtype(int dt) { return dt == ZK_F32 || dt == ZK_BF16 || dt == ZK_FP8_E4M3; }

@@ -58,6 +58,17 @@ def _batch(ids) -> SeqBatch:
     return ids if isinstance(ids, SeqBatch) else SeqBatch(ids)
 
 
+def _counts(num_tokens, n: int):
+    if isinstance(num_tokens, ctypes.Array):
+        arr = num_tokens
+    else:
+        vals = [int(x) for x in num_tokens]
+        arr = (ctypes.c_int32 * max(1, len(vals)))(*vals)
+        if len(vals) != n:
+            raise ValueError("num_tokens must hold one count per id")
+    return arr
+
+
 class KVCache:
     """kv_cache.rs:51-102.  One HBM slab holds every layer's K and V pool."""
 
@@ -169,6 +180,16 @@ class KVCache:
         _lib.check(_lib.lib().zk_cache_append_kv_batch(self._h, layer, b.arr, n, k.data_ptr(),
                                                        v.data_ptr(), dt))
 
+    def write_batch(self, layer: int, ids, num_tokens, k, v) -> None:
+        """Mixed step write: sequence ids[i] receives num_tokens[i] tokens
+        (packed in batch order in k, v [sum(num_tokens), Hkv, D]) at its
+        cached_tokens position; the last layer advances every sequence."""
+        b = _batch(ids)
+        nt = _counts(num_tokens, len(b))
+        dt = self._kv(k, v, int(sum(nt)))
+        _lib.check(_lib.lib().zk_cache_write_batch(self._h, layer, b.arr, ctypes.addressof(nt), len(b),
+                                                   k.data_ptr(), v.data_ptr(), dt))
+
     # -- decode --------------------------------------------------------------
     def paged_decode(self, layer: int, ids, q, out=None, scale=None, mapping="grouped"):
         """Decode attention for registered sequences `ids` (batch order; a list
@@ -185,6 +206,26 @@ class KVCache:
         m = {"grouped": _lib.GQA_GROUPED, "modulo": _lib.GQA_MODULO}[mapping]
         _lib.check(_lib.lib().zk_cache_paged_decode(self._h, layer, b.arr, n, q.data_ptr(),
                                                     zk_dtype(q), _dev(out, "out"), h, float(scale), m))
+        return out
+
+    def attention_batch(self, layer: int, ids, num_tokens, q, out=None, scale=None, mapping="grouped"):
+        """Mixed step attention after write_batch: the num_tokens[i] rows of
+        sequence ids[i] (packed in batch order in q [sum(num_tokens), H, D])
+        are its last num_tokens[i] tokens at this layer, attended causally."""
+        _dev(q, "q")
+        b = _batch(ids)
+        nt = _counts(num_tokens, len(b))
+        rows, h, d = q.shape
+        if rows != sum(nt) or d != self.head_dim:
+            raise ValueError("q must be [sum(num_tokens), H, head_dim]")
+        if out is None:
+            out = torch.empty_like(q)
+        if scale is None:
+            scale = 1.0 / math.sqrt(d)
+        m = {"grouped": _lib.GQA_GROUPED, "modulo": _lib.GQA_MODULO}[mapping]
+        _lib.check(_lib.lib().zk_cache_attention_batch(self._h, layer, b.arr, ctypes.addressof(nt), len(b),
+                                                       q.data_ptr(), zk_dtype(q), _dev(out, "out"), h,
+                                                       float(scale), m))
         return out
 
     def decode_sharing(self):
