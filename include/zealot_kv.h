@@ -91,6 +91,11 @@ int zk_bm_reference(zk_block_manager *bm, zk_block_handle handle);
 size_t zk_bm_available(const zk_block_manager *bm);
 size_t zk_bm_num_gpu_blocks(const zk_block_manager *bm); /* block_manager.rs:75-78 */
 size_t zk_bm_block_size(const zk_block_manager *bm);     /* block_manager.rs:80-83 */
+/* check (block_manager.rs:151-164, private there): OK for a live handle;
+ * BlockNotAllocated for an id out of range or a free block, StaleHandle on a
+ * generation mismatch.  The KV cache uses it to reject stale handles it is
+ * asked to bind. */
+int zk_bm_check(zk_block_manager *bm, zk_block_handle handle);
 /* Current refcount of a block (0 when free).  The reference keeps this
  * private (block_manager.rs:47); the KV cache needs it to decide copy-on-write. */
 size_t zk_bm_refcount(const zk_block_manager *bm, uint64_t block_id);
@@ -209,6 +214,21 @@ int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *id
 int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids,
                          const int32_t *num_tokens, int n, const void *k, const void *v,
                          zk_dtype src_dtype);
+/* Block tables from the caller's handles: sequence ids[i]'s table becomes
+ * blocks[o_i .. o_i + num_blocks[i]) (packed in batch order), registering the
+ * sequence on first use.  This is how a scheduler that shares `bm` with the
+ * cache hands over Sequence.blocks (scheduler.rs:60) instead of the cache
+ * allocating its own (kv_cache.rs:127-164, which nothing in the reference
+ * calls).  The handles stay the caller's: release_seq does not free them, and
+ * fork_seq, alloc_block and a copy-on-write on a bound sequence fail.  All
+ * checks run before anything changes: stale or free handles (zk_bm_check), a
+ * table longer than max_blocks_per_seq, an id bound twice, an id the cache
+ * allocated itself, fewer blocks than the written tokens need, and, when
+ * tokens_before is given, a sequence whose cached_tokens differ from it (the
+ * runner and the scheduler disagree).  One table-update launch per call. */
+int zk_cache_bind_blocks(zk_kv_cache *c, zk_block_manager *bm, const char *const *ids, int n,
+                         const zk_block_handle *blocks, const size_t *num_blocks,
+                         const size_t *tokens_before);
 /* fp8 pools: set the per-(layer, kv_head) dequant scales of a sequence
  * (k_scales/v_scales: host arrays of num_layers * Hkv floats). */
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales,

@@ -1,7 +1,8 @@
-"""The C ABI library: loads, exports every symbol include/zealot_kv.h declares,
+"""The C ABI library: loads, exports every symbol include/*.h declares,
 and rejects bad arguments on the host before any GPU work (no compute calls
 here, so these run without a GPU)."""
 import ctypes
+import glob
 import os
 import re
 import subprocess
@@ -13,12 +14,15 @@ from zealot_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "zealot_kv.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(zk_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(zk_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_the_boundary():
@@ -43,8 +47,9 @@ def test_exports_with_nm():
     assert set(declared_functions()) <= exported
 
 
-def test_header_compiles_as_c():
-    src = '#include "zealot_kv.h"\nint main(void){return ZK_OK;}\n'
+@pytest.mark.parametrize("header", ["zealot_kv.h", "zealot_sched.h"])
+def test_header_compiles_as_c(header):
+    src = f'#include "{header}"\nint main(void){{return ZK_OK;}}\n'
     r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only",
                         "-I", os.path.dirname(HEADER), "-x", "c", "-"], input=src,
                        capture_output=True, text=True)

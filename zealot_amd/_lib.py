@@ -1,4 +1,5 @@
-"""ctypes binding of libzealot_kv.so (the C ABI declared in include/zealot_kv.h).
+"""ctypes binding of libzealot_kv.so (the C ABI declared in include/zealot_kv.h and
+include/zealot_sched.h).
 
 The library is the product: there is no Python or CPU fallback.  If the
 shared library is missing, importing any op raises immediately.
@@ -35,6 +36,32 @@ class BlockHandleC(ctypes.Structure):
     _fields_ = [("block_id", ctypes.c_uint64), ("generation", ctypes.c_uint64)]
 
 
+class SchedConfigC(ctypes.Structure):
+    _fields_ = [("max_num_seqs", ctypes.c_size_t), ("block_size", ctypes.c_size_t),
+                ("num_gpu_blocks", ctypes.c_size_t), ("max_prefill_tokens", ctypes.c_size_t),
+                ("prefill_chunk_size", ctypes.c_size_t)]
+
+
+class SchedEntryC(ctypes.Structure):
+    _fields_ = [("request_id", ctypes.c_char_p), ("is_prefill", ctypes.c_int),
+                ("is_final_chunk", ctypes.c_int), ("num_tokens", ctypes.c_size_t),
+                ("tokens_before", ctypes.c_size_t), ("len", ctypes.c_size_t),
+                ("num_blocks", ctypes.c_size_t), ("blocks", ctypes.POINTER(BlockHandleC)),
+                ("block_offset", ctypes.c_size_t)]
+
+
+class SchedOutputC(ctypes.Structure):
+    _fields_ = [("batch", ctypes.POINTER(SchedEntryC)), ("batch_len", ctypes.c_size_t),
+                ("preempted", ctypes.POINTER(ctypes.c_char_p)), ("num_preempted", ctypes.c_size_t),
+                ("blocks", ctypes.POINTER(BlockHandleC))]
+
+
+class SchedSeqInfoC(ctypes.Structure):
+    _fields_ = [("state", ctypes.c_int), ("is_prefill", ctypes.c_int), ("prompt_len", ctypes.c_size_t),
+                ("output_len", ctypes.c_size_t), ("prefill_pos", ctypes.c_size_t),
+                ("chunk_size", ctypes.c_size_t), ("len", ctypes.c_size_t), ("num_blocks", ctypes.c_size_t)]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
@@ -42,7 +69,7 @@ _SZ = ctypes.c_size_t
 _F = ctypes.c_float
 _CP = ctypes.c_char_p
 
-# name -> (restype, argtypes); every symbol declared in include/zealot_kv.h.
+# name -> (restype, argtypes); every symbol declared in include/*.h.
 SIGNATURES = {
     "zk_last_error": (ctypes.c_char_p, []),
     "zk_abi_version": (_I, []),
@@ -55,6 +82,7 @@ SIGNATURES = {
     "zk_bm_num_gpu_blocks": (_SZ, [_P]),
     "zk_bm_block_size": (_SZ, [_P]),
     "zk_bm_refcount": (_SZ, [_P, ctypes.c_uint64]),
+    "zk_bm_check": (_I, [_P, BlockHandleC]),
     "zk_append": (_I, [_P, _P, _I, _P, _P, _I, _P, _I64, _I, _I, _I, _I64, _P, _P, _P, _P]),
     "zk_fp8_scales": (_I, [_P, _I, _P, _I, _I, _I, _P, _P]),
     "zk_gather": (_I, [_P, _P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I64, _P]),
@@ -74,6 +102,7 @@ SIGNATURES = {
     "zk_cache_store_kv": (_I, [_P, _SZ, _CP, _P, _P, _I, _SZ, _SZ]),
     "zk_cache_append_kv": (_I, [_P, _SZ, _CP, _P, _P, _I]),
     "zk_cache_append_kv_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _P, _I]),
+    "zk_cache_bind_blocks": (_I, [_P, _P, ctypes.POINTER(_CP), _I, _P, _P, _P]),
     "zk_cache_write_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _P, _I]),
     "zk_cache_set_fp8_scales": (_I, [_P, _CP, _P, _P]),
     "zk_cache_block_table_ptr": (_I, [_P, _CP, ctypes.POINTER(_P)]),
@@ -90,6 +119,22 @@ SIGNATURES = {
     "zk_timing_reset": (_I, []),
     "zk_timing_query": (_I, [_CP, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
     "zk_stream_copy": (_I, [_P, _P, _SZ, _P]),
+    "zk_sched_create": (_I, [ctypes.POINTER(SchedConfigC), _P, ctypes.POINTER(_P)]),
+    "zk_sched_destroy": (None, [_P]),
+    "zk_sched_block_manager": (_P, [_P]),
+    "zk_sched_make_sequence": (_I, [_P, _CP, _P, _SZ, _SZ, _I, ctypes.POINTER(_P)]),
+    "zk_sequence_destroy": (None, [_P]),
+    "zk_sched_add": (_I, [_P, _P]),
+    "zk_sched_schedule": (_I, [_P, ctypes.POINTER(SchedOutputC)]),
+    "zk_sched_push_token": (_I, [_P, _CP, _I64]),
+    "zk_sched_mark_prefilled": (_I, [_P, _CP]),
+    "zk_sched_promote_to_decoding": (None, [_P, _CP]),
+    "zk_sched_advance_prefill": (None, [_P, _CP]),
+    "zk_sched_finish": (_I, [_P, _CP, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "zk_sched_cancel": (_I, [_P, _CP, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "zk_sched_is_idle": (_I, [_P]),
+    "zk_sched_step_input": (_I, [_P, _CP, ctypes.POINTER(_I64), ctypes.POINTER(_SZ)]),
+    "zk_sched_seq_info": (_I, [_P, _CP, ctypes.POINTER(SchedSeqInfoC)]),
 }
 
 _lib = None

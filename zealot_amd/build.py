@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(HERE, "libzealot_kv.so")
-SOURCES = ["status.cpp", "timing.cpp", "block_manager.cpp", "kv_ops.hip", "paged_decode.hip", "paged_prefill.hip", "kv_cache.cpp"]
+SOURCES = ["status.cpp", "timing.cpp", "block_manager.cpp", "kv_ops.hip", "paged_decode.hip", "paged_prefill.hip", "kv_cache.cpp", "scheduler.cpp"]
 ARCH = "gfx950"
 HIPFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall",

@@ -129,6 +129,14 @@ int zk_bm_reference(zk_block_manager *bm, zk_block_handle h) {
     return ZK_OK;
 }
 
+int zk_bm_check(zk_block_manager *bm, zk_block_handle h) {
+    if (!bm) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_bm_check: NULL manager");
+    if (int rc = check(bm, h)) return rc;
+    if (bm->refcount[h.block_id].load(std::memory_order_acquire) == 0)
+        return zk::set_error(ZK_ERR_BLOCK_NOT_ALLOCATED, "Block " + std::to_string(h.block_id) + " is not allocated");
+    return ZK_OK;
+}
+
 size_t zk_bm_available(const zk_block_manager *bm) {
     if (!bm) return 0;
     auto *m = const_cast<zk_block_manager *>(bm);

@@ -41,6 +41,7 @@ namespace {
 struct SeqState {
     std::vector<zk_block_handle> handles;
     zk_block_manager *bm = nullptr;
+    bool borrowed = false;        // handles owned by the caller (zk_cache_bind_blocks)
     size_t cached_tokens = 0;     // tokens written at the last layer
     size_t block_offset = 0;
     size_t max_blocks = 0;
@@ -225,6 +226,11 @@ int flush_tables(zk_kv_cache *c) {
 // nothing has been copied and the fresh blocks are returned.
 int cow_blocks(zk_kv_cache *c, const std::vector<std::pair<SeqState *, size_t>> &targets) {
     if (targets.empty()) return ZK_OK;
+    for (const auto &t : targets)
+        if (t.first->borrowed)  // the caller owns these handles: it must not see them replaced
+            return set_error(ZK_ERR_FAILED_PRECONDITION,
+                             "Failed precondition: KVCache: copy-on-write of a block whose handle the caller "
+                             "owns (bound sequence)");
     const size_t n = targets.size();
     std::vector<zk_block_handle> fresh(n);
     std::vector<int32_t> pairs(2 * n);
@@ -461,6 +467,9 @@ int zk_cache_alloc_block(zk_kv_cache *c, const char *id, zk_block_manager *bm, s
     if (s->bm && s->bm != bm)
         return set_error(ZK_ERR_FAILED_PRECONDITION,
                          "Failed precondition: KVCache alloc_block: sequence uses another BlockManager");
+    if (s->borrowed)
+        return set_error(ZK_ERR_FAILED_PRECONDITION,
+                         "Failed precondition: KVCache alloc_block: the sequence's blocks are bound by the caller");
     if (zk_bm_num_gpu_blocks(bm) > c->num_blocks)
         return set_error(ZK_ERR_FAILED_PRECONDITION,
                          "Failed precondition: KVCache alloc_block: BlockManager larger than the pool");
@@ -487,6 +496,7 @@ int zk_cache_release_seq(zk_kv_cache *c, const char *id) {
     int first_rc = ZK_OK;
     std::string first_msg;
     for (const auto &h : s->handles) {
+        if (s->borrowed) break;  // the caller frees its own handles
         int rc = zk_bm_free(s->bm, h);
         if (rc && !first_rc) {
             first_rc = rc;
@@ -507,6 +517,9 @@ int zk_cache_fork_seq(zk_kv_cache *c, const char *parent, const char *child) {
     if (int rc = find_seq(c, parent, &p)) return rc;
     if (!child) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache fork: NULL child");
     if (c->seqs.count(child)) return set_error(ZK_ERR_ALREADY_EXISTS, std::string("Already exists: seq ") + child);
+    if (p->borrowed)
+        return set_error(ZK_ERR_FAILED_PRECONDITION,
+                         "Failed precondition: KVCache fork: the parent's blocks are owned by the caller");
     if (c->free_slots.empty())
         return set_error(ZK_ERR_FAILED_PRECONDITION, "Failed precondition: KVCache: all sequence slots in use");
     DeviceGuard g(c->device);
@@ -637,6 +650,80 @@ int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *id
                              const void *v, zk_dtype src_dtype) {
     std::vector<int32_t> ones(n > 0 ? (size_t)n : 0, 1);
     return zk_cache_write_batch(c, layer, ids, ones.data(), n, k, v, src_dtype);
+}
+
+int zk_cache_bind_blocks(zk_kv_cache *c, zk_block_manager *bm, const char *const *ids, int n,
+                         const zk_block_handle *blocks, const size_t *num_blocks, const size_t *tokens_before) {
+    if (!c || !bm || (n > 0 && (!ids || !num_blocks)))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache bind_blocks: NULL argument");
+    if (n <= 0) return ZK_OK;
+    if (zk_bm_block_size(bm) != c->block_size || zk_bm_num_gpu_blocks(bm) > c->num_blocks)
+        return set_error(ZK_ERR_FAILED_PRECONDITION,
+                         "Failed precondition: KVCache bind_blocks: BlockManager does not match the pool");
+    // validate everything before changing anything
+    size_t total = 0, fresh = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!ids[i]) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache bind_blocks: NULL id");
+        for (int j = 0; j < i; ++j)
+            if (std::strcmp(ids[j], ids[i]) == 0)
+                return set_error(ZK_ERR_INVALID_ARGUMENT,
+                                 std::string("Internal error: KVCache bind_blocks: seq ") + ids[i] + " twice");
+        if (num_blocks[i] > c->max_blocks_per_seq)
+            return set_error(ZK_ERR_SEQUENCE_TOO_LONG,
+                             "Sequence too long: worst case needs " + std::to_string(num_blocks[i]) +
+                                 " blocks, pool capacity is " + std::to_string(c->max_blocks_per_seq));
+        auto it = c->seqs.find(ids[i]);
+        const size_t have = it == c->seqs.end() ? 0 : it->second.cached_tokens;
+        if (it == c->seqs.end()) {
+            ++fresh;
+        } else if (!it->second.borrowed) {
+            return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: KVCache bind_blocks: seq ") +
+                                                             ids[i] + " owns its blocks (alloc_block / fork_seq)");
+        } else if (it->second.bm != bm) {
+            return set_error(ZK_ERR_FAILED_PRECONDITION,
+                             "Failed precondition: KVCache bind_blocks: sequence uses another BlockManager");
+        }
+        if (tokens_before && tokens_before[i] != have)
+            return set_error(ZK_ERR_FAILED_PRECONDITION,
+                             std::string("Failed precondition: KVCache bind_blocks: seq ") + ids[i] + " holds " +
+                                 std::to_string(have) + " tokens, the caller expects " +
+                                 std::to_string(tokens_before[i]));
+        if (have > num_blocks[i] * c->block_size)
+            return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: KVCache bind_blocks: seq ") +
+                                                             ids[i] + " would lose written tokens");
+        if (num_blocks[i] && !blocks)
+            return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache bind_blocks: NULL blocks");
+        for (size_t j = 0; j < num_blocks[i]; ++j)
+            if (int rc = zk_bm_check(bm, blocks[total + j])) return rc;  // stale handles rejected
+        total += num_blocks[i];
+    }
+    if (fresh > c->free_slots.size())
+        return set_error(ZK_ERR_FAILED_PRECONDITION, "Failed precondition: KVCache: all sequence slots in use");
+    DeviceGuard g(c->device);
+    size_t off = 0;
+    for (int i = 0; i < n; ++i) {
+        auto it = c->seqs.find(ids[i]);
+        if (it == c->seqs.end()) {
+            SeqState st;
+            st.max_blocks = c->max_blocks_per_seq;
+            st.layer_len.assign(c->num_layers, 0);
+            st.slot = c->free_slots.back();
+            st.borrowed = true;
+            st.bm = bm;
+            c->free_slots.pop_back();
+            it = c->seqs.emplace(ids[i], std::move(st)).first;  // free slots' rows hold -1
+        }
+        SeqState &st = it->second;
+        const zk_block_handle *h = blocks + off;
+        for (size_t j = 0; j < num_blocks[i]; ++j)
+            if (j >= st.handles.size() || st.handles[j].block_id != h[j].block_id)
+                queue_table_entry(c, st, j, (int32_t)h[j].block_id);
+        for (size_t j = num_blocks[i]; j < st.handles.size(); ++j) queue_table_entry(c, st, j, -1);
+        st.handles.assign(h, h + num_blocks[i]);
+        for (size_t &l : st.layer_len) l = std::min(l, num_blocks[i] * c->block_size);
+        off += num_blocks[i];
+    }
+    return flush_tables(c);
 }
 
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales, const float *v_scales) {
