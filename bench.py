@@ -8,7 +8,8 @@ also measures the chunked-prefill KV append (C3: 64 x 512 tokens at
 non-aligned offsets, bf16), the fp8-KV decode (C5: 512 sequences, context
 U[1024, 16384]) and prefix sharing with copy-on-write through the stateful
 KVCache (C4: 16 prefixes x 2048+r tokens x 32 layers, 128 forks, 64 decode
-steps) and the causal chunked-prefill attention of C3's chunks, and reports
+steps), the causal chunked-prefill attention of C3's chunks and one layer of
+a mixed runner step (252 decodes + 4 chunks through the KVCache), and reports
 them as extra fields.
 
 Algorithmic bytes (unique bytes that must cross HBM):
@@ -472,6 +473,89 @@ def bench_prefill(args, torch, ops, lib):
     return res
 
 
+def bench_mixed(args, torch, lib):
+    """One layer of a runner step through the KVCache, as the scheduler hands
+    it over: 252 decoding sequences (context U[512, 8192]) and 4 prompt chunks
+    of 512 tokens (starts U[0, 4096)), 32/8 heads, D = 128, bf16.  Timed:
+    zk_cache_write_batch + zk_cache_attention_batch for the whole batch (one
+    append launch; the decode rows as one paged decode, the chunks as one
+    chunked-prefill launch), beside the decode-only and chunk-only halves and
+    the reference's per-sequence pattern (append_kv / store_kv + a one-sequence
+    attention call each, cuda_runner.rs:274-461).  Layer 0 of a 2-layer cache is
+    rewritten each step, so the work is the same every step."""
+    from zealot_amd import BlockManager, KVCache
+    from zealot_amd.kv_cache import SeqBatch
+    ND, NC, C, H, Hkv, D, BS = 252, 4, 512, 32, 8, 128, 16
+    rng = np.random.default_rng(SEED + 7)
+    dec_ctx = rng.integers(512, 8193, ND)
+    starts = rng.integers(0, 4096, NC)
+    total = [int(x) for x in dec_ctx] + [int(s) + C for s in starts]
+    pages = [(t + BS - 1) // BS for t in total]
+    nb = sum(pages) + 16
+    dev = torch.device("cuda", 0)
+    bm = BlockManager(nb, BS)
+    cache = KVCache(nb, BS, 2, Hkv, D, dtype=torch.bfloat16, max_seqs=ND + NC, max_blocks_per_seq=max(pages))
+    ids = [f"d{i}" for i in range(ND)] + [f"c{i}" for i in range(NC)]
+    for sid, p in zip(ids, pages):
+        cache.register_seq(sid, p)
+        for _ in range(p):
+            cache.alloc_block(sid, bm)
+    # fill both layers up to the tokens before the step (decode: ctx - 1, chunk: start)
+    before = [int(x) - 1 for x in dec_ctx] + [int(s) for s in starts]
+    g = torch.Generator(device=dev).manual_seed(SEED + 8)
+    allb = SeqBatch(ids)
+    T0 = sum(before)
+    for layer in range(2):
+        k = torch.randn((T0, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((T0, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+        cache.write_batch(layer, allb, before, k, v)
+        del k, v
+    nt = [1] * ND + [C] * NC
+    T = sum(nt)
+    k = torch.randn((T, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((T, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn((T, H, D), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    decb, chb = SeqBatch(ids[:ND]), SeqBatch(ids[ND:])
+    log(f"mixed: {ND} decodes + {NC} chunks of {C}; {nb} blocks")
+
+    def mixed(_):
+        cache.write_batch(0, allb, nt, k, v)
+        cache.attention_batch(0, allb, nt, q, out=out)
+
+    def dec_only(_):
+        cache.write_batch(0, decb, nt[:ND], k[:ND], v[:ND])
+        cache.attention_batch(0, decb, nt[:ND], q[:ND], out=out[:ND])
+
+    def chunks_only(_):
+        cache.write_batch(0, chb, nt[ND:], k[ND:], v[ND:])
+        cache.attention_batch(0, chb, nt[ND:], q[ND:], out=out[ND:])
+
+    def per_seq(_):  # the reference's loop: one sequence per call
+        row = 0
+        for i, sid in enumerate(ids):
+            n = nt[i]
+            if n == 1:
+                cache.append_kv(0, sid, k[row:row + 1], v[row:row + 1])
+            else:
+                cache.store_kv(0, sid, k[row:row + n], v[row:row + n], before[i], n)
+            cache.attention_batch(0, [sid], [n], q[row:row + n], out=out[row:row + n])
+            row += n
+
+    ms = timed(mixed, args.steps, args.warmup, torch)
+    ms_dec = timed(dec_only, args.steps, args.warmup, torch)
+    ms_ch = timed(chunks_only, args.steps, args.warmup, torch)
+    ms_loop = timed(per_seq, max(2, args.steps // 10), 1, torch)
+    kv_dec = sum(int(x) for x in dec_ctx) * 2 * Hkv * D * 2
+    res = {"ms_per_step": ms, "decode_only_ms": ms_dec, "chunks_only_ms": ms_ch, "per_sequence_loop_ms": ms_loop,
+           "speedup_vs_per_sequence_loop": ms_loop / ms, "tokens_per_step": T,
+           "decode_kv_gbps_in_mixed_step": kv_dec / (ms * 1e-3) / 1e9,
+           "shape": {"decodes": ND, "chunks": NC, "chunk": C, "num_heads": H, "num_kv_heads": Hkv, "head_dim": D}}
+    del cache, k, v, q, out
+    torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 def cpu_model() -> str:
@@ -516,7 +600,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4", "prefill"], default=None,
+    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4", "prefill", "mixed"], default=None,
                     help="run one workload (for profiler passes)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
@@ -535,7 +619,7 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     result = {}
-    dec = lens = app = fp8 = c4 = pre = None
+    dec = lens = app = fp8 = c4 = pre = mix = None
     if args.only in (None, "decode"):
         dec, lens = bench_decode(args, torch, ops, lib, "bf16")
         log(f"decode bf16: {dec['ms_per_step']:.4f} ms {dec['gbps']:.1f} GB/s")
@@ -553,6 +637,10 @@ def main() -> int:
         pre = bench_prefill(args, torch, ops, lib)
         log(f"prefill: {pre['ms_per_step']:.3f} ms {pre['tflops']:.1f} TFLOP/s "
             f"(kernel {pre['roofline']['achieved']:.1f} TFLOP/s)")
+    if args.only in (None, "mixed"):
+        mix = bench_mixed(args, torch, lib)
+        log(f"mixed step: {mix['ms_per_step']:.3f} ms (decode-only {mix['decode_only_ms']:.3f}, chunks-only "
+            f"{mix['chunks_only_ms']:.3f}, per-sequence loop {mix['per_sequence_loop_ms']:.2f})")
     cpu = None
     if args.only is None and not args.no_cpu_baseline:
         cpu = cpu_baseline(lens, args.cpu_sample_seqs)
@@ -561,8 +649,10 @@ def main() -> int:
     if head is None and c4 is not None:  # --only c4
         head = {"gbps": c4["decode_step"]["logical_gbps"], "ms_per_step": c4["decode_step"]["ms_per_step"],
                 "roofline": None}
-    if head is None:  # --only prefill
+    if head is None and pre is not None:  # --only prefill
         head = {"gbps": pre["tflops"], "ms_per_step": pre["ms_per_step"], "roofline": pre["roofline"]}
+    if head is None:  # --only mixed
+        head = {"gbps": mix["decode_kv_gbps_in_mixed_step"], "ms_per_step": mix["ms_per_step"], "roofline": None}
     result = {
         "metric": METRIC,
         "value": round(head["gbps"], 2),
@@ -587,6 +677,7 @@ def main() -> int:
         "decode_fp8": fp8,
         "prefix_cow_c4": c4,
         "prefill_attention": pre,
+        "runner_step_mixed": mix,
         "gpu": torch.cuda.get_device_name(0),
     }
     if args.only is not None:
