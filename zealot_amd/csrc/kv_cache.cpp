@@ -153,6 +153,10 @@ struct zk_kv_cache {
     uint64_t dec_epoch = ~0ull;
     size_t dec_stride = 0;
     std::vector<const SeqState *> dec_ids;
+    // Second stream for the chunk half of a mixed attention batch, so the
+    // MFMA-bound prefill runs beside the HBM-bound decode (default priority).
+    hipStream_t side = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     int last_sg = 0;          // prefix subgroups of the last paged_decode
     int64_t last_sg_pages = 0;  // and the pages they shared (summed over subgroups)
 
@@ -163,6 +167,10 @@ struct zk_kv_cache {
 
     ~zk_kv_cache() {
         if (stream) (void)hipStreamSynchronize(stream);
+        if (side) (void)hipStreamSynchronize(side);
+        if (fork_ev) (void)hipEventDestroy(fork_ev);
+        if (join_ev) (void)hipEventDestroy(join_ev);
+        if (side) (void)hipStreamDestroy(side);
         if (slab) (void)hipFree(slab);
         if (tables) (void)hipFree(tables);
     }
@@ -886,7 +894,8 @@ int find_seqs(zk_kv_cache *c, const char *const *ids, int n, std::vector<const S
 // off[i] .. off[i] + len[i].
 int prefill_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState *> &seqs,
                   const std::vector<int32_t> &len, const std::vector<int64_t> &off, int64_t total_rows, const void *q,
-                  zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping) {
+                  zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping,
+                  hipStream_t launch) {
     const int n = (int)seqs.size();
     if (n <= 0) return ZK_OK;
     const size_t H = c->num_kv_heads;
@@ -921,13 +930,25 @@ int prefill_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState
     char *d = (char *)c->d_pre.dev.p;
     const float *dks = fp8 ? (const float *)(d + tbl_bytes + off_bytes + 2 * i32_bytes) : nullptr;
     const float *dvs = fp8 ? dks + (size_t)n * H : nullptr;
+    if (launch != c->stream) {  // the launch stream waits for everything queued so far
+        ZK_HIP_CHECK(hipEventRecord(c->fork_ev, c->stream), "KVCache prefill fork");
+        ZK_HIP_CHECK(hipStreamWaitEvent(launch, c->fork_ev, 0), "KVCache prefill fork");
+    }
     return zk::paged_prefill_rows(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
                                   (const int32_t *)d, (const int64_t *)(d + tbl_bytes),
                                   (const int32_t *)(d + tbl_bytes + off_bytes),
                                   (const int32_t *)(d + tbl_bytes + off_bytes + i32_bytes), n, total_rows, num_heads,
                                   (int)H, (int)c->head_dim, (int)c->block_size, (int)stride,
                                   (int64_t)c->num_blocks, scale, 1, mapping, dks, dvs, c->d_pws.p, c->d_pws.cap,
-                                  c->stream);
+                                  launch);
+}
+
+int ensure_side_stream(zk_kv_cache *c) {
+    if (c->side) return ZK_OK;
+    ZK_HIP_CHECK(hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming), "KVCache side stream");
+    ZK_HIP_CHECK(hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming), "KVCache side stream");
+    ZK_HIP_CHECK(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking), "KVCache side stream");
+    return ZK_OK;
 }
 
 }  // namespace
@@ -982,16 +1003,36 @@ int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *id
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache attention batch: too many rows");
     if (!q || !out) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache attention batch: NULL q/out");
     const bool identity = dec.size() == (size_t)n;  // all decode rows, in batch order
+    size_t pre_pages = 0;
+    for (const SeqState *s : pre) pre_pages = std::max(pre_pages, s->handles.size());
+    const bool mfma_prefill = !pre.empty() &&
+                              zk::paged_prefill_supported(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads,
+                                                          (int)c->num_kv_heads) &&
+                              pre_pages <= (size_t)zk::kPrefillMaxPages;
+    if (mfma_prefill) {
+        // chunks first, on the side stream when decodes share the step, so
+        // the two kernels overlap; the cache stream waits for both at the end
+        hipStream_t ps = c->stream;
+        if (!dec.empty()) {
+            if (int rc = ensure_side_stream(c)) return rc;
+            ps = c->side;
+        }
+        int rc = prefill_batch(c, layer, pre, pre_len, pre_off, row, q, q_dtype, out, num_heads, scale, mapping, ps);
+        if (!rc)
+            rc = decode_batch(c, layer, dec, nullptr, identity ? nullptr : &dec_rows, q, q_dtype, out, num_heads,
+                              scale, mapping, true);
+        if (ps != c->stream) {
+            hipError_t e = hipEventRecord(c->join_ev, ps);
+            if (e == hipSuccess) e = hipStreamWaitEvent(c->stream, c->join_ev, 0);
+            if (e != hipSuccess && !rc)
+                rc = set_error(ZK_ERR_HIP, std::string("Internal error: KVCache prefill join: ") + hipGetErrorString(e));
+        }
+        return rc;
+    }
     if (int rc = decode_batch(c, layer, dec, nullptr, identity ? nullptr : &dec_rows, q, q_dtype, out, num_heads,
                               scale, mapping, true))
         return rc;
     if (pre.empty()) return ZK_OK;
-    size_t pre_pages = 0;
-    for (const SeqState *s : pre) pre_pages = std::max(pre_pages, s->handles.size());
-    if (zk::paged_prefill_supported(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads,
-                                    (int)c->num_kv_heads) &&
-        pre_pages <= (size_t)zk::kPrefillMaxPages)
-        return prefill_batch(c, layer, pre, pre_len, pre_off, row, q, q_dtype, out, num_heads, scale, mapping);
     // shapes without the MFMA prefill: every chunk row is a decode of its
     // causal context (start + t + 1 tokens)
     std::vector<const SeqState *> ex;
