@@ -1,0 +1,57 @@
+/*
+ * zealot_dense.h -- C ABI of the dense ops around the paged-KV path (gfx950):
+ * the elementwise / normalisation kernels and projections of a Llama layer
+ * that the reference runner launches around its KV calls
+ * (src/cuda_runner.rs:287-660).  Asynchronous on `stream`; shapes are checked
+ * on the host first and nothing is launched when a check fails.  Tensors are
+ * row-major, f32 or bf16 (zk_dtype of zealot_kv.h) with f32 arithmetic.
+ */
+#ifndef ZEALOT_DENSE_H
+#define ZEALOT_DENSE_H
+
+#include "zealot_kv.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* RMSNorm (attention/kernels/rms_norm.cu:4-55):
+ *   out[i] = s[r] * rsqrt(mean(s[r]^2) + eps) * weight
+ * over rows r = rows ? rows[i] : i (i < num_rows), with s = x, or, when
+ * `residual` is given, s = x + residual (the reference's add_kernel,
+ * activation.cu:14-20, fused in) written to residual_out[i] (which may be
+ * `residual` itself).  dim <= 32768 (bf16) / 16384 (f32) for 16-byte rows,
+ * <= 4096 otherwise.  out / residual_out are packed [num_rows, dim]. */
+int zk_rms_norm(const void *x, const void *residual, const void *weight, void *out,
+                void *residual_out, const int64_t *rows, int64_t num_rows, int64_t dim, float eps,
+                zk_dtype dtype, void *stream);
+
+/* silu_gate_mul (activation.cu:4-12): out[r, c] = silu(gate[r, c]) * up[r, c]
+ * with silu(g) = g / (1 + exp(-g)); gate / up rows are gate_stride /
+ * up_stride elements apart (0 = cols), so the halves of a fused gate|up
+ * projection [rows, 2 * cols] feed it in place. */
+int zk_silu_mul(const void *gate, const void *up, void *out, int64_t rows, int64_t cols,
+                int64_t gate_stride, int64_t up_stride, zk_dtype dtype, void *stream);
+
+/* add_kernel (activation.cu:14-20): out = a + b over n elements. */
+int zk_add(const void *a, const void *b, void *out, int64_t n, zk_dtype dtype, void *stream);
+
+/* embedding_gather_kernel (embedding.cu:4-22): out[t] = table[ids[t]]
+ * (ids: device int64 [num_tokens]); an id outside [0, vocab) gives a zero row
+ * (the reference reads out of bounds). */
+int zk_embedding(const int64_t *ids, const void *table, void *out, int64_t num_tokens, int64_t vocab,
+                 int64_t dim, zk_dtype dtype, void *stream);
+
+/* Projection y[m, n] = x[m, k] . w[n, k]^T (w in nn.Linear layout), the
+ * product of every cublasSgemm_v2 site (attention/cublas.rs:72-114;
+ * cuda_runner.rs:331-369, :483-495, :531-559, :577-589, :627-639), on
+ * hipBLASLt with f32 accumulation.  in_dtype F32 -> out F32; in_dtype BF16 ->
+ * out BF16 or F32 (e.g. f32 logits). */
+int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype in_dtype,
+              zk_dtype out_dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZEALOT_DENSE_H */

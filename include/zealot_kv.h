@@ -210,10 +210,15 @@ int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *id
  * batch.  Writing the last layer advances each sequence by its num_tokens[i].
  * Replaces the per-sequence store_kv / append_kv calls of the runner's step
  * (cuda_runner.rs:274-406, kv_cache.rs:206-356).  Fails before writing
- * anything if a position has no block (kv_cache.rs:234-239) or an id repeats. */
+ * anything if a position has no block (kv_cache.rs:234-239) or an id repeats.
+ * src_token_stride: elements from one token's K (V) row block to the next
+ * (0 = Hkv * D); with a fused QKV projection output [T, (H + 2 Hkv) * D], k
+ * and v point at its K and V columns and the stride is (H + 2 Hkv) * D, so
+ * the append reads them in place (no transpose or copy, cf. the head-major
+ * transposes of cuda_runner.rs:373-392). */
 int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids,
                          const int32_t *num_tokens, int n, const void *k, const void *v,
-                         zk_dtype src_dtype);
+                         zk_dtype src_dtype, int64_t src_token_stride);
 /* Block tables from the caller's handles: sequence ids[i]'s table becomes
  * blocks[o_i .. o_i + num_blocks[i]) (packed in batch order), registering the
  * sequence on first use.  This is how a scheduler that shares `bm` with the
@@ -260,10 +265,13 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
  * One-row entries run as one paged decode (with prefix sharing), longer ones
  * as one chunked-prefill launch (zk_paged_prefill); shapes outside the
  * prefill kernel's run every chunk row as a decode.  Replaces the runner's
- * per-sequence paged_forward (cuda_runner.rs:438-461). */
+ * per-sequence paged_forward (cuda_runner.rs:438-461).  q rows are
+ * q_token_stride elements apart (0 = H * D; a fused QKV output's row length
+ * reads q in place); out rows are packed [rows, H, D]. */
 int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *ids,
                              const int32_t *num_tokens, int n, const void *q, zk_dtype q_dtype,
-                             void *out, int num_heads, float scale, zk_gqa_mapping mapping);
+                             int64_t q_token_stride, void *out, int num_heads, float scale,
+                             zk_gqa_mapping mapping);
 /* Prefix sharing of the last zk_cache_paged_decode: subgroups formed and the
  * pages they shared (sum over subgroups).  No reference counterpart. */
 int zk_cache_decode_sharing(zk_kv_cache *c, int *subgroups, int64_t *shared_pages);

@@ -30,6 +30,11 @@ Parity status of each restated function (how it is pinned, see tests/):
   or_e4m3_from_f32 / or_f32_from_e4m3
       pinned exhaustively against torch.float8_e4m3fn (all 256 codes; all
       in-range bf16 values) -- tests/test_oracle.py.
+  or_rms_norm / or_silu_gate_mul / or_add / or_embedding / linear
+      pinned against numpy float64 restatements of the textbook formulas
+      (RMSNorm, SiLU = g * sigmoid(g), x @ W.T) and closed forms (a constant
+      row normalises to sign(x) * w; silu(0) = 0, silu(g) -> g for large g;
+      index-tagged embedding rows) -- tests/test_oracle_dense.py.
   block_manager_model
       pinned by the reference's known-answer tests (tests/test_block_manager.py,
       block_manager.rs:179-249) and its proptest regression seeds.
@@ -106,6 +111,14 @@ def _declare(L):
     L.or_matmul.argtypes = [_P, _P, _I, _I, _I, _P]
     L.or_repeat_interleave_kv.restype = None
     L.or_repeat_interleave_kv.argtypes = [_P, _I, _I, _I, _I, _P]
+    L.or_rms_norm.restype = None
+    L.or_rms_norm.argtypes = [_P, _P, _P, _I64, _I64, _F]
+    L.or_silu_gate_mul.restype = None
+    L.or_silu_gate_mul.argtypes = [_P, _P, _P, _I64]
+    L.or_add.restype = None
+    L.or_add.argtypes = [_P, _P, _P, _I64]
+    L.or_embedding.restype = None
+    L.or_embedding.argtypes = [_P, _P, _P, _I64, _I64]
 
 
 def _ptr(a):
@@ -255,3 +268,50 @@ def repeat_interleave_kv(src, kv_heads, num_heads, seq_len, head_dim):
     out = np.zeros(num_heads * seq_len * head_dim, dtype=np.float32)
     lib().or_repeat_interleave_kv(_ptr(src), kv_heads, num_heads, seq_len, head_dim, _ptr(out))
     return out
+
+
+# ----------------------------------------------------------------- dense ops
+
+def rms_norm(x, w, eps=1e-6):
+    """rms_norm.cu:4-55 over the rows of x [rows, dim] (f32)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().or_rms_norm(_ptr(x), _ptr(w), _ptr(out), x.shape[0] if x.ndim > 1 else 1, x.shape[-1], eps)
+    return out
+
+
+def silu_gate_mul(g, u):
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    out = np.empty_like(g)
+    lib().or_silu_gate_mul(_ptr(g), _ptr(u), _ptr(out), g.size)
+    return out
+
+
+def add(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().or_add(_ptr(a), _ptr(b), _ptr(out), a.size)
+    return out
+
+
+def embedding(ids, table):
+    ids = np.ascontiguousarray(ids, dtype=np.int64)
+    table = np.ascontiguousarray(table, dtype=np.float32)
+    out = np.empty((ids.size, table.shape[1]), np.float32)
+    lib().or_embedding(_ptr(ids), _ptr(table), _ptr(out), ids.size, table.shape[1])
+    return out
+
+
+def linear(x, w):
+    """y = x @ w.T with or_matmul (attention/mod.rs matmul), w [n, k]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    wt = np.ascontiguousarray(np.asarray(w, dtype=np.float32).T)
+    m, k = x.shape
+    n = wt.shape[1]
+    out = np.empty((m, n), np.float32)
+    lib().or_matmul(_ptr(x), _ptr(wt), m, k, n, _ptr(out))
+    return out
+

@@ -393,3 +393,37 @@ void or_repeat_interleave_kv(const float *src, int kv_heads, int num_heads, int 
                 out[(head * seq_len + pos) * head_dim + dim] = src[(pos * kv_heads + kh) * head_dim + dim];
     }
 }
+
+/* ------------------------------------------------------------ dense ops
+ * rms_norm.cu:4-55: var = sum x^2 over the row; rms = rsqrt(var / dim + eps);
+ * out = x * rms * w.  The sum runs in index order (the kernel's tree order
+ * differs by rounding only). */
+void or_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t dim, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * dim;
+        float var = 0.0f;
+        for (int64_t i = 0; i < dim; ++i) var += xr[i] * xr[i];
+        const float rms = 1.0f / sqrtf(var / (float)dim + eps);
+        for (int64_t i = 0; i < dim; ++i) out[r * dim + i] = xr[i] * rms * w[i];
+    }
+}
+
+/* activation.cu:4-12: out = (g / (1 + exp(-g))) * u. */
+void or_silu_gate_mul(const float *gate, const float *up, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = gate[i];
+        out[i] = (g / (1.0f + expf(-g))) * up[i];
+    }
+}
+
+/* activation.cu:14-20. */
+void or_add(const float *a, const float *b, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+
+/* embedding.cu:4-22: out[t] = table[ids[t]] (ids must be in range). */
+void or_embedding(const int64_t *ids, const float *table, float *out, int64_t n, int64_t dim) {
+    for (int64_t t = 0; t < n; ++t)
+        for (int64_t i = 0; i < dim; ++i) out[t * dim + i] = table[ids[t] * dim + i];
+}
+

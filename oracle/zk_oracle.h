@@ -88,4 +88,10 @@ void or_repeat_interleave_kv(const float *src, int kv_heads, int num_heads, int 
 #ifdef __cplusplus
 }
 #endif
+/* dense ops around the path (rms_norm.cu, activation.cu, embedding.cu) */
+void or_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t dim, float eps);
+void or_silu_gate_mul(const float *gate, const float *up, float *out, int64_t n);
+void or_add(const float *a, const float *b, float *out, int64_t n);
+void or_embedding(const int64_t *ids, const float *table, float *out, int64_t n, int64_t dim);
+
 #endif

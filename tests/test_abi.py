@@ -47,7 +47,7 @@ def test_exports_with_nm():
     assert set(declared_functions()) <= exported
 
 
-@pytest.mark.parametrize("header", ["zealot_kv.h", "zealot_sched.h"])
+@pytest.mark.parametrize("header", ["zealot_kv.h", "zealot_sched.h", "zealot_dense.h"])
 def test_header_compiles_as_c(header):
     src = f'#include "{header}"\nint main(void){{return ZK_OK;}}\n'
     r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only",

@@ -1,0 +1,135 @@
+"""Dense ops around the path (zk_rms_norm, zk_silu_mul, zk_add, zk_embedding,
+zk_linear) on the MI355X against the oracle's restatements of rms_norm.cu,
+activation.cu, embedding.cu and the cublasSgemm_v2 product.
+
+Bars: add and embedding bit-exact (f32 sum / bf16 round of the f32 sum; rows
+copied); f32 rms_norm / silu_mul within 2e-6 relative (f32 rounding order);
+bf16 outputs within one bf16 rounding (2^-8 relative) of the f32 value of the
+same bf16 inputs; f32 linear within 1e-5 relative of the float64 product,
+bf16 linear within 1e-2 of the largest |y| (f32 accumulation, bf16 output)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.gpu_util import announce, as_f32, normal, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _vals(a, dt):
+    return a if dt == "f32" else as_f32(a, oracle.BF16)
+
+
+def _rand(rng, shape, dt, scale=1.0):
+    x = (rng.standard_normal(shape) * scale).astype(np.float32)
+    return x if dt == "f32" else oracle.bf16_bits_from_f32(x).reshape(shape)
+
+
+def _close(got, ref, dt, rtol_f32=2e-6):
+    if dt == "f32":
+        return np.allclose(got, ref, rtol=rtol_f32, atol=rtol_f32 * max(1.0, np.abs(ref).max()))
+    return np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,dim", [(1, 4096), (7, 4096), (5, 1000), (3, 8192), (2, 24), (4, 7)])
+def test_rms_norm(dt, rows, dim):
+    from zealot_amd import dense
+    rng = np.random.default_rng(rows * 7 + dim)
+    x, w = _rand(rng, (rows, dim), dt, 3.0), _rand(rng, (dim,), dt)
+    announce(f"rms_norm {dt} {rows}x{dim}")
+    got = _vals(to_host(dense.rms_norm(to_dev(x), to_dev(w), 1e-6)), dt)
+    ref = oracle.rms_norm(_vals(x, dt), _vals(w, dt), 1e-6)
+    assert _close(got, ref, dt)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_add_rms_norm_fused_in_place_and_selected_rows(dt):
+    from zealot_amd import dense
+    rng = np.random.default_rng(3)
+    rows, dim = 9, 4096
+    x, r, w = _rand(rng, (rows, dim), dt), _rand(rng, (rows, dim), dt), _rand(rng, (dim,), dt)
+    announce(f"add+rms_norm {dt}")
+    rd = to_dev(r)
+    out, res = dense.rms_norm(to_dev(x), to_dev(w), 1e-6, residual=rd, residual_out=rd)
+    s = oracle.add(_vals(x, dt), _vals(r, dt))
+    s_stored = s if dt == "f32" else as_f32(oracle.bf16_bits_from_f32(s).reshape(s.shape), oracle.BF16)
+    assert np.array_equal(_vals(to_host(res), dt), s_stored)  # the new residual, rounded as stored
+    assert _close(_vals(to_host(out), dt), oracle.rms_norm(s_stored, _vals(w, dt), 1e-6), dt)
+    # selected rows: the final norm of the last token of each sequence
+    sel = torch.tensor([8, 0, 3], dtype=torch.int64, device="cuda")
+    out2, res2 = dense.rms_norm(to_dev(x), to_dev(w), 1e-6, residual=to_dev(r), rows=sel)
+    assert np.array_equal(_vals(to_host(res2), dt), s_stored[[8, 0, 3]])
+    assert _close(_vals(to_host(out2), dt), oracle.rms_norm(s_stored[[8, 0, 3]], _vals(w, dt), 1e-6), dt)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,cols", [(5, 14336), (3, 100), (1, 8)])
+def test_silu_mul_on_fused_gate_up(dt, rows, cols):
+    from zealot_amd import dense
+    rng = np.random.default_rng(rows + cols)
+    gu = _rand(rng, (rows, 2 * cols), dt, 4.0)
+    announce(f"silu_mul {dt} {rows}x{cols}")
+    g = to_dev(gu)
+    got = _vals(to_host(dense.silu_mul(g[:, :cols], g[:, cols:])), dt)
+    v = _vals(gu, dt)
+    ref = oracle.silu_gate_mul(np.ascontiguousarray(v[:, :cols]), np.ascontiguousarray(v[:, cols:]))
+    assert _close(got, ref, dt, rtol_f32=4e-6)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("n", [1, 13, 4096 * 33])
+def test_add_bit_exact(dt, n):
+    from zealot_amd import dense
+    rng = np.random.default_rng(n)
+    a, b = _rand(rng, (n,), dt), _rand(rng, (n,), dt)
+    announce(f"add {dt} {n}")
+    got = to_host(dense.add(to_dev(a), to_dev(b)))
+    s = oracle.add(_vals(a, dt), _vals(b, dt))
+    assert np.array_equal(got, s if dt == "f32" else oracle.bf16_bits_from_f32(s).reshape(s.shape))
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_embedding_rows_and_out_of_range(dt):
+    from zealot_amd import dense
+    rng = np.random.default_rng(5)
+    vocab, dim = 1000, 4096
+    table = _rand(rng, (vocab, dim), dt)
+    ids = np.array([5, 999, 0, 5, 1000, -1, 123], np.int64)
+    announce(f"embedding {dt}")
+    got = to_host(dense.embedding(to_dev(ids), to_dev(table)))
+    ok = (ids >= 0) & (ids < vocab)
+    ref = oracle.embedding(ids[ok], _vals(table, dt))
+    assert np.array_equal(_vals(got[ok], dt), ref)
+    assert np.all(got[~ok] == 0)  # the reference reads out of bounds here
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (37, 6144, 4096), (256, 512, 1024), (5, 7, 3)])
+def test_linear_f32(m, n, k):
+    from zealot_amd import dense
+    rng = np.random.default_rng(m + n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    announce(f"linear f32 {m}x{n}x{k}")
+    got = to_host(dense.linear(to_dev(x), to_dev(w)))
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max()) * 4
+    if m * n * k <= 10 ** 6:  # the oracle's scalar product on small shapes
+        assert np.allclose(got, oracle.linear(x, w), rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("m,n,k,out_f32", [(1, 4096, 4096, False), (300, 28672, 4096, False),
+                                           (7, 128256, 4096, True), (64, 4096, 14336, False)])
+def test_linear_bf16(m, n, k, out_f32):
+    from zealot_amd import dense
+    rng = np.random.default_rng(m + n)
+    x = normal(rng, (m, k), oracle.BF16)
+    w = oracle.bf16_bits_from_f32((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)).reshape(n, k)
+    announce(f"linear bf16 {m}x{n}x{k}")
+    y = dense.linear(to_dev(x), to_dev(w), out_dtype=torch.float32 if out_f32 else None)
+    got = to_host(y) if out_f32 else as_f32(to_host(y), oracle.BF16)
+    xs, ws = as_f32(x, oracle.BF16), as_f32(w, oracle.BF16)
+    cols = rng.choice(n, size=min(n, 512), replace=False)  # a sample of outputs against float64
+    ref = xs.astype(np.float64) @ ws[cols].astype(np.float64).T
+    assert np.abs(got[:, cols] - ref).max() <= 1e-2 * np.abs(ref).max()

@@ -1,5 +1,5 @@
-"""ctypes binding of libzealot_kv.so (the C ABI declared in include/zealot_kv.h and
-include/zealot_sched.h).
+"""ctypes binding of libzealot_kv.so (the C ABI declared in include/zealot_kv.h,
+include/zealot_sched.h and include/zealot_dense.h).
 
 The library is the product: there is no Python or CPU fallback.  If the
 shared library is missing, importing any op raises immediately.
@@ -103,7 +103,7 @@ SIGNATURES = {
     "zk_cache_append_kv": (_I, [_P, _SZ, _CP, _P, _P, _I]),
     "zk_cache_append_kv_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _P, _I]),
     "zk_cache_bind_blocks": (_I, [_P, _P, ctypes.POINTER(_CP), _I, _P, _P, _P]),
-    "zk_cache_write_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _P, _I]),
+    "zk_cache_write_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _P, _I, _I64]),
     "zk_cache_set_fp8_scales": (_I, [_P, _CP, _P, _P]),
     "zk_cache_block_table_ptr": (_I, [_P, _CP, ctypes.POINTER(_P)]),
     "zk_cache_k_pool_ptr": (_P, [_P, _SZ]),
@@ -113,12 +113,17 @@ SIGNATURES = {
                                 ctypes.POINTER(_SZ)]),
     "zk_cache_block_ids": (_I, [_P, _CP, ctypes.POINTER(_I64), ctypes.POINTER(_SZ)]),
     "zk_cache_paged_decode": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _I, _P, _I, _F, _I]),
-    "zk_cache_attention_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _I, _P, _I, _F, _I]),
+    "zk_cache_attention_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _I, _I64, _P, _I, _F, _I]),
     "zk_cache_decode_sharing": (_I, [_P, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int64)]),
     "zk_timing_enable": (_I, [_I]),
     "zk_timing_reset": (_I, []),
     "zk_timing_query": (_I, [_CP, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
     "zk_stream_copy": (_I, [_P, _P, _SZ, _P]),
+    "zk_rms_norm": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _I, _P]),
+    "zk_silu_mul": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),
+    "zk_add": (_I, [_P, _P, _P, _I64, _I, _P]),
+    "zk_embedding": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
+    "zk_linear": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _I, _P]),
     "zk_sched_create": (_I, [ctypes.POINTER(SchedConfigC), _P, ctypes.POINTER(_P)]),
     "zk_sched_destroy": (None, [_P]),
     "zk_sched_block_manager": (_P, [_P]),

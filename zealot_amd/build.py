@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(HERE, "libzealot_kv.so")
-SOURCES = ["status.cpp", "timing.cpp", "block_manager.cpp", "kv_ops.hip", "paged_decode.hip", "paged_prefill.hip", "kv_cache.cpp", "scheduler.cpp"]
+SOURCES = ["status.cpp", "timing.cpp", "block_manager.cpp", "kv_ops.hip", "paged_decode.hip", "paged_prefill.hip", "kv_cache.cpp", "scheduler.cpp",
+           "dense_ops.hip", "gemm.cpp"]
 ARCH = "gfx950"
 HIPFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall",
@@ -54,7 +55,9 @@ def build(verbose: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    # hipBLASLt carries the dense projections (gemm.cpp)
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-L/opt/rocm/lib", "-lhipblaslt",
+           "-Wl,-rpath,/opt/rocm/lib", "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

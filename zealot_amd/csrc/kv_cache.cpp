@@ -567,7 +567,7 @@ int zk_cache_append_kv(zk_kv_cache *c, size_t layer, const char *id, const void 
 }
 
 int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,
-                         const void *k, const void *v, zk_dtype src_dtype) {
+                         const void *k, const void *v, zk_dtype src_dtype, int64_t src_token_stride) {
     if (!c || (n > 0 && (!ids || !num_tokens)))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: NULL argument");
     if (layer >= c->num_layers)
@@ -638,9 +638,9 @@ int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids, c
     const int32_t *d_rows = fp8 ? (const int32_t *)(d + slots_bytes) : nullptr;
     const float *d_ks = fp8 ? (const float *)(d + slots_bytes + rows_bytes) : nullptr;
     const float *d_vs = fp8 ? d_ks + (size_t)n * H : nullptr;
-    if (int rc = zk_append(c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, k, v, src_dtype,
-                           (const int64_t *)d, (int64_t)T, (int)H, (int)c->head_dim, (int)bs,
-                           (int64_t)c->num_blocks, d_ks, d_vs, d_rows, c->stream))
+    if (int rc = zk::append(c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, k, v, src_dtype,
+                            src_token_stride, (const int64_t *)d, (int64_t)T, (int)H, (int)c->head_dim, (int)bs,
+                            (int64_t)c->num_blocks, d_ks, d_vs, d_rows, c->stream))
         return rc;
     for (int i = 0; i < n; ++i) {
         SeqState &s = *seqs[i];
@@ -657,7 +657,7 @@ int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids, c
 int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *k,
                              const void *v, zk_dtype src_dtype) {
     std::vector<int32_t> ones(n > 0 ? (size_t)n : 0, 1);
-    return zk_cache_write_batch(c, layer, ids, ones.data(), n, k, v, src_dtype);
+    return zk_cache_write_batch(c, layer, ids, ones.data(), n, k, v, src_dtype, 0);
 }
 
 int zk_cache_bind_blocks(zk_kv_cache *c, zk_block_manager *bm, const char *const *ids, int n,
@@ -802,7 +802,8 @@ namespace {
 // and the lengths are the layer's.
 int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState *> &seqs,
                  const std::vector<int32_t> *lens_in, const std::vector<int32_t> *q_rows, const void *q,
-                 zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping, bool share) {
+                 zk_dtype q_dtype, int64_t q_stride, void *out, int num_heads, float scale, zk_gqa_mapping mapping,
+                 bool share) {
     const int n = (int)seqs.size();
     if (n <= 0) return ZK_OK;
     const size_t H = c->num_kv_heads;
@@ -872,7 +873,8 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
     return zk::paged_decode(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
                             (const int32_t *)c->d_tbl.dev.p, (const int32_t *)d, n, num_heads, (int)H,
                             (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
-                            mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr, drows);
+                            mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr, drows,
+                            q_stride);
 }
 
 // Looks up ids[0..n) (each must be registered; fp8 caches need scales).
@@ -894,7 +896,7 @@ int find_seqs(zk_kv_cache *c, const char *const *ids, int n, std::vector<const S
 // off[i] .. off[i] + len[i].
 int prefill_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState *> &seqs,
                   const std::vector<int32_t> &len, const std::vector<int64_t> &off, int64_t total_rows, const void *q,
-                  zk_dtype q_dtype, void *out, int num_heads, float scale, zk_gqa_mapping mapping,
+                  zk_dtype q_dtype, int64_t q_stride, void *out, int num_heads, float scale, zk_gqa_mapping mapping,
                   hipStream_t launch) {
     const int n = (int)seqs.size();
     if (n <= 0) return ZK_OK;
@@ -940,7 +942,7 @@ int prefill_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState
                                   (const int32_t *)(d + tbl_bytes + off_bytes + i32_bytes), n, total_rows, num_heads,
                                   (int)H, (int)c->head_dim, (int)c->block_size, (int)stride,
                                   (int64_t)c->num_blocks, scale, 1, mapping, dks, dvs, c->d_pws.p, c->d_pws.cap,
-                                  launch);
+                                  launch, q_stride);
 }
 
 int ensure_side_stream(zk_kv_cache *c) {
@@ -964,12 +966,12 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
     DeviceGuard g(c->device);
     std::vector<const SeqState *> seqs;
     if (int rc = find_seqs(c, ids, n, seqs)) return rc;
-    return decode_batch(c, layer, seqs, nullptr, nullptr, q, q_dtype, out, num_heads, scale, mapping, true);
+    return decode_batch(c, layer, seqs, nullptr, nullptr, q, q_dtype, 0, out, num_heads, scale, mapping, true);
 }
 
 int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,
-                             const void *q, zk_dtype q_dtype, void *out, int num_heads, float scale,
-                             zk_gqa_mapping mapping) {
+                             const void *q, zk_dtype q_dtype, int64_t q_token_stride, void *out, int num_heads,
+                             float scale, zk_gqa_mapping mapping) {
     if (!c || (n > 0 && (!ids || !num_tokens)))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache attention batch: NULL argument");
     if (layer >= c->num_layers)
@@ -1017,10 +1019,11 @@ int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *id
             if (int rc = ensure_side_stream(c)) return rc;
             ps = c->side;
         }
-        int rc = prefill_batch(c, layer, pre, pre_len, pre_off, row, q, q_dtype, out, num_heads, scale, mapping, ps);
+        int rc = prefill_batch(c, layer, pre, pre_len, pre_off, row, q, q_dtype, q_token_stride, out, num_heads,
+                               scale, mapping, ps);
         if (!rc)
-            rc = decode_batch(c, layer, dec, nullptr, identity ? nullptr : &dec_rows, q, q_dtype, out, num_heads,
-                              scale, mapping, true);
+            rc = decode_batch(c, layer, dec, nullptr, identity ? nullptr : &dec_rows, q, q_dtype, q_token_stride, out,
+                              num_heads, scale, mapping, true);
         if (ps != c->stream) {
             hipError_t e = hipEventRecord(c->join_ev, ps);
             if (e == hipSuccess) e = hipStreamWaitEvent(c->stream, c->join_ev, 0);
@@ -1029,8 +1032,8 @@ int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *id
         }
         return rc;
     }
-    if (int rc = decode_batch(c, layer, dec, nullptr, identity ? nullptr : &dec_rows, q, q_dtype, out, num_heads,
-                              scale, mapping, true))
+    if (int rc = decode_batch(c, layer, dec, nullptr, identity ? nullptr : &dec_rows, q, q_dtype, q_token_stride, out,
+                              num_heads, scale, mapping, true))
         return rc;
     if (pre.empty()) return ZK_OK;
     // shapes without the MFMA prefill: every chunk row is a decode of its
@@ -1045,7 +1048,8 @@ int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *id
             ex_rows.push_back((int32_t)(pre_off[i] + t));
         }
     }
-    return decode_batch(c, layer, ex, &ex_len, &ex_rows, q, q_dtype, out, num_heads, scale, mapping, false);
+    return decode_batch(c, layer, ex, &ex_len, &ex_rows, q, q_dtype, q_token_stride, out, num_heads, scale, mapping,
+                        false);
 }
 
 int zk_cache_decode_sharing(zk_kv_cache *c, int *subgroups, int64_t *shared_pages) {

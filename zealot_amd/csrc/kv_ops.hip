@@ -45,7 +45,7 @@ __global__ void __launch_bounds__(kThreads)
 append_copy_kernel(const char *__restrict__ k, const char *__restrict__ v, char *__restrict__ k_pool,
                    char *__restrict__ v_pool, const int64_t *__restrict__ slots, uint32_t total,
                    uint32_t chunks_per_row, uint32_t hkv, uint32_t row_bytes, uint32_t block_size,
-                   int64_t num_slots) {
+                   int64_t num_slots, uint64_t src_token_bytes) {
     const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;
     if (idx >= total) return;
     const uint32_t c = idx % chunks_per_row;
@@ -55,7 +55,7 @@ append_copy_kernel(const char *__restrict__ k, const char *__restrict__ v, char 
     const uint32_t kv = r & 1u;
     const uint32_t t = r >> 1;
     const int64_t slot = slots[t];
-    const size_t src_off = ((size_t)t * hkv + h) * row_bytes + (size_t)c * 16;
+    const size_t src_off = (size_t)t * src_token_bytes + (size_t)h * row_bytes + (size_t)c * 16;
     const uint4 data = ld16_nt((kv ? v : k) + src_off);
     if (slot < 0 || slot >= num_slots) return;
     const int64_t blk = slot / block_size, tib = slot % block_size;
@@ -72,7 +72,8 @@ append_fp8_kernel(const char *__restrict__ k, const char *__restrict__ v, uint8_
                   uint8_t *__restrict__ v_pool, const int64_t *__restrict__ slots,
                   const float *__restrict__ k_scales, const float *__restrict__ v_scales,
                   const int32_t *__restrict__ token_row, uint32_t total, uint32_t chunks_per_row,
-                  uint32_t hkv, uint32_t head_dim, uint32_t block_size, int64_t num_slots) {
+                  uint32_t hkv, uint32_t head_dim, uint32_t block_size, int64_t num_slots,
+                  uint64_t src_token_elems) {
     uint32_t idx = blockIdx.x * kThreads + threadIdx.x;
     if (idx >= total) return;
     uint32_t c = idx % chunks_per_row;
@@ -85,7 +86,7 @@ append_fp8_kernel(const char *__restrict__ k, const char *__restrict__ v, uint8_
     if (slot < 0 || slot >= num_slots) return;
     float s = (kv ? v_scales : k_scales)[(size_t)token_row[t] * hkv + h];
     float inv = 1.0f / s;  // IEEE division, identical to the host's
-    size_t elem = ((size_t)t * hkv + h) * head_dim + (size_t)c * 16;
+    size_t elem = (size_t)t * src_token_elems + (size_t)h * head_dim + (size_t)c * 16;
     float x[16];
     if (SRC == ZK_BF16) {
         const char *src = (kv ? v : k) + elem * 2;
@@ -126,7 +127,7 @@ append_elem_kernel(const void *__restrict__ k, const void *__restrict__ v, void 
                    const int64_t *__restrict__ slots, const float *__restrict__ k_scales,
                    const float *__restrict__ v_scales, const int32_t *__restrict__ token_row,
                    uint64_t total, uint32_t hkv, uint32_t head_dim, uint32_t block_size,
-                   int64_t num_slots) {
+                   int64_t num_slots, uint64_t src_token_elems) {
     uint64_t idx = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
     if (idx >= total) return;
     uint64_t d = idx % head_dim;
@@ -137,7 +138,7 @@ append_elem_kernel(const void *__restrict__ k, const void *__restrict__ v, void 
     uint64_t t = r >> 1;
     int64_t slot = slots[t];
     if (slot < 0 || slot >= num_slots) return;
-    uint64_t src_i = (t * hkv + h) * head_dim + d;
+    uint64_t src_i = t * src_token_elems + h * head_dim + d;
     const void *src = kv ? v : k;
     int64_t blk = slot / block_size, tib = slot % block_size;
     uint64_t dst_i = (((uint64_t)blk * hkv + h) * block_size + (uint64_t)tib) * head_dim + d;
@@ -336,6 +337,16 @@ int zk_append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, c
               zk_dtype src_dtype, const int64_t *slot_mapping, int64_t num_tokens, int num_kv_heads,
               int head_dim, int block_size, int64_t num_blocks, const float *k_scales,
               const float *v_scales, const int32_t *token_row, void *stream) {
+    return zk::append(k_pool, v_pool, cache_dtype, k, v, src_dtype, 0, slot_mapping, num_tokens, num_kv_heads,
+                      head_dim, block_size, num_blocks, k_scales, v_scales, token_row, stream);
+}
+
+}  // extern "C"
+
+int zk::append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, const void *v, zk_dtype src_dtype,
+               int64_t src_token_stride, const int64_t *slot_mapping, int64_t num_tokens, int num_kv_heads,
+               int head_dim, int block_size, int64_t num_blocks, const float *k_scales, const float *v_scales,
+               const int32_t *token_row, void *stream) {
     if (!valid_dtype(cache_dtype) || (src_dtype != ZK_F32 && src_dtype != ZK_BF16))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: unsupported dtype");
     if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks <= 0)
@@ -348,11 +359,17 @@ int zk_append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, c
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: fp8 pool needs scales and token_row");
     if (!fp8 && (k_scales || v_scales || token_row))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: scales given for a non-fp8 pool");
+    const int64_t row_elems = (int64_t)num_kv_heads * head_dim;
+    if (src_token_stride == 0) src_token_stride = row_elems;
+    if (src_token_stride < row_elems)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append: source token stride below Hkv * D");
     hipStream_t s = (hipStream_t)stream;
     int64_t num_slots = num_blocks * block_size;
     uint32_t row_bytes = (uint32_t)head_dim * elt_size(cache_dtype);
     uint64_t total_rows = (uint64_t)num_tokens * 2 * num_kv_heads;
-    bool aligned = (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_pool | (uintptr_t)v_pool) & 15u) == 0;
+    const uint64_t src_token_bytes = (uint64_t)src_token_stride * elt_size(src_dtype);
+    bool aligned = (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_pool | (uintptr_t)v_pool) & 15u) == 0 &&
+                   (src_token_bytes % 16) == 0;
     if (aligned && cache_dtype == src_dtype && (row_bytes % 16) == 0 && total_rows * (row_bytes / 16) < (1ull << 31)) {
         uint32_t cpr = row_bytes / 16;
         uint32_t total = (uint32_t)(total_rows * cpr);
@@ -360,7 +377,8 @@ int zk_append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, c
         KernelTimer timer("append", s);
         append_copy_kernel<<<grid, kThreads, 0, s>>>((const char *)k, (const char *)v, (char *)k_pool,
                                                      (char *)v_pool, slot_mapping, total, cpr,
-                                                     num_kv_heads, row_bytes, block_size, num_slots);
+                                                     num_kv_heads, row_bytes, block_size, num_slots,
+                                                     src_token_bytes);
         return check_launch("zk_append");
     }
     if (aligned && fp8 && (head_dim % 16) == 0 && total_rows * (head_dim / 16) < (1ull << 31)) {
@@ -371,11 +389,13 @@ int zk_append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, c
         if (src_dtype == ZK_BF16)
             append_fp8_kernel<ZK_BF16><<<grid, kThreads, 0, s>>>(
                 (const char *)k, (const char *)v, (uint8_t *)k_pool, (uint8_t *)v_pool, slot_mapping,
-                k_scales, v_scales, token_row, total, cpr, num_kv_heads, head_dim, block_size, num_slots);
+                k_scales, v_scales, token_row, total, cpr, num_kv_heads, head_dim, block_size, num_slots,
+                (uint64_t)src_token_stride);
         else
             append_fp8_kernel<ZK_F32><<<grid, kThreads, 0, s>>>(
                 (const char *)k, (const char *)v, (uint8_t *)k_pool, (uint8_t *)v_pool, slot_mapping,
-                k_scales, v_scales, token_row, total, cpr, num_kv_heads, head_dim, block_size, num_slots);
+                k_scales, v_scales, token_row, total, cpr, num_kv_heads, head_dim, block_size, num_slots,
+                (uint64_t)src_token_stride);
         return check_launch("zk_append");
     }
     uint64_t total = total_rows * (uint64_t)head_dim;
@@ -386,9 +406,11 @@ int zk_append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, c
     append_elem_kernel<<<(uint32_t)grid, kThreads, 0, s>>>(k, v, k_pool, v_pool, src_dtype, cache_dtype,
                                                            slot_mapping, k_scales, v_scales, token_row,
                                                            total, num_kv_heads, head_dim, block_size,
-                                                           num_slots);
+                                                           num_slots, (uint64_t)src_token_stride);
     return check_launch("zk_append");
 }
+
+extern "C" {
 
 int zk_fp8_scales(const void *x, zk_dtype src_dtype, const int64_t *cu_seqlens, int num_seqs,
                   int num_kv_heads, int head_dim, float *scales, void *stream) {

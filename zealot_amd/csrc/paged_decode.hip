@@ -80,6 +80,7 @@ struct Params {
     const float *k_scales;
     const float *v_scales;
     const int32_t *q_rows;  // optional: q / out row of each sequence
+    int64_t q_stride;       // elements between consecutive q rows (out rows: H * D)
     int32_t *eff_len;     // [N] length after the page walk
     int4 *items;          // [N * MP] work-item descriptors, longest first (MFMA path):
                           //   {n, part, first page, pages} of a sequence's own pages or
@@ -410,7 +411,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
 
     // B fragment of query row (n, qh): this lane group's DG dims as KK bf16x8.
     auto load_q = [&](int n, int qh, bf16x8 *qf) {
-        const size_t qb = (qrow(p, n) * H + qh) * D + (size_t)grp * DG;
+        const size_t qb = qrow(p, n) * (size_t)p.q_stride + (size_t)qh * D + (size_t)grp * DG;
         if (p.q_f32) {
             const float *qq = (const float *)p.q + qb;
 #pragma unroll
@@ -686,7 +687,7 @@ __global__ void __launch_bounds__(kWave) decode_generic_kernel(Params p) {
 
     for (int i = lane; i < G * D; i += kWave) {
         int j = i / D, d = i % D;
-        q_s[i] = load_q(p, (qrow(p, n) * H + qhead_of(p, kvh, j, G)) * D + d);
+        q_s[i] = load_q(p, qrow(p, n) * (size_t)p.q_stride + (size_t)qhead_of(p, kvh, j, G) * D + d);
     }
     __syncthreads();
     float ks = 1.0f, vs = 1.0f;
@@ -962,7 +963,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                      int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                      float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                      void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
-                     const int32_t *q_rows) {
+                     const int32_t *q_rows, int64_t q_stride) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: q dtype must be f32 or bf16");
     if (!valid_dtype(kv_dtype))
@@ -1016,6 +1017,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.k_scales = k_scales;
     p.v_scales = v_scales;
     p.q_rows = q_rows;
+    p.q_stride = q_stride > 0 ? q_stride : (int64_t)num_heads * head_dim;
     char *ws = (char *)workspace;
     p.eff_len = (int32_t *)(ws + w.eff);
     p.items = (int4 *)(ws + w.map);

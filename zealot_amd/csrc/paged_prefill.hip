@@ -54,6 +54,7 @@ struct PParams {
     const int64_t *cu_q;  // [N + 1] chunk rows per sequence (or, when q_off is set,
     const int64_t *q_off; //  sequence n's rows are q_off[n] .. q_off[n] + q_len[n])
     const int32_t *q_len;
+    int64_t q_stride;     // elements between consecutive q rows (out rows: H * D)
     const int32_t *start; // [N] cached tokens before each chunk
     const float *k_scales;
     const float *v_scales;
@@ -242,7 +243,8 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
             const int tok_c = min(tok, len - 1);  // padding rows see what the last row sees
             lim[t] = min(p.causal ? st + tok_c + 1 : st + len, eff);
             if (real[t]) {
-                const size_t qb = ((size_t)(row0 + r / G) * H + qhead_of(p, kvh, r % G, G)) * D + (size_t)grp * DG;
+                const size_t qb = (size_t)(row0 + r / G) * (size_t)p.q_stride + (size_t)qhead_of(p, kvh, r % G, G) * D +
+                                  (size_t)grp * DG;
                 if (p.q_f32) {
                     const float *qq = (const float *)p.q + qb;
 #pragma unroll
@@ -477,7 +479,7 @@ int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void
                  const int32_t *q_len, const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                  float scale, int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                 void *workspace, size_t workspace_bytes, void *stream);
+                 void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride);
 
 }  // namespace
 
@@ -487,12 +489,13 @@ int zk::paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, 
                            int num_heads, int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq,
                            int64_t num_blocks, float scale, int causal, zk_gqa_mapping mapping,
                            const float *k_scales, const float *v_scales, void *workspace, size_t workspace_bytes,
-                           void *stream) {
+                           void *stream, int64_t q_stride) {
     if (!q_off || !q_len)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: paged prefill: NULL row offsets");
     return prefill_impl(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, nullptr, q_off, q_len, start_pos,
                         num_seqs, total_q, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq,
-                        num_blocks, scale, causal, mapping, k_scales, v_scales, workspace, workspace_bytes, stream);
+                        num_blocks, scale, causal, mapping, k_scales, v_scales, workspace, workspace_bytes, stream,
+                        q_stride);
 }
 
 extern "C" {
@@ -514,7 +517,7 @@ int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     return prefill_impl(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, cu_seqlens_q, nullptr, nullptr,
                         start_pos, num_seqs, total_q, num_heads, num_kv_heads, head_dim, block_size,
                         max_blocks_per_seq, num_blocks, scale, causal, mapping, k_scales, v_scales, workspace,
-                        workspace_bytes, stream);
+                        workspace_bytes, stream, 0);
 }
 
 }  // extern "C"
@@ -526,7 +529,7 @@ int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void
                  const int32_t *q_len, const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                  float scale, int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                 void *workspace, size_t workspace_bytes, void *stream) {
+                 void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: q dtype must be f32 or bf16");
     if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
@@ -566,6 +569,7 @@ int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void
     p.cu_q = cu_seqlens_q;
     p.q_off = q_off;
     p.q_len = q_len;
+    p.q_stride = q_stride > 0 ? q_stride : (int64_t)num_heads * head_dim;
     p.start = start_pos;
     p.k_scales = k_scales;
     p.v_scales = v_scales;

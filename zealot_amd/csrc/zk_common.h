@@ -40,6 +40,13 @@ class KernelTimer {
     bool active_ = false;
 };
 
+// zk_append with the source's token stride (elements from one token's K row
+// block to the next; 0 = Hkv * D, the packed layout): K/V can be read in
+// place from a fused projection output.
+int append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, const void *v, zk_dtype src_dtype,
+           int64_t src_token_stride, const int64_t *slot_mapping, int64_t num_tokens, int num_kv_heads, int head_dim,
+           int block_size, int64_t num_blocks, const float *k_scales, const float *v_scales, const int32_t *token_row,
+           void *stream);
 // Internal launcher (kv_ops.hip): base[pairs[i].x] = pairs[i].y for i < n,
 // offsets checked on the device against `limit`.  Used by the KV cache to
 // apply a batch of block-table updates in one launch.
@@ -55,32 +62,33 @@ struct PrefixGroups {
     int num_sg;
     long total_shared_pages;
 };
-// zk_paged_decode with optional shared prefixes (pg may be null) and an
-// optional device map from sequence to q / out row (q_rows may be null).
+// zk_paged_decode with optional shared prefixes (pg may be null), an
+// optional device map from sequence to q / out row (q_rows may be null) and
+// the q row stride in elements (0 = H * D; out rows stay H * D apart).
 int paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
                  void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                  float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                  void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
-                 const int32_t *q_rows);
+                 const int32_t *q_rows, int64_t q_stride = 0);
 // zk_paged_prefill with the chunk rows of sequence n given as a device
 // offset and length (q_off[n], q_len[n]) instead of cu_seqlens_q; total_q is
-// an upper bound of the rows.
+// an upper bound of the rows; q rows are q_stride elements apart (0 = H * D).
 int paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
                        void *out, const int32_t *block_tables, const int64_t *q_off, const int32_t *q_len,
                        const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads, int num_kv_heads,
                        int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks, float scale,
                        int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                       void *workspace, size_t workspace_bytes, void *stream);
+                       void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride = 0);
 size_t paged_decode_workspace(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq, int block_size,
                               bool shared);
 // Whether paged_decode runs shared-prefix items for this shape (otherwise pg
 // is ignored and every sequence reads its whole table).
 bool paged_decode_shares_prefixes(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads);
-// Whether paged_prefill / paged_prefill_rows run this shape (the MFMA kernel's
-// shapes: bf16 or fp8 pools, block_size 16, head_dim 64 or 128, H/Hkv in {1,2,4,8}).
 // Longest block table (pages per sequence) paged_prefill accepts.
 constexpr int kPrefillMaxPages = 2048;
+// Whether paged_prefill / paged_prefill_rows run this shape (the MFMA kernel's
+// shapes: bf16 or fp8 pools, block_size 16, head_dim 64 or 128, H/Hkv in {1,2,4,8}).
 bool paged_prefill_supported(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads);
 
 inline int elt_size(int dt) { return dt == ZK_F32 ? 4 : dt == ZK_BF16 ? 2 : 1; }

@@ -1,0 +1,79 @@
+"""Dense ops around the paged-KV path over the C ABI (include/zealot_dense.h):
+rms_norm (optionally fused with the residual add), silu_mul, add, embedding
+and linear (hipBLASLt).  Torch device tensors in, launches on torch's current
+stream; the kernels are in zealot_amd/csrc/dense_ops.hip and gemm.cpp."""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .ops import _dev, _stream, zk_dtype
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"dense ops take float32 or bfloat16 tensors, got {t.dtype}")
+    return zk_dtype(t)
+
+
+def rms_norm(x, weight, eps: float = 1e-6, residual=None, out=None, residual_out=None, rows=None, stream=None):
+    """out = rms_norm(s) * weight, s = x (+ residual, written to residual_out,
+    which may be `residual`), over x's rows or over the rows listed in `rows`
+    (device int64); rms_norm.cu:4-55."""
+    dim = x.shape[-1]
+    n = rows.numel() if rows is not None else x.numel() // dim
+    if out is None:
+        out = torch.empty((n, dim), dtype=x.dtype, device=x.device)
+    if residual is not None and residual_out is None:
+        residual_out = torch.empty((n, dim), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().zk_rms_norm(
+        _dev(x, "x"), None if residual is None else _dev(residual, "residual"), _dev(weight, "weight"),
+        _dev(out, "out"), None if residual_out is None else _dev(residual_out, "residual_out"),
+        None if rows is None else _dev(rows, "rows", torch.int64), n, dim, float(eps), _dt(x), _stream(stream)))
+    return out if residual is None else (out, residual_out)
+
+
+def silu_mul(gate, up, out=None, stream=None):
+    """silu(gate) * up (activation.cu:4-12); gate / up may be column slices
+    of one [rows, 2 * cols] tensor (a fused gate|up projection)."""
+    rows, cols = gate.shape
+    for name, t in (("gate", gate), ("up", up)):
+        _dev(t, name, contiguous=False)
+        if t.shape != (rows, cols) or t.stride(1) != 1:
+            raise ValueError(f"{name} must be [rows, cols] with contiguous rows")
+    if out is None:
+        out = torch.empty((rows, cols), dtype=gate.dtype, device=gate.device)
+    _lib.check(_lib.lib().zk_silu_mul(gate.data_ptr(), up.data_ptr(), _dev(out, "out"), rows, cols, gate.stride(0),
+                                      up.stride(0), _dt(gate), _stream(stream)))
+    return out
+
+
+def add(a, b, out=None, stream=None):
+    if out is None:
+        out = torch.empty_like(a)
+    _lib.check(_lib.lib().zk_add(_dev(a, "a"), _dev(b, "b"), _dev(out, "out"), a.numel(), _dt(a), _stream(stream)))
+    return out
+
+
+def embedding(ids, table, out=None, stream=None):
+    """table[ids] (embedding.cu:4-22); out-of-range ids give zero rows."""
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((n, table.shape[1]), dtype=table.dtype, device=table.device)
+    _lib.check(_lib.lib().zk_embedding(_dev(ids, "ids", torch.int64), _dev(table, "table"), _dev(out, "out"), n,
+                                       table.shape[0], table.shape[1], _dt(table), _stream(stream)))
+    return out
+
+
+def linear(x, weight, out=None, out_dtype=None, stream=None):
+    """x [m, k] . weight[n, k]^T on hipBLASLt (the cublasSgemm_v2 sites)."""
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or weight.dtype != x.dtype:
+        raise ValueError("weight must be [n, k] of x's dtype")
+    od = out_dtype or x.dtype
+    if out is None:
+        out = torch.empty((m, n), dtype=od, device=x.device)
+    _lib.check(_lib.lib().zk_linear(_dev(x, "x"), _dev(weight, "weight"), _dev(out, "out"), m, n, k, _dt(x),
+                                    zk_dtype(out), _stream(stream)))
+    return out

@@ -58,6 +58,20 @@ def _batch(ids) -> SeqBatch:
     return ids if isinstance(ids, SeqBatch) else SeqBatch(ids)
 
 
+def _token_stride(t, name: str, rows: int, heads: int, dim: int) -> int:
+    """Elements between consecutive token rows of a [rows, heads, dim] device
+    tensor whose inner [heads, dim] block is packed."""
+    _dev(t, name, contiguous=False)
+    if tuple(t.shape) != (rows, heads, dim):
+        raise RuntimeError(f"Internal error: KVCache: {name} has shape {tuple(t.shape)}, expected "
+                           f"{(rows, heads, dim)}")
+    if t.stride(2) != 1 or (heads > 1 and t.stride(1) != dim):
+        raise ValueError(f"{name} must have packed [heads, dim] rows")
+    if rows > 1 and t.stride(0) < heads * dim:
+        raise ValueError(f"{name} rows overlap")
+    return t.stride(0) if rows > 1 else heads * dim
+
+
 def _counts(num_tokens, n: int):
     if isinstance(num_tokens, ctypes.Array):
         arr = num_tokens
@@ -183,12 +197,19 @@ class KVCache:
     def write_batch(self, layer: int, ids, num_tokens, k, v) -> None:
         """Mixed step write: sequence ids[i] receives num_tokens[i] tokens
         (packed in batch order in k, v [sum(num_tokens), Hkv, D]) at its
-        cached_tokens position; the last layer advances every sequence."""
+        cached_tokens position; the last layer advances every sequence.  k and
+        v may be row-strided views (e.g. the K / V columns of a fused QKV
+        projection output): only the token stride may differ from packed."""
         b = _batch(ids)
         nt = _counts(num_tokens, len(b))
-        dt = self._kv(k, v, int(sum(nt)))
+        rows = int(sum(nt))
+        stride = _token_stride(k, "k", rows, self.num_kv_heads, self.head_dim)
+        if _token_stride(v, "v", rows, self.num_kv_heads, self.head_dim) != stride:
+            raise ValueError("k and v must share a token stride")
+        if k.dtype != v.dtype or k.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("k and v must both be float32 or bfloat16")
         _lib.check(_lib.lib().zk_cache_write_batch(self._h, layer, b.arr, ctypes.addressof(nt), len(b),
-                                                   k.data_ptr(), v.data_ptr(), dt))
+                                                   k.data_ptr(), v.data_ptr(), zk_dtype(k), stride))
 
     # -- decode --------------------------------------------------------------
     def paged_decode(self, layer: int, ids, q, out=None, scale=None, mapping="grouped"):
@@ -211,20 +232,22 @@ class KVCache:
     def attention_batch(self, layer: int, ids, num_tokens, q, out=None, scale=None, mapping="grouped"):
         """Mixed step attention after write_batch: the num_tokens[i] rows of
         sequence ids[i] (packed in batch order in q [sum(num_tokens), H, D])
-        are its last num_tokens[i] tokens at this layer, attended causally."""
-        _dev(q, "q")
+        are its last num_tokens[i] tokens at this layer, attended causally.
+        q may be a row-strided view (the Q columns of a fused QKV output);
+        out is packed [rows, H, D]."""
         b = _batch(ids)
         nt = _counts(num_tokens, len(b))
         rows, h, d = q.shape
         if rows != sum(nt) or d != self.head_dim:
             raise ValueError("q must be [sum(num_tokens), H, head_dim]")
+        qs = _token_stride(q, "q", rows, h, d)
         if out is None:
-            out = torch.empty_like(q)
+            out = torch.empty((rows, h, d), dtype=q.dtype, device=q.device)
         if scale is None:
             scale = 1.0 / math.sqrt(d)
         m = {"grouped": _lib.GQA_GROUPED, "modulo": _lib.GQA_MODULO}[mapping]
         _lib.check(_lib.lib().zk_cache_attention_batch(self._h, layer, b.arr, ctypes.addressof(nt), len(b),
-                                                       q.data_ptr(), zk_dtype(q), _dev(out, "out"), h,
+                                                       q.data_ptr(), zk_dtype(q), qs, _dev(out, "out"), h,
                                                        float(scale), m))
         return out
 

@@ -1,0 +1,144 @@
+"""A batched Llama-shaped ModelRunner step on the gfx950 path: the dense ops
+(zealot_amd.dense) around one KV write and one attention call per layer for
+the whole schedule() batch.
+
+Same math as the reference runner's step (src/cuda_runner.rs:271-660):
+embedding -> per layer [RMSNorm -> q/k/v projections -> KV store -> paged
+attention -> o_proj -> residual add -> RMSNorm -> gate/up projections ->
+SiLU(gate) * up -> down projection -> residual add] -> final RMSNorm of each
+sequence's last token -> lm_head logits (no rotary embedding, as in the
+reference).  What differs is the shape of the work:
+  - one launch per op for all sequences of the batch (the reference loops
+    over sequences, cuda_runner.rs:274);
+  - q/k/v come from ONE projection against a fused [(H + 2 Hkv) D, hidden]
+    weight, gate/up from one against [2 I, hidden]; K and V are appended and
+    q attended straight out of the fused output through row strides (no
+    transpose kernels, no copies; cf. cuda_runner.rs:373-392);
+  - each residual add is fused into the RMSNorm that follows it, and the
+    final norm runs only over the last row of each sequence;
+  - weights are random-initialised here (there is no checkpoint loader in
+    this build; the reference loads HF weights, model_loader.rs:241).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import dense
+from .runner import PagedKVRunner, StepPlan
+
+
+@dataclass
+class LlamaConfig:
+    vocab_size: int
+    hidden_size: int
+    intermediate_size: int
+    num_layers: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    rms_eps: float = 1e-6
+
+    @staticmethod
+    def llama3_8b(num_layers: int = 32) -> "LlamaConfig":
+        return LlamaConfig(128256, 4096, 14336, num_layers, 32, 8, 128)
+
+
+@dataclass
+class LayerWeights:
+    attn_norm: torch.Tensor  # [hidden]
+    qkv: torch.Tensor        # [(H + 2 Hkv) D, hidden]: q rows, then k, then v
+    o: torch.Tensor          # [hidden, H D]
+    ffn_norm: torch.Tensor   # [hidden]
+    gate_up: torch.Tensor    # [2 I, hidden]: gate rows, then up
+    down: torch.Tensor       # [hidden, I]
+
+
+@dataclass
+class LlamaWeights:
+    embedding: torch.Tensor  # [vocab, hidden]
+    layers: list
+    final_norm: torch.Tensor  # [hidden]
+    lm_head: torch.Tensor     # [vocab, hidden]
+
+    @staticmethod
+    def random(cfg: LlamaConfig, dtype=torch.bfloat16, device="cuda", seed: int = 0) -> "LlamaWeights":
+        """N(0, 1/fan_in) projections and N(1, 0.1) norm weights (seeded)."""
+        g = torch.Generator(device=device).manual_seed(seed)
+
+        def lin(n, k):
+            return (torch.randn((n, k), generator=g, device=device) / math.sqrt(k)).to(dtype)
+
+        def norm(n):
+            return (1 + 0.1 * torch.randn((n,), generator=g, device=device)).to(dtype)
+
+        H, Hkv, D, hid, I = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden_size, cfg.intermediate_size
+        layers = [LayerWeights(norm(hid), lin((H + 2 * Hkv) * D, hid), lin(hid, H * D), norm(hid),
+                               lin(2 * I, hid), lin(hid, I)) for _ in range(cfg.num_layers)]
+        emb = torch.randn((cfg.vocab_size, hid), generator=g, device=device).to(dtype)
+        return LlamaWeights(emb, layers, norm(hid), lin(cfg.vocab_size, hid))
+
+
+class HipModelRunner:
+    """ModelRunner::step (engine.rs:15-37) for a schedule() batch: returns the
+    f32 logits [len(batch), vocab] of each sequence's last step token."""
+
+    def __init__(self, cfg: LlamaConfig, weights: LlamaWeights, kv: PagedKVRunner):
+        c = kv.cache
+        if (c.num_layers, c.num_kv_heads, c.head_dim) != (cfg.num_layers, cfg.num_kv_heads, cfg.head_dim):
+            raise ValueError("KV cache shape does not match the model")
+        self.cfg, self.w, self.kv = cfg, weights, kv
+
+    def drop_state(self, request_id: str) -> None:
+        self.kv.drop_state(request_id)
+
+    def step(self, out) -> torch.Tensor:
+        """One step over ScheduleOutput `out` (zealot_amd.scheduler)."""
+        plan = self.kv.begin_step(out)
+        if not out.batch:
+            return torch.empty((0, self.cfg.vocab_size), dtype=torch.float32, device=self.w.embedding.device)
+        ids = [t for e in out.batch for t in e.step_input()]
+        dev = self.w.embedding.device
+        ids_dev = torch.tensor(ids, dtype=torch.int64, device=dev)
+        last = torch.tensor(plan_last_rows(plan), dtype=torch.int64, device=dev)
+        return self.forward(plan, ids_dev, last)
+
+    def forward(self, plan: StepPlan, ids: torch.Tensor, last_rows: torch.Tensor) -> torch.Tensor:
+        cfg, w = self.cfg, self.w
+        H, Hkv, D, I = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.intermediate_size
+        T = plan.total_tokens
+        if ids.numel() != T:
+            raise ValueError("one token id per step row")
+        qd, kd = H * D, Hkv * D
+        resid = dense.embedding(ids, w.embedding)  # the residual stream [T, hidden]
+        normed = torch.empty_like(resid)
+        delta = None
+        for layer, lw in enumerate(w.layers):
+            if delta is None:
+                dense.rms_norm(resid, lw.attn_norm, cfg.rms_eps, out=normed)
+            else:  # resid += delta; normed = norm(resid)
+                dense.rms_norm(delta, lw.attn_norm, cfg.rms_eps, residual=resid, out=normed, residual_out=resid)
+            qkv = dense.linear(normed, lw.qkv)
+            q = qkv[:, :qd].view(T, H, D)
+            k = qkv[:, qd:qd + kd].view(T, Hkv, D)
+            v = qkv[:, qd + kd:].view(T, Hkv, D)
+            self.kv.write(layer, plan, k, v)
+            attn = self.kv.attention(layer, plan, q)
+            o = dense.linear(attn.view(T, qd), lw.o)
+            dense.rms_norm(o, lw.ffn_norm, cfg.rms_eps, residual=resid, out=normed, residual_out=resid)
+            gu = dense.linear(normed, lw.gate_up)
+            act = dense.silu_mul(gu[:, :I], gu[:, I:])
+            delta = dense.linear(act, lw.down)
+        final, _ = dense.rms_norm(delta, w.final_norm, cfg.rms_eps, residual=resid, rows=last_rows)
+        return dense.linear(final, w.lm_head, out_dtype=torch.float32)
+
+
+def plan_last_rows(plan: StepPlan) -> list:
+    """Row of each entry's last step token in the packed batch."""
+    rows, o = [], 0
+    for n in plan.num_tokens[:len(plan.ids)]:
+        o += int(n)
+        rows.append(o - 1)
+    return rows
