@@ -8,9 +8,10 @@ also measures the chunked-prefill KV append (C3: 64 x 512 tokens at
 non-aligned offsets, bf16), the fp8-KV decode (C5: 512 sequences, context
 U[1024, 16384]) and prefix sharing with copy-on-write through the stateful
 KVCache (C4: 16 prefixes x 2048+r tokens x 32 layers, 128 forks, 64 decode
-steps), the causal chunked-prefill attention of C3's chunks and one layer of
-a mixed runner step (252 decodes + 4 chunks through the KVCache), and reports
-them as extra fields.
+steps), the causal chunked-prefill attention of C3's chunks, one layer of
+a mixed runner step (252 decodes + 4 chunks through the KVCache) and a full
+32-layer decode step of a Llama-3-8B-shaped model with the dense ops, and
+reports them as extra fields.
 
 Algorithmic bytes (unique bytes that must cross HBM):
   decode  sum(ctx) * 2 * Hkv * D * elt  + Q + O + block-table entries + seq_lens
@@ -556,6 +557,78 @@ def bench_mixed(args, torch, lib):
     return res
 
 
+def bench_model(args, torch, lib):
+    """One decode step of a Llama-3-8B-shaped model (32 layers, 32/8 heads,
+    D = 128, hidden 4096, intermediate 14336, vocab 128256, bf16, random
+    weights) for 64 sequences with contexts U[512, 8192], through
+    HipModelRunner: embedding, per layer fused-add RMSNorm, the fused QKV /
+    o / gate-up / down projections on hipBLASLt, SiLU*up, one KV write and
+    one paged decode for the batch, final norm and f32 lm_head logits.  Each
+    step appends one token per sequence (contexts grow by the step count,
+    < 1 %)."""
+    import ctypes
+    from zealot_amd import BlockManager, KVCache, PagedKVRunner
+    from zealot_amd.kv_cache import SeqBatch
+    from zealot_amd.model import HipModelRunner, LlamaConfig, LlamaWeights
+    from zealot_amd.runner import StepPlan
+    N, BS = 64, 16
+    cfg = LlamaConfig.llama3_8b()
+    rng = np.random.default_rng(SEED + 9)
+    ctx = rng.integers(512, 8193, N)
+    grow = args.warmup + args.steps + max(2, args.steps // 5) + 1
+    pages = [(int(c) + grow + BS - 1) // BS for c in ctx]
+    nb = sum(pages) + 16
+    dev = torch.device("cuda", 0)
+    bm = BlockManager(nb, BS)
+    cache = KVCache(nb, BS, cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, dtype=torch.bfloat16, max_seqs=N,
+                    max_blocks_per_seq=max(pages))
+    ids = [f"s{i}" for i in range(N)]
+    for sid, p in zip(ids, pages):
+        cache.register_seq(sid, p)
+        for _ in range(p):
+            cache.alloc_block(sid, bm)
+    g = torch.Generator(device=dev).manual_seed(SEED + 10)
+    before = [int(c) - 1 for c in ctx]
+    allb = SeqBatch(ids)
+    T0 = sum(before)
+    for layer in range(cfg.num_layers):  # context K/V (values do not matter for timing)
+        kv = torch.randn((T0, cfg.num_kv_heads, cfg.head_dim), generator=g, device=dev).to(torch.bfloat16)
+        cache.write_batch(layer, allb, before, kv, kv)
+        del kv
+    w = LlamaWeights.random(cfg, dtype=torch.bfloat16, seed=SEED + 11)
+    model = HipModelRunner(cfg, w, PagedKVRunner(cache, bm))
+    plan = StepPlan(allb, (ctypes.c_int32 * N)(*([1] * N)), before, N)
+    tok = torch.randint(0, cfg.vocab_size, (N,), generator=g, device=dev)
+    last = torch.arange(N, dtype=torch.int64, device=dev)
+    log(f"model: Llama-3-8B shape, {N} seqs ctx {int(ctx.min())}..{int(ctx.max())}, {nb} blocks")
+
+    def step(_):
+        model.forward(plan, tok, last)
+
+    ms = timed(step, args.steps, args.warmup, torch)
+    prof_steps = max(2, args.steps // 5)
+    lib.zk_timing_reset()
+    lib.zk_timing_enable(1)
+    timed(step, prof_steps, 0, torch)
+    lib.zk_timing_enable(0)
+    per = {}
+    for nm in ("linear", "decode_partials", "decode_reduce", "decode_plan", "decode_seq_info", "append",
+               "rms_norm", "silu_mul", "embedding"):
+        k_ms, k_n = kernel_ms(lib, nm)
+        if k_n:
+            per[nm] = {"ms_per_step": k_ms * k_n / prof_steps, "launches_per_step": k_n / prof_steps}
+    lib.zk_timing_reset()
+    wbytes = sum(t.numel() * 2 for lw in w.layers for t in (lw.qkv, lw.o, lw.gate_up, lw.down)) + w.lm_head.numel() * 2
+    kvbytes = int(sum(int(c) for c in ctx)) * cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
+    res = {"ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), "weight_bytes": wbytes, "kv_bytes": kvbytes,
+           "gbps_weights_plus_kv": (wbytes + kvbytes) / (ms * 1e-3) / 1e9, "kernels": per,
+           "shape": {"model": "Llama-3-8B shape (random bf16 weights)", "layers": cfg.num_layers, "seqs": N,
+                     "ctx": [int(ctx.min()), int(ctx.max())]}}
+    del model, w, cache
+    torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 def cpu_model() -> str:
@@ -600,7 +673,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4", "prefill", "mixed"], default=None,
+    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4", "prefill", "mixed", "model"], default=None,
                     help="run one workload (for profiler passes)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
@@ -619,7 +692,7 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     result = {}
-    dec = lens = app = fp8 = c4 = pre = mix = None
+    dec = lens = app = fp8 = c4 = pre = mix = mdl = None
     if args.only in (None, "decode"):
         dec, lens = bench_decode(args, torch, ops, lib, "bf16")
         log(f"decode bf16: {dec['ms_per_step']:.4f} ms {dec['gbps']:.1f} GB/s")
@@ -641,6 +714,9 @@ def main() -> int:
         mix = bench_mixed(args, torch, lib)
         log(f"mixed step: {mix['ms_per_step']:.3f} ms (decode-only {mix['decode_only_ms']:.3f}, chunks-only "
             f"{mix['chunks_only_ms']:.3f}, per-sequence loop {mix['per_sequence_loop_ms']:.2f})")
+    if args.only in (None, "model"):
+        mdl = bench_model(args, torch, lib)
+        log(f"model decode step: {mdl['ms_per_step']:.3f} ms, {mdl['tokens_per_s']:.0f} tokens/s")
     cpu = None
     if args.only is None and not args.no_cpu_baseline:
         cpu = cpu_baseline(lens, args.cpu_sample_seqs)
@@ -651,8 +727,10 @@ def main() -> int:
                 "roofline": None}
     if head is None and pre is not None:  # --only prefill
         head = {"gbps": pre["tflops"], "ms_per_step": pre["ms_per_step"], "roofline": pre["roofline"]}
-    if head is None:  # --only mixed
+    if head is None and mix is not None:  # --only mixed
         head = {"gbps": mix["decode_kv_gbps_in_mixed_step"], "ms_per_step": mix["ms_per_step"], "roofline": None}
+    if head is None:  # --only model
+        head = {"gbps": mdl["gbps_weights_plus_kv"], "ms_per_step": mdl["ms_per_step"], "roofline": None}
     result = {
         "metric": METRIC,
         "value": round(head["gbps"], 2),
@@ -678,6 +756,7 @@ def main() -> int:
         "prefix_cow_c4": c4,
         "prefill_attention": pre,
         "runner_step_mixed": mix,
+        "model_decode_step": mdl,
         "gpu": torch.cuda.get_device_name(0),
     }
     if args.only is not None:
