@@ -234,6 +234,27 @@ int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids,
 int zk_cache_bind_blocks(zk_kv_cache *c, zk_block_manager *bm, const char *const *ids, int n,
                          const zk_block_handle *blocks, const size_t *num_blocks,
                          const size_t *tokens_before);
+/* ---- KV swap (docs/architecture.md:452-469: swap-out to CPU frees GPU
+ * blocks, preemption prefers it to recompute; no reference code).
+ * enable_swap: pinned host space of num_host_blocks slots, each holding one
+ * block of every pool (2 * num_layers * block_size * Hkv * D elements).
+ * swap_out: the written blocks of each sequence (ceil(tokens / block_size))
+ * are staged through device memory in chunks and copied to host slots, one
+ * DMA per run of consecutive slots; then the sequence's device blocks are
+ * freed to its BlockManager (bound sequences: dropped, the caller frees its
+ * handles) and its table cleared.  Its token counts stay; writes and
+ * attention on it fail until swap_in.  OutOfBlocks (nothing moved) when the
+ * host space is short.
+ * swap_in: the cache allocates fresh blocks from `bm` (or the sequence's own
+ * manager) for a sequence it owns, all or nothing; a bound sequence must have
+ * been given its new handles with zk_cache_bind_blocks first.  The host data
+ * is copied back into them and the host slots freed.  Asynchronous on the
+ * cache stream like every other cache call; release_seq frees host slots. */
+int zk_cache_enable_swap(zk_kv_cache *c, size_t num_host_blocks);
+int zk_cache_swap_space(zk_kv_cache *c, size_t *total, size_t *free_blocks);
+int zk_cache_swap_out(zk_kv_cache *c, const char *const *ids, int n);
+int zk_cache_swap_in(zk_kv_cache *c, const char *const *ids, int n, zk_block_manager *bm);
+int zk_cache_seq_swapped(zk_kv_cache *c, const char *id, int *swapped);
 /* fp8 pools: set the per-(layer, kv_head) dequant scales of a sequence
  * (k_scales/v_scales: host arrays of num_layers * Hkv floats). */
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales,

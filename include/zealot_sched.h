@@ -36,6 +36,8 @@ typedef struct zk_sched_config {
     size_t num_gpu_blocks;     /* block pool capacity (admission control) */
     size_t max_prefill_tokens; /* prompt tokens per step */
     size_t prefill_chunk_size; /* prompt tokens per chunk */
+    size_t swap_blocks;        /* host swap space in blocks (0: preempt by recompute only, the
+                                  reference's policy); see zk_sched_output.swapped_out */
 } zk_sched_config;
 
 /* One batch entry of zk_sched_schedule: a snapshot of the sequence
@@ -62,6 +64,15 @@ typedef struct zk_sched_output {
     const char *const *preempted;
     size_t num_preempted;
     const zk_block_handle *blocks; /* every entry's handles, packed in batch order */
+    /* Preempted by swap this step: the runner moves their KV to host slots
+     * (zk_cache_swap_out) BEFORE any write of this step, since their freed
+     * blocks may already be another entry's.  Re-admitted this step: the
+     * runner binds their new blocks and copies the KV back
+     * (zk_cache_swap_in) before attention. */
+    const char *const *swapped_out;
+    size_t num_swapped_out;
+    const char *const *swapped_in;
+    size_t num_swapped_in;
 } zk_sched_output;
 
 typedef struct zk_scheduler zk_scheduler;
@@ -101,7 +112,9 @@ void zk_sched_advance_prefill(zk_scheduler *s, const char *request_id);
 int zk_sched_finish(zk_scheduler *s, const char *request_id, size_t *prompt_len,
                     size_t *output_len);
 
-/* cancel (scheduler.rs:460-469) -> CancelOutcome (scheduler.rs:191-197). */
+/* cancel (scheduler.rs:460-469) -> CancelOutcome (scheduler.rs:191-197).
+ * A swapped sequence cancelled while waiting is WasWaiting; the runner
+ * releases its host slots (zk_cache_release_seq). */
 typedef enum zk_cancel_outcome {
     ZK_CANCEL_NOT_FOUND = 0,
     ZK_CANCEL_WAS_WAITING = 1, /* prompt_len set, output_len 0 */
@@ -123,6 +136,7 @@ typedef struct zk_seq_info {
     int state;
     int is_prefill;
     size_t prompt_len, output_len, prefill_pos, chunk_size, len, num_blocks;
+    int swapped; /* waiting with its KV in host slots */
 } zk_seq_info;
 int zk_sched_seq_info(zk_scheduler *s, const char *request_id, zk_seq_info *info);
 

@@ -9,7 +9,9 @@ Requests of different prompt lengths run through chunked prefill and decode
 pools -- logits within 2e-4 of the largest |logit| (f32 rounding order of the
 GEMMs and attention); bf16 -- within 6e-2 of the largest |logit| (bf16
 activations between ops, f32 reference) and the same argmax on at least 90 %
-of the rows."""
+of the rows.  A third run squeezes four requests into eight blocks so the
+scheduler preempts by swap (zk_cache_swap_out / _in through the runner) and
+by recompute; the logits must not notice."""
 import numpy as np
 import pytest
 import torch
@@ -19,34 +21,45 @@ from tests.gpu_util import announce
 pytestmark = pytest.mark.gpu
 
 
-def _run(dtype, tol, argmax_frac):
+def _run(dtype, tol, argmax_frac, swap=False):
     import zealot_amd as ze
     from oracle.llama_ref import LlamaRef, weights_to_numpy
-    from zealot_amd import KVCache, PagedKVRunner, Scheduler, SchedulerConfig
+    from zealot_amd import KVCache, PagedKVRunner, Priority, Scheduler, SchedulerConfig
     from zealot_amd.model import HipModelRunner, LlamaConfig, LlamaWeights
     cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_layers=2, num_heads=8,
                       num_kv_heads=2, head_dim=64)
-    NB, BS = 64, 16
+    # with swap: 8 blocks for four requests, so the scheduler preempts by
+    # swap (and once by recompute) while the reference keeps every sequence
+    NB, BS = (8, 16) if swap else (64, 16)
     bm = ze.BlockManager(NB, BS)
     sched = Scheduler(SchedulerConfig(max_num_seqs=4, block_size=BS, num_gpu_blocks=NB, max_prefill_tokens=64,
-                                      prefill_chunk_size=32), block_manager=bm)
+                                      prefill_chunk_size=32, swap_blocks=64 if swap else 0), block_manager=bm)
     cache = KVCache(NB, BS, cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, dtype=dtype, max_seqs=8,
                     max_blocks_per_seq=NB)
+    if swap:
+        cache.enable_swap(64)
     w = LlamaWeights.random(cfg, dtype=dtype, seed=11)
     runner = HipModelRunner(cfg, w, PagedKVRunner(cache, bm))
     ref = LlamaRef(cfg, weights_to_numpy(w))
     rng = np.random.default_rng(12)
-    prompts = {"a": 45, "b": 7, "c": 70}
-    max_new = {"a": 6, "b": 9, "c": 4}
+    if swap:
+        prompts = {"a": 45, "b": 7, "c": 70, "d": 20}
+        max_new = {"a": 20, "b": 30, "c": 12, "d": 25}
+        prio = {"a": Priority.Lowest, "b": Priority.High, "c": Priority.Medium, "d": Priority.Highest}
+    else:
+        prompts = {"a": 45, "b": 7, "c": 70}
+        max_new = {"a": 6, "b": 9, "c": 4}
+        prio = {r: Priority.Medium for r in prompts}
     for rid, p in prompts.items():
-        sched.add(sched.make_sequence(rid, list(rng.integers(0, cfg.vocab_size, p)), max_new[rid]))
-    worst, agree, rows, steps = 0.0, 0, 0, 0
+        sched.add(sched.make_sequence(rid, list(rng.integers(0, cfg.vocab_size, p)), max_new[rid], prio[rid]))
+    worst, agree, rows, steps, swaps = 0.0, 0, 0, 0, 0
     while not sched.is_idle():
         steps += 1
         assert steps < 100
         out = sched.schedule()
         for rid in out.preempted:
             ref.drop(rid)
+        swaps += len(out.swapped_out)
         announce(f"model {dtype} step {steps}: {[(e.request_id, e.num_tokens, e.tokens_before) for e in out.batch]}")
         entries = [(e.request_id, e.step_input(), e.tokens_before) for e in out.batch]
         logits = runner.step(out).cpu().numpy()
@@ -73,6 +86,8 @@ def _run(dtype, tol, argmax_frac):
     assert worst <= tol, worst
     assert agree >= argmax_frac * rows, (agree, rows)
     assert bm.free_blocks == NB
+    if swap:
+        assert swaps >= 1 and cache.swap_space()[1] == 64
 
 
 def test_model_step_f32_matches_reference():
@@ -81,3 +96,11 @@ def test_model_step_f32_matches_reference():
 
 def test_model_step_bf16_close_to_reference():
     _run(torch.bfloat16, 6e-2, 0.9)
+
+
+def test_model_step_with_swap_preemption_matches_reference():
+    """Eight blocks for four requests: sequences are swapped out and back in
+    (and one is recomputed) mid-stream; the logits still follow the
+    reference, which never preempts."""
+    _run(torch.float32, 2e-4, 1.0, swap=True)
+

@@ -284,3 +284,78 @@ def test_duplicate_ids_are_rejected():
     s.schedule()
     with pytest.raises(ZealotError):
         s.add(s.make_sequence("a", [1], 1))
+
+
+# ---------------------------------------------------------------- swap preemption
+def _swap_case(swap_blocks):
+    """_recompute_case's pool (6 blocks of 2 tokens) with host swap space."""
+    s = Scheduler(SchedulerConfig(max_num_seqs=2, block_size=2, num_gpu_blocks=6, max_prefill_tokens=64,
+                                  prefill_chunk_size=4, swap_blocks=swap_blocks))
+    s.add(s.make_sequence("b", [9, 9], 4, Priority.High))
+    s.add(s.make_sequence("a", list(range(6)), 2, Priority.Lowest))
+    tok = iter(range(50, 100))
+    for step in range(4):
+        out = s.schedule()
+        for e in out.batch:
+            _engine_write_back(e, (lambda: next(tok)) if e.request_id == "a" else (lambda: 20 + step))
+        for e in out.batch:
+            if e.is_prefill():
+                s.advance_prefill(e.request_id)
+    return s, out
+
+
+def test_swap_preemption_keeps_progress():
+    s, out = _swap_case(swap_blocks=8)
+    assert out.preempted == [] and out.swapped_out == ["a"]
+    info = s.seq_info("a")
+    assert info["swapped"] == 1 and info["state"] == 0 and not info["is_prefill"] and info["output_len"] == 2
+    assert s.free_blocks() == 3  # a's 4 blocks went back; b took one more
+    s.finish("b")
+    out = s.schedule()
+    assert out.swapped_in == ["a"] and out.swapped_out == []
+    (e,) = out.batch
+    # straight back to decoding: prompt 6 + outputs 2, the last output is the input
+    assert (e.request_id, e.is_prefill(), e.num_tokens, e.tokens_before, e.len()) == ("a", False, 1, 7, 8)
+    assert e.step_input() == [51] and len(e.blocks) == 4
+
+
+def test_swap_space_full_falls_back_to_recompute():
+    s, out = _swap_case(swap_blocks=3)  # a's KV (7 tokens) needs 4 host blocks
+    assert out.swapped_out == [] and out.preempted == ["a"]
+    assert s.seq_info("a")["swapped"] == 0 and s.seq_info("a")["is_prefill"]
+
+
+def test_swap_mid_prefill_resumes_at_its_position():
+    """A sequence swapped while its prompt is half done resumes the prompt
+    where it stopped (the reference restarts it from token 0).  Two 24-token
+    prompts in chunks of 8 over 8 blocks of 4: the high-priority one's third
+    chunk needs the low one's blocks."""
+    s = Scheduler(SchedulerConfig(max_num_seqs=2, block_size=4, num_gpu_blocks=8, max_prefill_tokens=64,
+                                  prefill_chunk_size=8, swap_blocks=16))
+    s.add(s.make_sequence("lo", list(range(100, 124)), 2, Priority.Lowest))
+    s.add(s.make_sequence("hi", list(range(24)), 2, Priority.High))
+    for _ in range(2):
+        out = s.schedule()
+        assert sorted(e.request_id for e in out.batch) == ["hi", "lo"]
+        for e in out.batch:
+            s.advance_prefill(e.request_id)
+    out = s.schedule()
+    assert out.swapped_out == ["lo"] and out.preempted == []
+    info = s.seq_info("lo")
+    assert info["swapped"] == 1 and info["is_prefill"] and info["prefill_pos"] == 16
+    s.finish("hi")
+    out = s.schedule()
+    assert out.swapped_in == ["lo"]
+    (e,) = out.batch
+    assert e.is_prefill() and e.is_final_chunk() and e.tokens_before == 16
+    assert e.step_input() == list(range(116, 124)) and len(e.blocks) == 6
+
+
+def test_cancel_of_a_swapped_sequence_returns_its_host_space():
+    s, out = _swap_case(swap_blocks=4)
+    assert out.swapped_out == ["a"]
+    assert s.cancel("a")[0] == CancelOutcome.WasWaiting
+    # the host space is free again: the same preemption swaps instead of recomputing
+    s.add(s.make_sequence("c", list(range(6)), 2, Priority.Lowest))
+    s.finish("b")
+    assert s.seq_info("c")["swapped"] == 0

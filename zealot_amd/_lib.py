@@ -39,7 +39,7 @@ class BlockHandleC(ctypes.Structure):
 class SchedConfigC(ctypes.Structure):
     _fields_ = [("max_num_seqs", ctypes.c_size_t), ("block_size", ctypes.c_size_t),
                 ("num_gpu_blocks", ctypes.c_size_t), ("max_prefill_tokens", ctypes.c_size_t),
-                ("prefill_chunk_size", ctypes.c_size_t)]
+                ("prefill_chunk_size", ctypes.c_size_t), ("swap_blocks", ctypes.c_size_t)]
 
 
 class SchedEntryC(ctypes.Structure):
@@ -53,13 +53,16 @@ class SchedEntryC(ctypes.Structure):
 class SchedOutputC(ctypes.Structure):
     _fields_ = [("batch", ctypes.POINTER(SchedEntryC)), ("batch_len", ctypes.c_size_t),
                 ("preempted", ctypes.POINTER(ctypes.c_char_p)), ("num_preempted", ctypes.c_size_t),
-                ("blocks", ctypes.POINTER(BlockHandleC))]
+                ("blocks", ctypes.POINTER(BlockHandleC)),
+                ("swapped_out", ctypes.POINTER(ctypes.c_char_p)), ("num_swapped_out", ctypes.c_size_t),
+                ("swapped_in", ctypes.POINTER(ctypes.c_char_p)), ("num_swapped_in", ctypes.c_size_t)]
 
 
 class SchedSeqInfoC(ctypes.Structure):
     _fields_ = [("state", ctypes.c_int), ("is_prefill", ctypes.c_int), ("prompt_len", ctypes.c_size_t),
                 ("output_len", ctypes.c_size_t), ("prefill_pos", ctypes.c_size_t),
-                ("chunk_size", ctypes.c_size_t), ("len", ctypes.c_size_t), ("num_blocks", ctypes.c_size_t)]
+                ("chunk_size", ctypes.c_size_t), ("len", ctypes.c_size_t), ("num_blocks", ctypes.c_size_t),
+                ("swapped", ctypes.c_int)]
 
 
 _P = ctypes.c_void_p
@@ -104,6 +107,11 @@ SIGNATURES = {
     "zk_cache_append_kv_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _P, _I]),
     "zk_cache_bind_blocks": (_I, [_P, _P, ctypes.POINTER(_CP), _I, _P, _P, _P]),
     "zk_cache_write_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _P, _I, _I64]),
+    "zk_cache_enable_swap": (_I, [_P, _SZ]),
+    "zk_cache_swap_space": (_I, [_P, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "zk_cache_swap_out": (_I, [_P, ctypes.POINTER(_CP), _I]),
+    "zk_cache_swap_in": (_I, [_P, ctypes.POINTER(_CP), _I, _P]),
+    "zk_cache_seq_swapped": (_I, [_P, _CP, ctypes.POINTER(ctypes.c_int)]),
     "zk_cache_set_fp8_scales": (_I, [_P, _CP, _P, _P]),
     "zk_cache_block_table_ptr": (_I, [_P, _CP, ctypes.POINTER(_P)]),
     "zk_cache_k_pool_ptr": (_P, [_P, _SZ]),

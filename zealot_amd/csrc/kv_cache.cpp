@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <functional>
 #include <cstdint>
 #include <cstring>
 #include <new>
@@ -42,6 +43,8 @@ struct SeqState {
     std::vector<zk_block_handle> handles;
     zk_block_manager *bm = nullptr;
     bool borrowed = false;        // handles owned by the caller (zk_cache_bind_blocks)
+    bool swapped = false;         // K/V held in host slots (zk_cache_swap_out)
+    std::vector<int32_t> host_slots;  // host slot of block i while swapped
     size_t cached_tokens = 0;     // tokens written at the last layer
     size_t block_offset = 0;
     size_t max_blocks = 0;
@@ -157,6 +160,13 @@ struct zk_kv_cache {
     // MFMA-bound prefill runs beside the HBM-bound decode (default priority).
     hipStream_t side = nullptr;
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    // Swap space: pinned host slots of one block of every pool (all layers,
+    // K and V: 2 * L * block_bytes), lowest free slot first so a sequence's
+    // blocks form long runs (one DMA each); device staging in chunks.
+    char *host_pool = nullptr;
+    size_t host_total = 0;
+    std::vector<int32_t> host_free;  // sorted descending: back() is the lowest
+    DevBuf d_stage, d_swap_ids;
     int last_sg = 0;          // prefix subgroups of the last paged_decode
     int64_t last_sg_pages = 0;  // and the pages they shared (summed over subgroups)
 
@@ -171,6 +181,7 @@ struct zk_kv_cache {
         if (fork_ev) (void)hipEventDestroy(fork_ev);
         if (join_ev) (void)hipEventDestroy(join_ev);
         if (side) (void)hipStreamDestroy(side);
+        if (host_pool) (void)hipHostFree(host_pool);
         if (slab) (void)hipFree(slab);
         if (tables) (void)hipFree(tables);
     }
@@ -287,6 +298,57 @@ int cow_blocks(zk_kv_cache *c, const std::vector<std::pair<SeqState *, size_t>> 
     return rc;
 }
 
+void release_host_slots(zk_kv_cache *c, SeqState &s) {
+    for (int32_t h : s.host_slots) c->host_free.push_back(h);
+    std::sort(c->host_free.begin(), c->host_free.end(), std::greater<int32_t>());
+    s.host_slots.clear();
+    s.swapped = false;
+}
+
+size_t host_slot_bytes(const zk_kv_cache *c) { return 2 * c->num_layers * c->block_bytes(); }
+
+// Moves blocks between the pools and host slots: pairs (slot, device block)
+// sorted by slot, staged through device memory in chunks, one DMA per run of
+// consecutive slots.  out: pools -> host, else host -> pools.
+int swap_move(zk_kv_cache *c, std::vector<std::pair<int32_t, int32_t>> &pairs, bool out) {
+    if (pairs.empty()) return ZK_OK;
+    std::sort(pairs.begin(), pairs.end());
+    const size_t sb = host_slot_bytes(c);
+    constexpr size_t kStageBytes = 512ull << 20;
+    const size_t chunk = std::max<size_t>(1, kStageBytes / sb);
+    const size_t n = pairs.size();
+    std::vector<int32_t> blocks(n);
+    for (size_t i = 0; i < n; ++i) blocks[i] = pairs[i].second;
+    if (int rc = c->d_swap_ids.ensure(n * sizeof(int32_t), "KVCache swap ids")) return rc;
+    if (int rc = upload(c, c->d_swap_ids.p, blocks.data(), n * sizeof(int32_t))) return rc;
+    if (int rc = c->d_stage.ensure(std::min(n, chunk) * sb, "KVCache swap staging")) return rc;
+    char *stage = (char *)c->d_stage.p;
+    for (size_t c0 = 0; c0 < n; c0 += chunk) {
+        const size_t cn = std::min(chunk, n - c0);
+        if (out && (int)cn > 0)
+            if (int rc = zk::swap_stage(c->slab, c->pool_bytes, c->block_bytes(), (int)(2 * c->num_layers),
+                                        (const int32_t *)c->d_swap_ids.p + c0, (int)cn, stage, (int64_t)c->num_blocks,
+                                        true, c->stream))
+                return rc;
+        for (size_t r0 = 0; r0 < cn;) {  // runs of consecutive host slots
+            size_t r1 = r0 + 1;
+            while (r1 < cn && pairs[c0 + r1].first == pairs[c0 + r1 - 1].first + 1) ++r1;
+            char *host = c->host_pool + (size_t)pairs[c0 + r0].first * sb;
+            char *dev = stage + r0 * sb;
+            ZK_HIP_CHECK(hipMemcpyAsync(out ? host : dev, out ? dev : host, (r1 - r0) * sb,
+                                        out ? hipMemcpyDeviceToHost : hipMemcpyHostToDevice, c->stream),
+                         "KVCache swap copy");
+            r0 = r1;
+        }
+        if (!out)
+            if (int rc = zk::swap_stage(c->slab, c->pool_bytes, c->block_bytes(), (int)(2 * c->num_layers),
+                                        (const int32_t *)c->d_swap_ids.p + c0, (int)cn, stage, (int64_t)c->num_blocks,
+                                        false, c->stream))
+                return rc;
+    }
+    return ZK_OK;
+}
+
 int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, const void *k, const void *v,
                  zk_dtype src_dtype, size_t start, size_t n, const char *what) {
     if (layer >= c->num_layers)
@@ -296,6 +358,8 @@ int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, cons
         return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache ") + what + ": bad src dtype");
     if (n == 0) return ZK_OK;
     if (!k || !v) return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache ") + what + ": NULL k/v");
+    if (s.swapped)
+        return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + id + " is swapped out");
     const size_t bs = c->block_size;
     size_t last_idx = (start + n - 1) / bs;
     if (last_idx >= s.handles.size())  // kv_cache.rs:234-239
@@ -478,6 +542,9 @@ int zk_cache_alloc_block(zk_kv_cache *c, const char *id, zk_block_manager *bm, s
     if (s->borrowed)
         return set_error(ZK_ERR_FAILED_PRECONDITION,
                          "Failed precondition: KVCache alloc_block: the sequence's blocks are bound by the caller");
+    if (s->swapped)
+        return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + id +
+                                                         " is swapped out");
     if (zk_bm_num_gpu_blocks(bm) > c->num_blocks)
         return set_error(ZK_ERR_FAILED_PRECONDITION,
                          "Failed precondition: KVCache alloc_block: BlockManager larger than the pool");
@@ -511,6 +578,7 @@ int zk_cache_release_seq(zk_kv_cache *c, const char *id) {
             first_msg = zk_last_error();
         }
     }
+    release_host_slots(c, *s);
     std::vector<int32_t> row(c->max_blocks_per_seq, -1);
     int rc = upload(c, c->table_row(s->slot), row.data(), row.size() * sizeof(int32_t));
     c->free_slots.push_back(s->slot);
@@ -528,6 +596,9 @@ int zk_cache_fork_seq(zk_kv_cache *c, const char *parent, const char *child) {
     if (p->borrowed)
         return set_error(ZK_ERR_FAILED_PRECONDITION,
                          "Failed precondition: KVCache fork: the parent's blocks are owned by the caller");
+    if (p->swapped)
+        return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + parent +
+                                                         " is swapped out");
     if (c->free_slots.empty())
         return set_error(ZK_ERR_FAILED_PRECONDITION, "Failed precondition: KVCache: all sequence slots in use");
     DeviceGuard g(c->device);
@@ -582,6 +653,9 @@ int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids, c
     size_t T = 0;
     for (int i = 0; i < n; ++i) {
         if (int rc = find_seq(c, ids[i], &seqs[i])) return rc;
+        if (seqs[i]->swapped)
+            return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + ids[i] +
+                                                             " is swapped out");
         for (int j = 0; j < i; ++j)
             if (seqs[j] == seqs[i])
                 return set_error(ZK_ERR_INVALID_ARGUMENT,
@@ -732,6 +806,161 @@ int zk_cache_bind_blocks(zk_kv_cache *c, zk_block_manager *bm, const char *const
         off += num_blocks[i];
     }
     return flush_tables(c);
+}
+
+int zk_cache_enable_swap(zk_kv_cache *c, size_t num_host_blocks) {
+    if (!c) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap: NULL cache");
+    if (c->host_pool) return set_error(ZK_ERR_ALREADY_EXISTS, "Already exists: KVCache swap space");
+    if (num_host_blocks == 0 || num_host_blocks > 0x7fffffff)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap: bad host block count");
+    DeviceGuard g(c->device);
+    ZK_HIP_CHECK(hipHostMalloc((void **)&c->host_pool, num_host_blocks * host_slot_bytes(c), hipHostMallocDefault),
+                 "KVCache swap space");
+    c->host_total = num_host_blocks;
+    c->host_free.resize(num_host_blocks);
+    for (size_t i = 0; i < num_host_blocks; ++i) c->host_free[i] = (int32_t)(num_host_blocks - 1 - i);
+    return ZK_OK;
+}
+
+int zk_cache_seq_swapped(zk_kv_cache *c, const char *id, int *swapped) {
+    SeqState *s;
+    if (int rc = find_seq(c, id, &s)) return rc;
+    if (swapped) *swapped = s->swapped ? 1 : 0;
+    return ZK_OK;
+}
+
+int zk_cache_swap_space(zk_kv_cache *c, size_t *total, size_t *free_blocks) {
+    if (!c) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap: NULL cache");
+    if (total) *total = c->host_total;
+    if (free_blocks) *free_blocks = c->host_free.size();
+    return ZK_OK;
+}
+
+int zk_cache_swap_out(zk_kv_cache *c, const char *const *ids, int n) {
+    if (!c || (n > 0 && !ids)) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap_out: NULL argument");
+    if (n <= 0) return ZK_OK;
+    if (!c->host_pool)
+        return set_error(ZK_ERR_FAILED_PRECONDITION, "Failed precondition: KVCache swap_out: no swap space");
+    std::vector<SeqState *> seqs((size_t)n);
+    std::vector<size_t> nblk((size_t)n);
+    size_t need = 0;
+    for (int i = 0; i < n; ++i) {
+        if (int rc = find_seq(c, ids[i], &seqs[i])) return rc;
+        for (int j = 0; j < i; ++j)
+            if (seqs[j] == seqs[i])
+                return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache swap_out: seq ") + ids[i] + " twice");
+        if (seqs[i]->swapped)
+            return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + ids[i] +
+                                                             " is swapped out");
+        size_t written = 0;
+        for (size_t l : seqs[i]->layer_len) written = std::max(written, l);
+        nblk[i] = (written + c->block_size - 1) / c->block_size;
+        need += nblk[i];
+    }
+    if (need > c->host_free.size())
+        return set_error(ZK_ERR_OUT_OF_BLOCKS, "Out of blocks: requested " + std::to_string(need) +
+                                                   ", available " + std::to_string(c->host_free.size()));
+    DeviceGuard g(c->device);
+    std::vector<std::pair<int32_t, int32_t>> pairs;
+    pairs.reserve(need);
+    for (int i = 0; i < n; ++i) {
+        SeqState &s = *seqs[i];
+        s.host_slots.resize(nblk[i]);
+        for (size_t b = 0; b < nblk[i]; ++b) {
+            s.host_slots[b] = c->host_free.back();
+            c->host_free.pop_back();
+            pairs.emplace_back(s.host_slots[b], (int32_t)s.handles[b].block_id);
+        }
+    }
+    int rc = swap_move(c, pairs, true);
+    if (rc) {  // nothing was given up: put the slots back
+        for (int i = 0; i < n; ++i) release_host_slots(c, *seqs[i]);
+        return rc;
+    }
+    // the device blocks are free from here on; later writes into them are
+    // queued after the staging copy on the same stream
+    int first_rc = ZK_OK;
+    std::string first_msg;
+    for (int i = 0; i < n; ++i) {
+        SeqState &s = *seqs[i];
+        for (size_t j = 0; j < s.handles.size(); ++j) {
+            queue_table_entry(c, s, j, -1);
+            if (!s.borrowed) {
+                int r = zk_bm_free(s.bm, s.handles[j]);
+                if (r && !first_rc) {
+                    first_rc = r;
+                    first_msg = zk_last_error();
+                }
+            }
+        }
+        s.handles.clear();
+        s.swapped = true;
+    }
+    rc = flush_tables(c);
+    if (first_rc) return set_error(first_rc, first_msg);
+    return rc;
+}
+
+int zk_cache_swap_in(zk_kv_cache *c, const char *const *ids, int n, zk_block_manager *bm) {
+    if (!c || (n > 0 && !ids)) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap_in: NULL argument");
+    if (n <= 0) return ZK_OK;
+    std::vector<SeqState *> seqs((size_t)n);
+    size_t need = 0;
+    for (int i = 0; i < n; ++i) {
+        if (int rc = find_seq(c, ids[i], &seqs[i])) return rc;
+        for (int j = 0; j < i; ++j)
+            if (seqs[j] == seqs[i])
+                return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache swap_in: seq ") + ids[i] + " twice");
+        SeqState &s = *seqs[i];
+        if (!s.swapped)
+            return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + ids[i] +
+                                                             " is not swapped out");
+        if (s.borrowed) {
+            if (s.handles.size() < s.host_slots.size())
+                return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + ids[i] +
+                                                                 ": bind its new blocks before swap_in");
+        } else {
+            if (!bm && !s.bm)
+                return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap_in: NULL manager");
+            if (bm && s.bm && bm != s.bm)
+                return set_error(ZK_ERR_FAILED_PRECONDITION,
+                                 "Failed precondition: KVCache swap_in: sequence uses another BlockManager");
+            need += s.host_slots.size();
+        }
+    }
+    DeviceGuard g(c->device);
+    // fresh device blocks for the sequences the cache owns: all or nothing
+    std::vector<std::vector<zk_block_handle>> fresh((size_t)n);
+    for (int i = 0; i < n; ++i) {
+        SeqState &s = *seqs[i];
+        if (s.borrowed) continue;
+        zk_block_manager *m = s.bm ? s.bm : bm;
+        for (size_t b = 0; b < s.host_slots.size(); ++b) {
+            zk_block_handle h;
+            if (int rc = zk_bm_allocate(m, &h)) {
+                std::string msg = zk_last_error();
+                for (int j = 0; j <= i; ++j)
+                    for (const auto &x : fresh[j]) (void)zk_bm_free(seqs[j]->bm ? seqs[j]->bm : bm, x);
+                return set_error(rc, msg);
+            }
+            fresh[i].push_back(h);
+        }
+    }
+    std::vector<std::pair<int32_t, int32_t>> pairs;
+    for (int i = 0; i < n; ++i) {
+        SeqState &s = *seqs[i];
+        if (!s.borrowed) {
+            s.bm = s.bm ? s.bm : bm;
+            s.handles = fresh[i];
+            for (size_t j = 0; j < s.handles.size(); ++j) queue_table_entry(c, s, j, (int32_t)s.handles[j].block_id);
+        }
+        for (size_t b = 0; b < s.host_slots.size(); ++b)
+            pairs.emplace_back(s.host_slots[b], (int32_t)s.handles[b].block_id);
+    }
+    if (int rc = flush_tables(c)) return rc;
+    if (int rc = swap_move(c, pairs, false)) return rc;
+    for (int i = 0; i < n; ++i) release_host_slots(c, *seqs[i]);
+    return ZK_OK;
 }
 
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales, const float *v_scales) {
@@ -886,6 +1115,9 @@ int find_seqs(zk_kv_cache *c, const char *const *ids, int n, std::vector<const S
         if (c->dtype == ZK_FP8_E4M3 && s->k_scales.empty())
             return set_error(ZK_ERR_FAILED_PRECONDITION,
                              std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
+        if (s->swapped)
+            return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + ids[i] +
+                                                             " is swapped out");
         out[i] = s;
     }
     return ZK_OK;

@@ -291,6 +291,33 @@ copy_blocks_kernel(PoolArgs pools, const int32_t *__restrict__ src, const int32_
     }
 }
 
+// Swap staging: block blocks[i] of every pool (pool p at slab + p *
+// pool_bytes) <-> staging row (i * num_pools + p) * block_bytes, so one
+// sequence's blocks of all layers, K and V, are one contiguous staging range
+// for a single host DMA.  Workgroup (i, p); out-of-range ids are skipped.
+__global__ void __launch_bounds__(kThreads)
+swap_stage_kernel(char *__restrict__ slab, uint64_t pool_bytes, uint64_t block_bytes, const int32_t *__restrict__ blocks,
+                  char *__restrict__ staging, int64_t num_blocks, int to_staging) {
+    const uint32_t i = blockIdx.x, p = blockIdx.y, np = gridDim.y;
+    const int64_t b = blocks[i];
+    if (b < 0 || b >= num_blocks) return;
+    char *pool = slab + (size_t)p * pool_bytes + (size_t)b * block_bytes;
+    char *stage = staging + ((size_t)i * np + p) * block_bytes;
+    const char *from = to_staging ? pool : stage;
+    char *to = to_staging ? stage : pool;
+    const uint64_t n16 = block_bytes >> 4;
+    uint64_t i0 = threadIdx.x;
+    for (; i0 + 3 * kThreads < n16; i0 += 4 * kThreads) {
+        uint4 a = ld16_nt(from + 16 * i0), c = ld16_nt(from + 16 * (i0 + kThreads));
+        uint4 d = ld16_nt(from + 16 * (i0 + 2 * kThreads)), e = ld16_nt(from + 16 * (i0 + 3 * kThreads));
+        st16_nt(to + 16 * i0, a);
+        st16_nt(to + 16 * (i0 + kThreads), c);
+        st16_nt(to + 16 * (i0 + 2 * kThreads), d);
+        st16_nt(to + 16 * (i0 + 3 * kThreads), e);
+    }
+    for (; i0 < n16; i0 += kThreads) st16_nt(to + 16 * i0, ld16_nt(from + 16 * i0));
+}
+
 // Streaming copy (bandwidth yardstick): 4 x 16 B per lane in flight.
 __global__ void __launch_bounds__(kThreads)
 stream_copy_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, uint64_t n16) {
@@ -408,6 +435,19 @@ int zk::append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, 
                                                            total, num_kv_heads, head_dim, block_size,
                                                            num_slots, (uint64_t)src_token_stride);
     return check_launch("zk_append");
+}
+
+int zk::swap_stage(char *slab, size_t pool_bytes, size_t block_bytes, int num_pools, const int32_t *blocks, int n,
+                   char *staging, int64_t num_blocks, bool to_staging, hipStream_t stream) {
+    if (n <= 0) return ZK_OK;
+    if ((block_bytes & 15u) || (pool_bytes & 15u) || (((uintptr_t)slab | (uintptr_t)staging) & 15u))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap: blocks must be 16-byte multiples");
+    if (num_pools <= 0 || num_pools > 65535)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap: bad pool count");
+    KernelTimer timer(to_staging ? "swap_out" : "swap_in", stream);
+    swap_stage_kernel<<<dim3((unsigned)n, (unsigned)num_pools), kThreads, 0, stream>>>(
+        slab, pool_bytes, block_bytes, blocks, staging, num_blocks, to_staging ? 1 : 0);
+    return check_launch("KVCache swap");
 }
 
 extern "C" {

@@ -31,6 +31,12 @@
 //    single-chunk recompute is the same in both;
 //  - a request id already queued or running is rejected (AlreadyExists): ids
 //    key the KV cache's sequences;
+//  - with swap space configured (swap_blocks > 0), a victim whose KV fits
+//    the remaining host space is swapped instead of recomputed (the policy of
+//    docs/architecture.md:452-469: swap first, recompute when the swap pool
+//    is full): it keeps its prefill position and outputs, and is listed in
+//    swapped_out; when re-admitted it is listed in swapped_in and resumes as
+//    it stood (a decoding sequence goes straight back to decoding);
 //  - a sequence whose blocks do not cover len() after the top-up (no victim
 //    was left, scheduler.rs:386) stays out of the batch until a later step
 //    finds its blocks, as the reference's comment there intends; the
@@ -56,6 +62,8 @@ struct Seq {
     std::vector<zk_block_handle> blocks;
     bool prefill_pending = true;
     size_t prefill_pos = 0, chunk_size = 0;
+    bool swapped = false;  // preempted with its KV moved to host slots
+    size_t swap_blocks = 0;
 
     size_t len() const {  // scheduler.rs:115-121
         return prefill_pending ? prefill_pos + output.size() + chunk_size : prompt.size() + output.size();
@@ -69,6 +77,8 @@ struct Seq {
         return chunk + (final_chunk() ? output.size() : 0);
     }
     size_t tokens_before() const { return prefill_pending ? prefill_pos : len() - 1; }
+    // KV tokens a preempted sequence holds (nothing of the chunk in flight).
+    size_t kv_tokens() const { return prefill_pending ? prefill_pos : prompt.size() + output.size() - 1; }
     // Order of the waiting queue: priority desc, arrival asc.
     bool before_or_tie(const Seq &o) const {
         return std::make_tuple(-priority, arrival) <= std::make_tuple(-o.priority, o.arrival);
@@ -91,8 +101,9 @@ struct zk_scheduler {
     uint64_t next_arrival = 0;
     // snapshot of the last schedule() output
     std::vector<zk_sched_entry> out;
-    std::vector<std::string> out_ids, pre_ids;
-    std::vector<const char *> pre_ptrs;
+    std::vector<std::string> out_ids, pre_ids, swap_out_ids, swap_in_ids;
+    std::vector<const char *> pre_ptrs, swap_out_ptrs, swap_in_ptrs;
+    size_t swap_used = 0;  // host blocks held by swapped sequences
     std::vector<zk_block_handle> out_blocks;
 
     ~zk_scheduler() {
@@ -112,7 +123,8 @@ struct zk_scheduler {
 
     // scheduler.rs:347-393: grow queue[idx]'s blocks to cover len(); returns
     // the requester's index after preemptions.
-    size_t ensure_blocks(std::vector<Seq> &queue, size_t idx, std::vector<std::string> &preempted) {
+    size_t ensure_blocks(std::vector<Seq> &queue, size_t idx, std::vector<std::string> &preempted,
+                         std::vector<std::string> &swapped_out) {
         const size_t need = blocks_for(queue[idx].len(), cfg.block_size);
         while (queue[idx].blocks.size() < need) {
             zk_block_handle h;
@@ -132,11 +144,21 @@ struct zk_scheduler {
             Seq victim = std::move(queue[vi]);
             queue.erase(queue.begin() + (ptrdiff_t)vi);
             free_blocks(victim);
-            victim.prefill_pending = true;
-            victim.prefill_pos = 0;
             victim.chunk_size = 0;
             victim.running = false;
-            preempted.push_back(victim.id);
+            const size_t kv = victim.kv_tokens(), kvb = blocks_for(kv, cfg.block_size);
+            if (kv > 0 && swap_used + kvb <= cfg.swap_blocks) {
+                // swap: the runner moves its KV to host slots before the
+                // blocks are reused; it resumes where it stopped
+                victim.swapped = true;
+                victim.swap_blocks = kvb;
+                swap_used += kvb;
+                swapped_out.push_back(victim.id);
+            } else {  // recompute (scheduler.rs:372-376)
+                victim.prefill_pending = true;
+                victim.prefill_pos = 0;
+                preempted.push_back(victim.id);
+            }
             insert_waiting(std::move(victim));
             if (vi < idx) --idx;
         }
@@ -235,7 +257,7 @@ int zk_sched_add(zk_scheduler *s, zk_sequence *q) {
 int zk_sched_schedule(zk_scheduler *s, zk_sched_output *out) {
     if (!s || !out) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_sched_schedule: NULL argument");
     const zk_sched_config &cfg = s->cfg;
-    std::vector<std::string> preempted;
+    std::vector<std::string> preempted, swapped_out, swapped_in;
     // 1. next chunks of prefilling sequences (scheduler.rs:270-282)
     size_t prefill_tokens = 0;
     for (Seq &q : s->prefilling) {
@@ -250,9 +272,11 @@ int zk_sched_schedule(zk_scheduler *s, zk_sched_output *out) {
     while (!s->waiting.empty()) {
         if (s->prefilling.size() + s->decoding.size() >= cfg.max_num_seqs) break;
         const Seq &w = s->waiting.front();
-        const size_t chunk = std::min(w.remaining(), cfg.prefill_chunk_size);
-        if (prefill_tokens + chunk > cfg.max_prefill_tokens && prefill_tokens > 0) break;
-        const size_t need = blocks_for(w.prefill_pos + chunk + w.output.size(), cfg.block_size);
+        const bool resume_decode = w.swapped && !w.prefill_pending;  // back to decoding, no prompt tokens
+        const size_t chunk = resume_decode ? 0 : std::min(w.remaining(), cfg.prefill_chunk_size);
+        if (!resume_decode && prefill_tokens + chunk > cfg.max_prefill_tokens && prefill_tokens > 0) break;
+        const size_t need = resume_decode ? blocks_for(w.len(), cfg.block_size)
+                                          : blocks_for(w.prefill_pos + chunk + w.output.size(), cfg.block_size);
         if (zk_bm_available(s->bm) < need) break;
         Seq q = std::move(s->waiting.front());
         s->waiting.erase(s->waiting.begin());
@@ -265,14 +289,24 @@ int zk_sched_schedule(zk_scheduler *s, zk_sched_output *out) {
             }
             q.blocks.push_back(h);
         }
-        q.chunk_size = chunk;
         q.running = true;
+        if (q.swapped) {
+            s->swap_used -= q.swap_blocks;
+            q.swapped = false;
+            q.swap_blocks = 0;
+            swapped_in.push_back(q.id);
+        }
+        if (resume_decode) {
+            s->decoding.push_back(std::move(q));
+            continue;
+        }
+        q.chunk_size = chunk;
         prefill_tokens += chunk;
         s->prefilling.push_back(std::move(q));
     }
     // 3. blocks for every running sequence (scheduler.rs:311-334)
-    for (size_t i = 0; i < s->prefilling.size(); ++i) i = s->ensure_blocks(s->prefilling, i, preempted);
-    for (size_t i = 0; i < s->decoding.size(); ++i) i = s->ensure_blocks(s->decoding, i, preempted);
+    for (size_t i = 0; i < s->prefilling.size(); ++i) i = s->ensure_blocks(s->prefilling, i, preempted, swapped_out);
+    for (size_t i = 0; i < s->decoding.size(); ++i) i = s->ensure_blocks(s->decoding, i, preempted, swapped_out);
     // 4. batch: prefilling with a chunk, then decoding (scheduler.rs:336-343);
     // a sequence left short of blocks waits for the next step
     auto covered = [&](const Seq &q) { return q.blocks.size() >= blocks_for(q.len(), cfg.block_size); };
@@ -313,6 +347,30 @@ int zk_sched_schedule(zk_scheduler *s, zk_sched_output *out) {
     out->preempted = s->pre_ptrs.data();
     out->num_preempted = s->pre_ptrs.size();
     out->blocks = s->out_blocks.data();
+    // a sequence re-admitted from swap and preempted again within one step
+    // never left host memory: swapped out again, report neither; preempted by
+    // recompute, only the drop (which frees its host slots)
+    for (auto it = swapped_in.begin(); it != swapped_in.end();) {
+        auto o = std::find(swapped_out.begin(), swapped_out.end(), *it);
+        if (o != swapped_out.end()) {
+            swapped_out.erase(o);
+            it = swapped_in.erase(it);
+        } else if (std::find(s->pre_ids.begin(), s->pre_ids.end(), *it) != s->pre_ids.end()) {
+            it = swapped_in.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    s->swap_out_ids = std::move(swapped_out);
+    s->swap_in_ids = std::move(swapped_in);
+    s->swap_out_ptrs.resize(s->swap_out_ids.size());
+    s->swap_in_ptrs.resize(s->swap_in_ids.size());
+    for (size_t i = 0; i < s->swap_out_ids.size(); ++i) s->swap_out_ptrs[i] = s->swap_out_ids[i].c_str();
+    for (size_t i = 0; i < s->swap_in_ids.size(); ++i) s->swap_in_ptrs[i] = s->swap_in_ids[i].c_str();
+    out->swapped_out = s->swap_out_ptrs.data();
+    out->num_swapped_out = s->swap_out_ptrs.size();
+    out->swapped_in = s->swap_in_ptrs.data();
+    out->num_swapped_in = s->swap_in_ptrs.size();
     return ZK_OK;
 }
 
@@ -374,6 +432,7 @@ int zk_sched_cancel(zk_scheduler *s, const char *id, size_t *prompt_len, size_t 
         if (s->waiting[i].id == id) {
             if (prompt_len) *prompt_len = s->waiting[i].prompt.size();
             if (output_len) *output_len = 0;
+            if (s->waiting[i].swapped) s->swap_used -= s->waiting[i].swap_blocks;
             s->waiting.erase(s->waiting.begin() + (ptrdiff_t)i);
             return ZK_CANCEL_WAS_WAITING;
         }
@@ -423,6 +482,7 @@ int zk_sched_seq_info(zk_scheduler *s, const char *id, zk_seq_info *info) {
     info->chunk_size = q->chunk_size;
     info->len = q->len();
     info->num_blocks = q->blocks.size();
+    info->swapped = q->swapped ? 1 : 0;
     return ZK_OK;
 }
 

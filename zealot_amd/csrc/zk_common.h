@@ -47,6 +47,11 @@ int append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, cons
            int64_t src_token_stride, const int64_t *slot_mapping, int64_t num_tokens, int num_kv_heads, int head_dim,
            int block_size, int64_t num_blocks, const float *k_scales, const float *v_scales, const int32_t *token_row,
            void *stream);
+// Swap staging (kv_ops.hip): blocks[i] of each of the num_pools pools at
+// slab + p * pool_bytes <-> staging[(i * num_pools + p) * block_bytes ...]
+// (to_staging: pools -> staging, else staging -> pools).
+int swap_stage(char *slab, size_t pool_bytes, size_t block_bytes, int num_pools, const int32_t *blocks, int n,
+               char *staging, int64_t num_blocks, bool to_staging, hipStream_t stream);
 // Internal launcher (kv_ops.hip): base[pairs[i].x] = pairs[i].y for i < n,
 // offsets checked on the device against `limit`.  Used by the KV cache to
 // apply a batch of block-table updates in one launch.

@@ -257,6 +257,30 @@ class KVCache:
         _lib.check(_lib.lib().zk_cache_decode_sharing(self._h, ctypes.byref(sg), ctypes.byref(pages)))
         return sg.value, pages.value
 
+    # -- swap (host <-> device block moves) -----------------------------------
+    def enable_swap(self, num_host_blocks: int) -> None:
+        """Pinned host space of num_host_blocks slots (one block of every pool)."""
+        _lib.check(_lib.lib().zk_cache_enable_swap(self._h, num_host_blocks))
+
+    def swap_space(self):
+        """(total, free) host slots."""
+        t, f = ctypes.c_size_t(), ctypes.c_size_t()
+        _lib.check(_lib.lib().zk_cache_swap_space(self._h, ctypes.byref(t), ctypes.byref(f)))
+        return t.value, f.value
+
+    def swap_out(self, ids) -> None:
+        b = _batch(ids)
+        _lib.check(_lib.lib().zk_cache_swap_out(self._h, b.arr, len(b)))
+
+    def swap_in(self, ids, bm: BlockManager | None = None) -> None:
+        b = _batch(ids)
+        _lib.check(_lib.lib().zk_cache_swap_in(self._h, b.arr, len(b), bm.handle if bm is not None else None))
+
+    def is_swapped(self, id: str) -> bool:
+        out = ctypes.c_int()
+        _lib.check(_lib.lib().zk_cache_seq_swapped(self._h, _id(id), ctypes.byref(out)))
+        return bool(out.value)
+
     # -- pool views ----------------------------------------------------------
     def _pool_view(self, ptr: int) -> torch.Tensor:
         """Device tensor aliasing a pool (shape [num_blocks, Hkv, bs, D])."""

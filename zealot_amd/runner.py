@@ -45,9 +45,14 @@ class PagedKVRunner:
         self._bound = set()
 
     def begin_step(self, out) -> StepPlan:
-        """Drop the state of preempted sequences, then bind every entry's
-        blocks (Sequence.blocks) as its block table, checking that the cache
-        holds exactly entry.tokens_before tokens of it."""
+        """Move the KV of sequences preempted by swap to host slots (before
+        anything of this step can write their freed blocks), drop the state of
+        those preempted by recompute, bind every entry's blocks
+        (Sequence.blocks) as its block table -- checking that the cache holds
+        exactly entry.tokens_before tokens of it -- and copy the KV of
+        re-admitted swapped sequences back into their new blocks."""
+        if out.swapped_out:
+            self.cache.swap_out(out.swapped_out)
         for rid in out.preempted:
             self.drop_state(rid)
         batch = out.batch
@@ -59,6 +64,8 @@ class PagedKVRunner:
         tb = (ctypes.c_size_t * max(1, n))(*[s.tokens_before for s in batch])
         _lib.check(_lib.lib().zk_cache_bind_blocks(self.cache._h, self.bm.handle, ids.arr, n, harr, nb, tb))
         self._bound.update(ids.ids)
+        if out.swapped_in:
+            self.cache.swap_in(out.swapped_in)
         nt = (ctypes.c_int32 * max(1, n))(*[s.num_tokens for s in batch])
         return StepPlan(ids, nt, [s.tokens_before for s in batch], sum(s.num_tokens for s in batch))
 

@@ -35,10 +35,11 @@ class SchedulerConfig:
     num_gpu_blocks: int = 1024
     max_prefill_tokens: int = 2048
     prefill_chunk_size: int = 512
+    swap_blocks: int = 0  # host swap space (0: recompute only, the reference's policy)
 
     def _c(self) -> _lib.SchedConfigC:
         return _lib.SchedConfigC(self.max_num_seqs, self.block_size, self.num_gpu_blocks,
-                                 self.max_prefill_tokens, self.prefill_chunk_size)
+                                 self.max_prefill_tokens, self.prefill_chunk_size, self.swap_blocks)
 
 
 class CancelOutcome(enum.IntEnum):
@@ -100,9 +101,12 @@ class Sequence:
 
 @dataclass
 class ScheduleOutput:
-    """scheduler.rs:185-189."""
+    """scheduler.rs:185-189, plus the sequences preempted by swap this step
+    and those re-admitted from swap."""
     batch: list
     preempted: list
+    swapped_out: list = None
+    swapped_in: list = None
 
 
 class Scheduler:
@@ -146,7 +150,9 @@ class Scheduler:
         _lib.check(_lib.lib().zk_sched_schedule(self._h, ctypes.byref(out)))
         batch = [Sequence(self, out.batch[i]) for i in range(out.batch_len)]
         pre = [out.preempted[i].decode() for i in range(out.num_preempted)]
-        return ScheduleOutput(batch, pre)
+        so = [out.swapped_out[i].decode() for i in range(out.num_swapped_out)]
+        si = [out.swapped_in[i].decode() for i in range(out.num_swapped_in)]
+        return ScheduleOutput(batch, pre, so, si)
 
     def finish(self, request_id: str):
         p, o = ctypes.c_size_t(), ctypes.c_size_t()
