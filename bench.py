@@ -629,6 +629,54 @@ def bench_model(args, torch, lib):
     return res
 
 
+def bench_swap(args, torch, lib):
+    """KV swap at C4's KV shape: 16 sequences x 2048 tokens x 32 layers (bf16,
+    8 kv heads x 128) moved to pinned host slots and back (zk_cache_swap_out /
+    zk_cache_swap_in: staging kernel + one DMA per run of host slots).  Bound
+    by PCIe, not HBM: reported in GB/s of KV bytes moved per direction."""
+    from zealot_amd import BlockManager, KVCache
+    from zealot_amd.kv_cache import SeqBatch
+    N, T, L, Hkv, D, BS = 16, 2048, 32, 8, 128, 16
+    nblk = T // BS
+    NB = N * nblk + 16
+    bm = BlockManager(NB, BS)
+    cache = KVCache(NB, BS, L, Hkv, D, dtype=torch.bfloat16, max_seqs=N, max_blocks_per_seq=nblk)
+    cache.enable_swap(N * nblk)
+    ids = [f"w{i}" for i in range(N)]
+    for sid in ids:
+        cache.register_seq(sid, nblk)
+        for _ in range(nblk):
+            cache.alloc_block(sid, bm)
+    g = torch.Generator(device="cuda").manual_seed(SEED + 12)
+    b = SeqBatch(ids)
+    x = torch.randn((N * T, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    for layer in range(L):
+        cache.write_batch(layer, b, [T] * N, x, x)
+    del x
+    nbytes = N * nblk * 2 * L * BS * Hkv * D * 2
+    log(f"swap: {N} x {T} tokens x {L} layers = {nbytes / 1e9:.2f} GB per direction")
+    outs, ins = [], []
+    for it in range(args.warmup + max(3, args.steps // 10)):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        cache.swap_out(b)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        cache.swap_in(b, bm)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if it >= args.warmup:
+            outs.append(t1 - t0)
+            ins.append(t2 - t1)
+    so, si = float(np.median(outs)), float(np.median(ins))
+    res = {"bytes_per_direction": nbytes, "swap_out_ms": so * 1e3, "swap_in_ms": si * 1e3,
+           "swap_out_gbps": nbytes / so / 1e9, "swap_in_gbps": nbytes / si / 1e9,
+           "shape": {"seqs": N, "tokens": T, "layers": L, "kv_heads": Hkv, "head_dim": D, "dtype": "bf16"}}
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 def cpu_model() -> str:
@@ -673,7 +721,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4", "prefill", "mixed", "model"], default=None,
+    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4", "prefill", "mixed", "model", "swap"],
+                    default=None,
                     help="run one workload (for profiler passes)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
@@ -692,7 +741,7 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     result = {}
-    dec = lens = app = fp8 = c4 = pre = mix = mdl = None
+    dec = lens = app = fp8 = c4 = pre = mix = mdl = swp = None
     if args.only in (None, "decode"):
         dec, lens = bench_decode(args, torch, ops, lib, "bf16")
         log(f"decode bf16: {dec['ms_per_step']:.4f} ms {dec['gbps']:.1f} GB/s")
@@ -717,6 +766,9 @@ def main() -> int:
     if args.only in (None, "model"):
         mdl = bench_model(args, torch, lib)
         log(f"model decode step: {mdl['ms_per_step']:.3f} ms, {mdl['tokens_per_s']:.0f} tokens/s")
+    if args.only in (None, "swap"):
+        swp = bench_swap(args, torch, lib)
+        log(f"swap: out {swp['swap_out_gbps']:.1f} GB/s, in {swp['swap_in_gbps']:.1f} GB/s")
     cpu = None
     if args.only is None and not args.no_cpu_baseline:
         cpu = cpu_baseline(lens, args.cpu_sample_seqs)
@@ -729,8 +781,10 @@ def main() -> int:
         head = {"gbps": pre["tflops"], "ms_per_step": pre["ms_per_step"], "roofline": pre["roofline"]}
     if head is None and mix is not None:  # --only mixed
         head = {"gbps": mix["decode_kv_gbps_in_mixed_step"], "ms_per_step": mix["ms_per_step"], "roofline": None}
-    if head is None:  # --only model
+    if head is None and mdl is not None:  # --only model
         head = {"gbps": mdl["gbps_weights_plus_kv"], "ms_per_step": mdl["ms_per_step"], "roofline": None}
+    if head is None:  # --only swap
+        head = {"gbps": swp["swap_out_gbps"], "ms_per_step": swp["swap_out_ms"], "roofline": None}
     result = {
         "metric": METRIC,
         "value": round(head["gbps"], 2),
@@ -757,6 +811,7 @@ def main() -> int:
         "prefill_attention": pre,
         "runner_step_mixed": mix,
         "model_decode_step": mdl,
+        "kv_swap": swp,
         "gpu": torch.cuda.get_device_name(0),
     }
     if args.only is not None:
