@@ -132,6 +132,7 @@ SIGNATURES = {
     "zk_add": (_I, [_P, _P, _P, _I64, _I, _P]),
     "zk_embedding": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "zk_linear": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _I, _P]),
+    "zk_linear_tuning": (_I, [_I]),
     "zk_sched_create": (_I, [ctypes.POINTER(SchedConfigC), _P, ctypes.POINTER(_P)]),
     "zk_sched_destroy": (None, [_P]),
     "zk_sched_block_manager": (_P, [_P]),
