@@ -156,6 +156,18 @@ def bench_decode(args, torch, ops, lib, kv="bf16"):
     lib.zk_timing_reset()
     lib.zk_timing_enable(1)
     ms_ev = timed(step, args.steps, 0, torch)
+    # read yardstick over the same pools: the practical ceiling of this read-bound kernel
+    import ctypes
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    pool_bytes = kp.numel() * kp.element_size()
+
+    def read_pools(_):
+        for t in (kp, vp):
+            lib.zk_stream_read(ctypes.c_void_p(t.data_ptr()), pool_bytes, ctypes.c_void_p(sink.data_ptr()), None)
+
+    timed(read_pools, args.steps, 2, torch)
+    rd_ms, rd_n = kernel_ms(lib, "stream_read")
+    read_gbps = pool_bytes / (rd_ms * 1e-3) / 1e9
     lib.zk_timing_enable(0)
     k_ms, k_n = kernel_ms(lib, "decode_partials")
     p_ms, _ = kernel_ms(lib, "decode_plan")
@@ -178,6 +190,8 @@ def bench_decode(args, torch, ops, lib, kv="bf16"):
         "kernel_ms": {"decode_partials": k_ms, "decode_reduce": r_ms, "decode_seq_info": i_ms,
                       "decode_plan": p_ms},
         "ms_per_step_with_kernel_events": ms_ev,
+        "read_ceiling_gbps": read_gbps,
+        "kernel_frac_of_read_ceiling": (alg_kernel / (k_ms * 1e-3) / 1e9) / read_gbps,
         "roofline": {"bound": "hbm", "achieved": kgbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": kgbps / PEAK_HBM_GBPS, "traffic": measured_traffic(f"decode_{kv}"),
                      "kernel": "decode_partials", "kernel_bytes_per_launch": alg_kernel,

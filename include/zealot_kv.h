@@ -329,13 +329,18 @@ int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const 
  * milliseconds of one kernel name since the last reset.  Kernel names:
  * "append", "fp8_scales", "gather", "copy_blocks", "decode_seq_info",
  * "decode_plan", "decode_partials", "decode_reduce", "prefill_plan",
- * "prefill_attention", "stream_copy". */
+ * "prefill_attention", "stream_copy", "stream_read", "rms_norm", "silu_mul",
+ * "add", "embedding", "linear", "swap_out", "swap_in". */
 int zk_timing_enable(int on);
 int zk_timing_reset(void);
 int zk_timing_query(const char *kernel, int64_t *launches, double *total_ms);
 /* Streaming copy of `bytes` (multiple of 16, 16-B aligned pointers): the
  * in-repo bandwidth yardstick and HBM-counter calibration kernel. */
 int zk_stream_copy(void *dst, const void *src, size_t bytes, void *stream);
+/* Streaming read of `bytes` (multiple of 16, 16-B aligned): the in-repo
+ * read-bandwidth yardstick (the practical ceiling of an HBM-read-bound kernel
+ * such as the decode).  `sink`: a device word the kernel may write. */
+int zk_stream_read(const void *src, size_t bytes, uint32_t *sink, void *stream);
 
 #ifdef __cplusplus
 }

@@ -127,6 +127,7 @@ SIGNATURES = {
     "zk_timing_reset": (_I, []),
     "zk_timing_query": (_I, [_CP, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
     "zk_stream_copy": (_I, [_P, _P, _SZ, _P]),
+    "zk_stream_read": (_I, [_P, _SZ, _P, _P]),
     "zk_rms_norm": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _I, _P]),
     "zk_silu_mul": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),
     "zk_add": (_I, [_P, _P, _P, _I64, _I, _P]),
