@@ -12,11 +12,16 @@
 // Kernels
 //   prefill_plan_kernel  one workgroup: effective context per sequence (the
 //       page walk stops at the first table entry < 0 or >= num_blocks, as in
-//       the decode), then work items (sequence, query tile, kv-head) listed
-//       longest first (counting sort on the pages a tile reads).
+//       the decode), then work items (sequence, query tile, kv-head) in one
+//       queue per XCD: every tile of a (sequence, kv-head) goes to the same
+//       XCD, (n * Hkv + kvh) mod 8, so the tiles reading the same pages share
+//       that XCD's L2; within a queue the groups run longest first (counting
+//       sort on their last tile's pages) and a group's tiles back to back,
+//       longest first.
 //   prefill_mfma_kernel<KV, D, G>  bf16 / fp8 pools, D in {64, 128}, G in
 //       {1, 2, 4, 8}, block_size 16: persistent one-wave workgroups take items
-//       from an atomic queue.  An item holds 64 query rows -- TQ = 64/G chunk
+//       from their XCD's queue (workgroups are dispatched round-robin over the
+//       8 XCDs), then from the others' when it runs dry.  An item holds 64 query rows -- TQ = 64/G chunk
 //       tokens x the G heads of one kv-head, token-major -- as four 16-column
 //       MFMA tiles, so each K/V page read serves all 64 rows.  Pages stream
 //       through LDS as in the decode (global_load_lds, two stages); QK^T and PV
@@ -42,7 +47,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWave = 64;
 constexpr int kRows = 64;            // query rows per item (4 MFMA tiles)
 constexpr int kTiles = kRows / 16;
-constexpr int kMaxBins = zk::kPrefillMaxPages;  // page-count bins of the longest-first sort
+constexpr int kMaxBins = zk::kPrefillMaxPages;  // LDS block ids per item; plan-kernel bins
+constexpr int kXcds = 8;                         // XCDs of an MI355X
+constexpr int kXcdBins = kMaxBins / kXcds;       // longest-first bins per XCD queue
+constexpr int kQueueStride = 32;                 // ints between XCD queue heads (128 B)
 constexpr float kRescaleSlack = 8.0f;  // lazy-rescale slack, log2 units
 
 struct PParams {
@@ -59,8 +67,8 @@ struct PParams {
     const float *k_scales;
     const float *v_scales;
     int32_t *eff;         // [N] context after the page walk
-    int4 *items;          // {n, query tile, pages, 0}, longest first
-    int32_t *work;        // [2] total items, queue head
+    int4 *items;          // {n, query tile, pages, kv-head}, per-XCD segments
+    int32_t *work;        // [0] total items; XCD x at 64 + 32 x: segment start, end, queue head
     int num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks, tq, num_waves, max_items;
     int64_t num_blocks;
     float scale_log2;
@@ -117,10 +125,18 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
     }
     __threadfence_block();
     __syncthreads();
-    auto bin = [&](int pages) { return kMaxBins - 1 - min(pages, kMaxBins - 1); };  // longest first
-    for (int n = t; n < p.num_seqs; n += 1024) {
+    const int Hkv = p.num_kv_heads;
+    // group (n, kvh) -> XCD queue x, longest group first within the queue
+    auto key = [&](int n, int kvh, int tiles) {
+        const int x = (n * Hkv + kvh) % kXcds;
+        const int maxp = tiles > 0 ? tile_pages(p, n, tiles - 1) : 0;
+        return x * kXcdBins + kXcdBins - 1 - min(maxp / 8, kXcdBins - 1);
+    };
+    const int groups = p.num_seqs * Hkv;  // one thread per (n, kvh)
+    for (int g = t; g < groups; g += 1024) {
+        const int n = g / Hkv, kvh = g % Hkv;
         const int tiles = (chunk_len(p, n) + p.tq - 1) / p.tq;
-        for (int qt = 0; qt < tiles; ++qt) atomicAdd(&hist[bin(tile_pages(p, n, qt))], 1);
+        if (tiles > 0) atomicAdd(&hist[key(n, kvh, tiles)], tiles);
     }
     __syncthreads();
     const int a = hist[2 * t], b = hist[2 * t + 1];
@@ -138,18 +154,25 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
     hist[2 * t + 1] = base + a;
     const int total = sums[1023];
     __syncthreads();
-    for (int n = t; n < p.num_seqs; n += 1024) {
+    if (t < kXcds) {  // segment of each XCD queue; its first waves take items statically
+        const int start = hist[t * kXcdBins], end = t + 1 < kXcds ? hist[(t + 1) * kXcdBins] : total;
+        int32_t *w = p.work + 64 + kQueueStride * t;
+        w[0] = start;
+        w[1] = end;
+        w[2] = start + p.num_waves / kXcds;
+    }
+    __syncthreads();
+    for (int g = t; g < groups; g += 1024) {
+        const int n = g / Hkv, kvh = g % Hkv;
         const int tiles = (chunk_len(p, n) + p.tq - 1) / p.tq;
-        for (int qt = 0; qt < tiles; ++qt) {
-            const int pages = tile_pages(p, n, qt);
-            const int pos = atomicAdd(&hist[bin(pages)], 1);
-            if (pos < p.max_items) p.items[pos] = make_int4(n, qt, pages, 0);
+        if (tiles == 0) continue;
+        const int pos = atomicAdd(&hist[key(n, kvh, tiles)], tiles);
+        for (int j = 0; j < tiles; ++j) {  // the group's tiles back to back, longest first
+            const int qt = tiles - 1 - j;
+            p.items[pos + j] = make_int4(n, qt, tile_pages(p, n, qt), kvh);
         }
     }
-    if (t == 0) {
-        p.work[0] = min(total, p.max_items) * p.num_kv_heads;  // total items
-        p.work[1] = p.num_waves;                                // items below are taken statically
-    }
+    if (t == 0) p.work[0] = total;
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -201,8 +224,7 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
     constexpr int T = kTiles;
     static_assert(PAGE % 1024 == 0 && KBYTES % 16 == 0 && DT % 2 == 0, "page shape");
     typedef typename LdsVec<VTB>::T vtrow_t;
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
-    __shared__ __attribute__((aligned(16))) char lds[2][2][PAGE];
+    __shared__ __attribute__((aligned(16))) char lds[2][2][2][PAGE];  // [stage][page of the pair][K|V]
     __shared__ int32_t bids[kMaxBins];
 
     const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
@@ -222,13 +244,29 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
     }
     const uint32_t vt_off = (uint32_t)((4 * grp) * RB + col * VTB);
 
-    const int total = p.work[0];
-    int item = blockIdx.x;  // first item static, the rest from the queue
-    int next = 0;
-    while (item < total) {
-        const int kvh = item % Hkv;
-        const int4 desc = p.items[item / Hkv];
-        const int n = desc.x, qt = desc.y, np = desc.z;
+    // this wave's XCD queue (round-robin dispatch); its first item is static
+    const int xcd = blockIdx.x % kXcds;
+    const int32_t *myq = p.work + 64 + kQueueStride * xcd;
+    int item = myq[0] + (int)blockIdx.x / kXcds;
+    if (item >= myq[1]) item = -1;
+    int next = -1;
+    // lane 0: next item from this XCD's queue, else from the others'
+    auto claim = [&]() {
+        for (int k = 0; k < kXcds; ++k) {
+            int32_t *w = p.work + 64 + kQueueStride * ((xcd + k) % kXcds);
+            if (__hip_atomic_load(&w[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= w[1]) continue;
+            const int v = atomicAdd(&w[2], 1);
+            if (v < w[1]) return v;
+        }
+        return -1;
+    };
+    if (item < 0) {
+        if (lane == 0) next = claim();
+        item = __builtin_amdgcn_readfirstlane(next);
+    }
+    while (item >= 0) {
+        const int4 desc = p.items[item];
+        const int n = desc.x, qt = desc.y, np = desc.z, kvh = desc.w;
         const int len = chunk_len(p, n), st = p.start[n], eff = p.eff[n];
         const int64_t row0 = chunk_row0(p, n) + (int64_t)qt * p.tq;  // first q row of the tile
 
@@ -289,14 +327,24 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
         const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
         const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
         const size_t block_bytes = (size_t)PAGE * Hkv;
-        auto issue = [&](int pi, int s) {
-            const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
-            const char *kp = kbase + (size_t)blk * block_bytes;
-            const char *vp = vbase + (size_t)blk * block_bytes;
+        // Pages go through LDS in pairs: 32 keys per PV step feed the
+        // 16x16x32 MFMA (the 16x16x16 form runs at half its rate).  A pair's
+        // second page may not exist (odd page count): it is not loaded and
+        // its keys lie past every row's limit.
+        auto issue = [&](int pj, int s) {
 #pragma unroll
-            for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[s][0] + 1024 * j));
+            for (int h = 0; h < 2; ++h) {
+                const int pi = 2 * pj + h;
+                if (pi < np) {
+                    const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
+                    const char *kp = kbase + (size_t)blk * block_bytes;
+                    const char *vp = vbase + (size_t)blk * block_bytes;
 #pragma unroll
-            for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[s][1] + 1024 * j));
+                    for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[s][h][0] + 1024 * j));
+#pragma unroll
+                    for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[s][h][1] + 1024 * j));
+                }
+            }
         };
         f32x4 o[DT][T];
         // m: the rows' reference max (log2 units); lsum: every element of
@@ -310,85 +358,114 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[dt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        const s16x4 ones = __builtin_bit_cast(s16x4, u32x2{0x3f803f80u, 0x3f803f80u});  // bf16 1.0 x 4
-        // MASK: the page holds keys some row of the tile may not see (the
-        // diagonal pages, or stale rows past the context); the pages before
-        // run without the per-element compares.
-        auto page = [&]<bool MASK>(int pi, int s) {
-            if (pi + 1 < np) wait_vmcnt<LPP>();
+        const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+        const int npair = (np + 1) / 2;
+        // V rows at or past vlim are zeroed: stale rows past the context and a
+        // missing second page (its LDS holds another page's bytes, which may
+        // not even be finite as fp8)
+        const int vlim = min(eff, np * BS);
+        // MASK: the pair holds keys some row of the tile may not see (the
+        // diagonal pages, stale rows past the context, a missing second
+        // page); the pairs before run without the per-element compares.
+        auto pair = [&]<bool MASK>(int pj, int s) {
+            const int left = np - 2 * (pj + 1);  // pages of the pair in flight behind this one
+            if (left >= 2) wait_vmcnt<2 * LPP>();
+            else if (left == 1) wait_vmcnt<LPP>();
             else wait_vmcnt<0>();
-            uint32_t kw[KBYTES / 4];
+            uint32_t kw[2][KBYTES / 4];
+            vtrow_t vt[2][4];
 #pragma unroll
-            for (int f = 0; f < KCH; ++f) {
-                const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[s][0] + kl[f]);
+            for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) kw[4 * f + j] = c4[j];
-            }
-            vtrow_t vt[4];
+                for (int f = 0; f < KCH; ++f) {
+                    const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[s][h][0] + kl[f]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) vt[i] = *reinterpret_cast<const vtrow_t *>(lds[s][1] + vt_off + i * RB);
-            wait_lgkmcnt0();
-            if (pi + 2 < np) issue(pi + 2, s);
-
-            f32x4 sacc[T];
-#pragma unroll
-            for (int t = 0; t < T; ++t) sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                u32x4 w;
-                if constexpr (KV == ZK_BF16) {
-                    w = u32x4{kw[4 * kk], kw[4 * kk + 1], kw[4 * kk + 2], kw[4 * kk + 3]};
-                } else {
-                    const u32x2 lo2 = e4m3x4_to_bf16x4(kw[2 * kk]), hi2 = e4m3x4_to_bf16x4(kw[2 * kk + 1]);
-                    w = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+                    for (int j = 0; j < 4; ++j) kw[h][4 * f + j] = c4[j];
                 }
 #pragma unroll
-                for (int t = 0; t < T; ++t)
-                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), qf[t][kk],
-                                                                      sacc[t], 0, 0, 0);
+                for (int i = 0; i < 4; ++i) vt[h][i] = *reinterpret_cast<const vtrow_t *>(lds[s][h][1] + vt_off + i * RB);
             }
-            uint32_t w[4][DT / 2];  // V rows as bf16 pairs
+            wait_lgkmcnt0();
+            if (pj + 2 < npair) issue(pj + 2, s);
+
+            f32x4 sacc[2][T];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if constexpr (KV == ZK_BF16) {
-                    __builtin_memcpy(w[i], &vt[i], 2 * DT);
-                } else {
-                    uint32_t b8[DT / 4];
-                    __builtin_memcpy(b8, &vt[i], DT);
+            for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                    for (int j = 0; j < DT / 4; ++j) {
-                        const u32x2 c2 = e4m3x4_to_bf16x4(b8[j]);
-                        w[i][2 * j] = c2[0];
-                        w[i][2 * j + 1] = c2[1];
+                for (int t = 0; t < T; ++t) sacc[h][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    u32x4 w;
+                    if constexpr (KV == ZK_BF16) {
+                        w = u32x4{kw[h][4 * kk], kw[h][4 * kk + 1], kw[h][4 * kk + 2], kw[h][4 * kk + 3]};
+                    } else {
+                        const u32x2 lo2 = e4m3x4_to_bf16x4(kw[h][2 * kk]), hi2 = e4m3x4_to_bf16x4(kw[h][2 * kk + 1]);
+                        w = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+                    }
+#pragma unroll
+                    for (int t = 0; t < T; ++t)
+                        sacc[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), qf[t][kk],
+                                                                             sacc[h][t], 0, 0, 0);
+                }
+            }
+            // V^T operand: k slots 8 grp + i (i < 4) are keys 4 grp + i of the
+            // first page, 8 grp + 4 + i those of the second, as in P^T below
+            u32x4 va[DT];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t w[4][DT / 2];  // V rows as bf16 pairs
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (KV == ZK_BF16) {
+                        __builtin_memcpy(w[i], &vt[h][i], 2 * DT);
+                    } else {
+                        uint32_t b8[DT / 4];
+                        __builtin_memcpy(b8, &vt[h][i], DT);
+#pragma unroll
+                        for (int j = 0; j < DT / 4; ++j) {
+                            const u32x2 c2 = e4m3x4_to_bf16x4(b8[j]);
+                            w[i][2 * j] = c2[0];
+                            w[i][2 * j + 1] = c2[1];
+                        }
                     }
                 }
-            }
-            const int key0 = pi * BS + 4 * grp;  // position of this lane's first key
-            if (MASK && key0 + 4 > eff) {  // past the context: stale rows must not reach O
+                const int key0 = (2 * pj + h) * BS + 4 * grp;  // position of this lane's first key
+                if (MASK && key0 + 4 > vlim) {  // stale rows past the context, a missing page: keep out of O
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (key0 + i >= eff)
+                    for (int i = 0; i < 4; ++i)
+                        if (key0 + i >= vlim)
 #pragma unroll
-                        for (int j = 0; j < DT / 2; ++j) w[i][j] = 0u;
-            }
-            s16x4 va[DT];
+                            for (int j = 0; j < DT / 2; ++j) w[i][j] = 0u;
+                }
 #pragma unroll
-            for (int j = 0; j < DT / 2; ++j) {
-                const u32x2 lo{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x05040100u),
-                               __builtin_amdgcn_perm(w[3][j], w[2][j], 0x05040100u)};
-                const u32x2 hi{__builtin_amdgcn_perm(w[1][j], w[0][j], 0x07060302u),
-                               __builtin_amdgcn_perm(w[3][j], w[2][j], 0x07060302u)};
-                va[2 * j] = __builtin_bit_cast(s16x4, lo);
-                va[2 * j + 1] = __builtin_bit_cast(s16x4, hi);
+                for (int j = 0; j < DT / 2; ++j) {
+                    va[2 * j][2 * h] = __builtin_amdgcn_perm(w[1][j], w[0][j], 0x05040100u);
+                    va[2 * j][2 * h + 1] = __builtin_amdgcn_perm(w[3][j], w[2][j], 0x05040100u);
+                    va[2 * j + 1][2 * h] = __builtin_amdgcn_perm(w[1][j], w[0][j], 0x07060302u);
+                    va[2 * j + 1][2 * h + 1] = __builtin_amdgcn_perm(w[3][j], w[2][j], 0x07060302u);
+                }
             }
+            const int key0a = 2 * pj * BS + 4 * grp, key0b = key0a + BS;
+            float sc[T][8];  // raw scores; the scale is applied inside the exponent
+            float mx[T];
+            bool grow = false;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                float sc[4];  // raw scores; the scale is applied inside the exponent
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sc[i] = !MASK || key0 + i < lim[t] ? sacc[t][i] : -INFINITY;
-                const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])) * sl2;
-                if (__builtin_amdgcn_ballot_w64(mx > m[t] + kRescaleSlack)) {
-                    float cm = fmaxf(mx, xor16(mx));
+                for (int i = 0; i < 4; ++i) {
+                    sc[t][i] = !MASK || key0a + i < lim[t] ? sacc[0][t][i] : -INFINITY;
+                    sc[t][4 + i] = !MASK || key0b + i < lim[t] ? sacc[1][t][i] : -INFINITY;
+                }
+                mx[t] = fmaxf(fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])),
+                              fmaxf(fmaxf(sc[t][4], sc[t][5]), fmaxf(sc[t][6], sc[t][7]))) * sl2;
+                grow |= mx[t] > m[t] + kRescaleSlack;
+            }
+            // one branch for the whole pair (it is rare past the first pages),
+            // so the tiles' exponentials and MFMAs below schedule as one block
+            if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    float cm = fmaxf(mx[t], xor16(mx[t]));
                     cm = fmaxf(cm, xor32(cm));
                     const float m_new = fmaxf(m[t], cm);
                     const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[t] - m_new);
@@ -397,26 +474,31 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
                     for (int dt = 0; dt < DT; ++dt) o[dt][t] *= alpha;
                     m[t] = m_new;
                 }
-                float pr[4];  // m is finite (key 0 is visible to every row)
+            }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) pr[i] = exp2_fast(fmaf(sc[i], sl2, -m[t]));
-                const s16x4 pb =
-                    __builtin_bit_cast(s16x4, u32x2{bf16x2_rne(pr[0], pr[1]), bf16x2_rne(pr[2], pr[3])});
-                lsum[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ones, pb, lsum[t], 0, 0, 0);
+            for (int t = 0; t < T; ++t) {
+                float pr[8];  // m is finite (key 0 is visible to every row)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pr[i] = exp2_fast(fmaf(sc[t][i], sl2, -m[t]));
+                const bf16x8 pb = __builtin_bit_cast(
+                    bf16x8, u32x4{bf16x2_rne(pr[0], pr[1]), bf16x2_rne(pr[2], pr[3]), bf16x2_rne(pr[4], pr[5]),
+                                  bf16x2_rne(pr[6], pr[7])});
+                lsum[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb, lsum[t], 0, 0, 0);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt)
-                    o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt][t], 0, 0, 0);
+                    o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, va[dt]), pb, o[dt][t],
+                                                                       0, 0, 0);
             }
         };
-        if (np > 0) issue(0, 0);
-        if (lane == 0) next = atomicAdd(&p.work[1], 1);  // overlaps the first page's round trip
-        if (np > 1) issue(1, 1);
-        // pages every row sees whole: below the first row's limit (rows are
-        // token-major, limits grow with the row)
+        if (npair > 0) issue(0, 0);
+        if (lane == 0) next = claim();  // overlaps the first pair's round trip
+        if (npair > 1) issue(1, 1);
+        // pairs every row sees whole: both pages below the first row's limit
+        // (rows are token-major, limits grow with the row)
         const int open = min(p.causal ? st + qt * p.tq + 1 : st + len, eff) / BS;
-        int pi = 0, s = 0;
-        for (; pi < min(open, np); ++pi, s ^= 1) page.template operator()<false>(pi, s);
-        for (; pi < np; ++pi, s ^= 1) page.template operator()<true>(pi, s);
+        int pj = 0, s = 0;
+        for (; pj < min(open / 2, npair); ++pj, s ^= 1) pair.template operator()<false>(pj, s);
+        for (; pj < npair; ++pj, s ^= 1) pair.template operator()<true>(pj, s);
 
         // rows of this lane: dims DT*(4*grp+i)+dt of row 16 t + col
 #pragma unroll
@@ -465,8 +547,9 @@ int persistent_waves() {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t kWorkBytes = 2048;  // total + 8 XCD queues of 128 B
 
-// Workspace: eff[N] | work[2] | items[max_items] (int4).
+// Workspace: eff[N] | work (kWorkBytes: total, 8 XCD queues) | items[max_items * Hkv] (int4).
 int max_items_for(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads) {
     const int G = num_kv_heads > 0 ? std::max(1, num_heads / num_kv_heads) : 1;
     const int tq = std::max(1, kRows / G);
@@ -502,8 +585,9 @@ extern "C" {
 
 size_t zk_paged_prefill_workspace_size(int num_seqs, int64_t total_q, int num_heads, int num_kv_heads) {
     if (num_seqs <= 0 || total_q < 0) return 256;
-    return align256(sizeof(int32_t) * (size_t)num_seqs) + 256 +
-           align256(sizeof(int4) * (size_t)max_items_for(num_seqs, total_q, num_heads, num_kv_heads));
+    return align256(sizeof(int32_t) * (size_t)num_seqs) + kWorkBytes +
+           align256(sizeof(int4) * (size_t)max_items_for(num_seqs, total_q, num_heads, num_kv_heads) *
+                    (size_t)num_kv_heads);
 }
 
 int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
@@ -576,7 +660,7 @@ int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void
     char *ws = (char *)workspace;
     p.eff = (int32_t *)ws;
     p.work = (int32_t *)(ws + align256(sizeof(int32_t) * (size_t)num_seqs));
-    p.items = (int4 *)(ws + align256(sizeof(int32_t) * (size_t)num_seqs) + 256);
+    p.items = (int4 *)(ws + align256(sizeof(int32_t) * (size_t)num_seqs) + kWorkBytes);
     p.num_seqs = num_seqs;
     p.num_heads = num_heads;
     p.num_kv_heads = num_kv_heads;
