@@ -120,7 +120,9 @@ def test_linear_f32(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,out_f32", [(1, 4096, 4096, False), (300, 28672, 4096, False),
-                                           (7, 128256, 4096, True), (64, 4096, 14336, False)])
+                                           (7, 128256, 4096, True), (64, 4096, 14336, False),
+                                           (16, 6144, 4096, False), (33, 1000, 512, False), (64, 28672, 4096, True),
+                                           (48, 37, 768, True)])
 def test_linear_bf16(m, n, k, out_f32):
     from zealot_amd import dense
     rng = np.random.default_rng(m + n)
@@ -133,3 +135,4 @@ def test_linear_bf16(m, n, k, out_f32):
     cols = rng.choice(n, size=min(n, 512), replace=False)  # a sample of outputs against float64
     ref = xs.astype(np.float64) @ ws[cols].astype(np.float64).T
     assert np.abs(got[:, cols] - ref).max() <= 1e-2 * np.abs(ref).max()
+
