@@ -1103,7 +1103,7 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
                             (const int32_t *)c->d_tbl.dev.p, (const int32_t *)d, n, num_heads, (int)H,
                             (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
                             mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr, drows,
-                            q_stride);
+                            q_stride, /*trusted_tables=*/true);  // built from the sequences' handles
 }
 
 // Looks up ids[0..n) (each must be registered; fp8 caches need scales).

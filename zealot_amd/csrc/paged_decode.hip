@@ -81,6 +81,7 @@ struct Params {
     const float *v_scales;
     const int32_t *q_rows;  // optional: q / out row of each sequence
     int64_t q_stride;       // elements between consecutive q rows (out rows: H * D)
+    int trusted;            // tables hold valid ids up to every length: no page walk
     int32_t *eff_len;     // [N] length after the page walk
     int4 *items;          // [N * MP] work-item descriptors, longest first (MFMA path):
                           //   {n, part, first page, pages} of a sequence's own pages or
@@ -221,6 +222,11 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
     const int t = threadIdx.x;
     hist[2 * t] = 0;
     hist[2 * t + 1] = 0;
+    if (p.trusted) {  // the caller built the tables: the walk would reach every length
+        const int cap = p.max_blocks * p.block_size;
+        for (int n = t; n < num_seqs; n += 1024) p.eff_len[n] = min(max(p.seq_lens[n], 0), cap);
+        __threadfence_block();
+    }
     __syncthreads();
     for (int n = t; n < num_seqs; n += 1024) {
         const int np = private_items_of(p, n);
@@ -963,7 +969,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                      int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                      float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                      void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
-                     const int32_t *q_rows, int64_t q_stride) {
+                     const int32_t *q_rows, int64_t q_stride, bool trusted_tables) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: q dtype must be f32 or bf16");
     if (!valid_dtype(kv_dtype))
@@ -1018,6 +1024,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.v_scales = v_scales;
     p.q_rows = q_rows;
     p.q_stride = q_stride > 0 ? q_stride : (int64_t)num_heads * head_dim;
+    p.trusted = trusted_tables ? 1 : 0;
     char *ws = (char *)workspace;
     p.eff_len = (int32_t *)(ws + w.eff);
     p.items = (int4 *)(ws + w.map);
@@ -1044,11 +1051,13 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.q_f32 = q_dtype == ZK_F32 ? 1 : 0;
 
     hipStream_t s = (hipStream_t)stream;
-    {
-        KernelTimer timer("decode_seq_info", s);
-        seq_info_kernel<<<num_seqs, kWave, 0, s>>>(p);
+    if (!(use_mfma && trusted_tables)) {  // trusted MFMA launches: the plan sets the lengths
+        {
+            KernelTimer timer("decode_seq_info", s);
+            seq_info_kernel<<<num_seqs, kWave, 0, s>>>(p);
+        }
+        if (int rc = check_launch("zk_paged_decode seq_info")) return rc;
     }
-    if (int rc = check_launch("zk_paged_decode seq_info")) return rc;
     if (use_mfma) {
         {
             KernelTimer timer("decode_plan", s);
