@@ -331,11 +331,11 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
         // 16x16x32 MFMA (the 16x16x16 form runs at half its rate).  A pair's
         // second page may not exist (odd page count): it is not loaded and
         // its keys lie past every row's limit.
-        auto issue = [&](int pj, int s) {
+        auto issue = [&]<bool FULL>(int pj, int s) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int pi = 2 * pj + h;
-                if (pi < np) {
+                if (FULL || pi < np) {
                     const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
                     const char *kp = kbase + (size_t)blk * block_bytes;
                     const char *vp = vbase + (size_t)blk * block_bytes;
@@ -367,9 +367,12 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
         // MASK: the pair holds keys some row of the tile may not see (the
         // diagonal pages, stale rows past the context, a missing second
         // page); the pairs before run without the per-element compares.
-        auto pair = [&]<bool MASK>(int pj, int s) {
+        // FULL: this pair and the two behind it hold two pages each, so the
+        // wait and the next issue take no branch and the whole pair up to
+        // the rescale test is one scheduling region.
+        auto pair = [&]<bool MASK, bool FULL>(int pj, int s) {
             const int left = np - 2 * (pj + 1);  // pages of the pair in flight behind this one
-            if (left >= 2) wait_vmcnt<2 * LPP>();
+            if (FULL || left >= 2) wait_vmcnt<2 * LPP>();
             else if (left == 1) wait_vmcnt<LPP>();
             else wait_vmcnt<0>();
             uint32_t kw[2][KBYTES / 4];
@@ -386,13 +389,12 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
                 for (int i = 0; i < 4; ++i) vt[h][i] = *reinterpret_cast<const vtrow_t *>(lds[s][h][1] + vt_off + i * RB);
             }
             wait_lgkmcnt0();
-            if (pj + 2 < npair) issue(pj + 2, s);
+            if constexpr (FULL) issue.template operator()<true>(pj + 2, s);
+            else if (pj + 2 < npair) issue.template operator()<false>(pj + 2, s);
 
-            f32x4 sacc[2][T];
+            bf16x8 kop[2][KK];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int t = 0; t < T; ++t) sacc[h][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int kk = 0; kk < KK; ++kk) {
                     u32x4 w;
@@ -402,12 +404,20 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
                         const u32x2 lo2 = e4m3x4_to_bf16x4(kw[h][2 * kk]), hi2 = e4m3x4_to_bf16x4(kw[h][2 * kk + 1]);
                         w = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
                     }
-#pragma unroll
-                    for (int t = 0; t < T; ++t)
-                        sacc[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), qf[t][kk],
-                                                                             sacc[h][t], 0, 0, 0);
+                    kop[h][kk] = __builtin_bit_cast(bf16x8, w);
                 }
-            }
+            // tile-major, so each tile's maximum can start while the next
+            // tile's scores are still in the MFMA pipe
+            f32x4 sacc[2][T];
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    sacc[h][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk)
+                        sacc[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[h][kk], qf[t][kk], sacc[h][t], 0, 0, 0);
+                }
             // V^T operand: k slots 8 grp + i (i < 4) are keys 4 grp + i of the
             // first page, 8 grp + 4 + i those of the second, as in P^T below
             u32x4 va[DT];
@@ -460,6 +470,13 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
                               fmaxf(fmaxf(sc[t][4], sc[t][5]), fmaxf(sc[t][6], sc[t][7]))) * sl2;
                 grow |= mx[t] > m[t] + kRescaleSlack;
             }
+            // a single wave per SIMD issues in order: spread the VALU work
+            // (V transposes, maxima) between the score MFMAs so both pipes run
+#pragma unroll
+            for (int i = 0; i < 2 * KK * T; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
             // one branch for the whole pair (it is rare past the first pages),
             // so the tiles' exponentials and MFMAs below schedule as one block
             if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -489,16 +506,29 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
                     o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, va[dt]), pb, o[dt][t],
                                                                        0, 0, 0);
             }
+            // the next tile's exponentials run under this tile's PV MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x002, 20, 1);
+#pragma unroll
+            for (int t = 0; t + 1 < T; ++t)
+#pragma unroll
+                for (int i = 0; i < DT + 1; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+                    if (i < 2) __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);
+                    else __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);
+                }
+            __builtin_amdgcn_sched_group_barrier(0x008, DT + 1, 1);
         };
-        if (npair > 0) issue(0, 0);
+        if (npair > 0) issue.template operator()<false>(0, 0);
         if (lane == 0) next = claim();  // overlaps the first pair's round trip
-        if (npair > 1) issue(1, 1);
+        if (npair > 1) issue.template operator()<false>(1, 1);
         // pairs every row sees whole: both pages below the first row's limit
         // (rows are token-major, limits grow with the row)
         const int open = min(p.causal ? st + qt * p.tq + 1 : st + len, eff) / BS;
+        const int full = np / 2 - 2;  // pairs pj < full have two whole pairs behind them
         int pj = 0, s = 0;
-        for (; pj < min(open / 2, npair); ++pj, s ^= 1) pair.template operator()<false>(pj, s);
-        for (; pj < npair; ++pj, s ^= 1) pair.template operator()<true>(pj, s);
+        for (; pj < min(open / 2, full); ++pj, s ^= 1) pair.template operator()<false, true>(pj, s);
+        for (; pj < min(open / 2, npair); ++pj, s ^= 1) pair.template operator()<false, false>(pj, s);
+        for (; pj < npair; ++pj, s ^= 1) pair.template operator()<true, false>(pj, s);
 
         // rows of this lane: dims DT*(4*grp+i)+dt of row 16 t + col
 #pragma unroll
