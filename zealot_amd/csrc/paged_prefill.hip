@@ -45,8 +45,12 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWave = 64;
-constexpr int kRows = 64;            // query rows per item (4 MFMA tiles)
-constexpr int kTiles = kRows / 16;
+constexpr int kWaves = 2;             // waves per workgroup, one per SIMD
+constexpr int kWaveRows = 64;         // query rows per wave (4 MFMA tiles)
+constexpr int kRows = kWaves * kWaveRows;  // query rows per item
+constexpr int kTiles = kWaveRows / 16;
+constexpr int kStages = 4;            // page pairs in LDS: the one computed on, three in flight
+static_assert((kStages & (kStages - 1)) == 0 && kStages >= 3, "stage ring");
 constexpr int kMaxBins = zk::kPrefillMaxPages;  // LDS block ids per item; plan-kernel bins
 constexpr int kXcds = 8;                         // XCDs of an MI355X
 constexpr int kXcdBins = kMaxBins / kXcds;       // longest-first bins per XCD queue
@@ -69,7 +73,7 @@ struct PParams {
     int32_t *eff;         // [N] context after the page walk
     int4 *items;          // {n, query tile, pages, kv-head}, per-XCD segments
     int32_t *work;        // [0] total items; XCD x at 64 + 32 x: segment start, end, queue head
-    int num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks, tq, num_waves, max_items;
+    int num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks, tq, num_groups, max_items;
     int64_t num_blocks;
     float scale_log2;
     int grouped, q_f32, causal;
@@ -159,7 +163,7 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
         int32_t *w = p.work + 64 + kQueueStride * t;
         w[0] = start;
         w[1] = end;
-        w[2] = start + p.num_waves / kXcds;
+        w[2] = start + p.num_groups / kXcds;
     }
     __syncthreads();
     for (int g = t; g < groups; g += 1024) {
@@ -188,6 +192,9 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+// workgroup barrier without the fences of __syncthreads (those would wait for
+// every load in flight); the memory clobber keeps LDS accesses on their side
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
 __device__ __forceinline__ float xor16(float v) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (0x10 << 10)));
 }
@@ -207,7 +214,7 @@ template <>
 struct LdsVec<4> { typedef uint32_t T; };
 
 template <int KV, int D, int G>
-__global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
+__global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p) {
     constexpr int BS = 16;
     constexpr int ELT = KV == ZK_BF16 ? 2 : 1;
     constexpr int DG = D / 4;         // head dims per lane group in QK
@@ -217,17 +224,20 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
     constexpr int CPR = RB / 16;      // 16-byte chunks per row
     constexpr int PAGE = BS * RB;     // bytes per (block, kv-head) page
     constexpr int LPK = PAGE / 1024;  // global_load_lds per page of K (or V)
-    constexpr int LPP = 2 * LPK;
+    constexpr int LPW = 2 * LPK;      // loads per wave and pair: K and V of one page
     constexpr int KBYTES = DG * ELT;
     constexpr int KCH = KBYTES / 16;
     constexpr int VTB = DT * ELT;
     constexpr int T = kTiles;
     static_assert(PAGE % 1024 == 0 && KBYTES % 16 == 0 && DT % 2 == 0, "page shape");
     typedef typename LdsVec<VTB>::T vtrow_t;
-    __shared__ __attribute__((aligned(16))) char lds[2][2][2][PAGE];  // [stage][page of the pair][K|V]
-    __shared__ int32_t bids[kMaxBins];
+    __shared__ __attribute__((aligned(16))) char lds[kStages][2][2][PAGE];  // [stage][page of the pair][K|V]
+    __shared__ int item_bcast;
 
-    const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+    // wave w computes rows 64 w .. 64 w + 63 of every item and loads page w
+    // of every pair; both waves read both pages
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave, col = lane & 15, grp = lane >> 4;
     const int H = p.num_heads, Hkv = p.num_kv_heads;
     uint32_t kg[LPK], vg[LPK];
 #pragma unroll
@@ -250,33 +260,40 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
     int item = myq[0] + (int)blockIdx.x / kXcds;
     if (item >= myq[1]) item = -1;
     int next = -1;
-    // lane 0: next item from this XCD's queue, else from the others'
+    // thread 0: next item from this XCD's queue, else from the others'
     auto claim = [&]() {
         for (int k = 0; k < kXcds; ++k) {
-            int32_t *w = p.work + 64 + kQueueStride * ((xcd + k) % kXcds);
-            if (__hip_atomic_load(&w[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= w[1]) continue;
-            const int v = atomicAdd(&w[2], 1);
-            if (v < w[1]) return v;
+            int32_t *wq = p.work + 64 + kQueueStride * ((xcd + k) % kXcds);
+            if (__hip_atomic_load(&wq[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= wq[1]) continue;
+            const int v = atomicAdd(&wq[2], 1);
+            if (v < wq[1]) return v;
         }
         return -1;
     };
-    if (item < 0) {
-        if (lane == 0) next = claim();
-        item = __builtin_amdgcn_readfirstlane(next);
-    }
+    // thread 0's item id to both waves, once both are done with the last
+    // item (its LDS stages and the broadcast slot)
+    auto bcast = [&](int v) {
+        wg_barrier();
+        if (threadIdx.x == 0) item_bcast = v;
+        wait_lgkmcnt0();
+        wg_barrier();
+        return __builtin_amdgcn_readfirstlane(item_bcast);
+    };
+    if (item < 0) item = bcast(threadIdx.x == 0 ? claim() : -1);
     while (item >= 0) {
         const int4 desc = p.items[item];
         const int n = desc.x, qt = desc.y, np = desc.z, kvh = desc.w;
         const int len = chunk_len(p, n), st = p.start[n], eff = p.eff[n];
-        const int64_t row0 = chunk_row0(p, n) + (int64_t)qt * p.tq;  // first q row of the tile
+        const int64_t row0 = chunk_row0(p, n) + (int64_t)qt * p.tq;  // first q row of the item
 
-        // rows: column col of tile t is row r = 16 t + col = token r / G, head r % G
+        // rows: column col of this wave's tile t is item row r = 64 w + 16 t + col
+        // = token r / G, head r % G
         bf16x8 qf[T][KK];
         int lim[T];       // keys at positions < lim[t] are visible to this lane's row
         bool real[T];     // the row is a chunk token (not padding past the chunk)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const int r = 16 * t + col, tok = qt * p.tq + r / G;
+            const int r = kWaveRows * w + 16 * t + col, tok = qt * p.tq + r / G;
             real[t] = tok < len;
             const int tok_c = min(tok, len - 1);  // padding rows see what the last row sees
             lim[t] = min(p.causal ? st + tok_c + 1 : st + len, eff);
@@ -307,44 +324,28 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
             sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
             vscale = p.v_scales[(size_t)n * Hkv + kvh];
         }
-        // block ids of the tile's pages into LDS (the LDS writes wait for
-        // their loads, retiring the Q loads too)
-        const int32_t *trow = p.bt + (size_t)n * p.max_blocks;
-        for (int i0 = 0; i0 < np; i0 += 8 * kWave) {
-            int32_t b[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + j * kWave + lane;
-                b[j] = i < np ? trow[i] : 0;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + j * kWave + lane;
-                if (i < np) bids[i] = b[j];
-            }
-        }
-        wait_lgkmcnt0();
+        // block ids by scalar loads (a constant-space view of the table: the
+        // kernel never writes it)
+        typedef const __attribute__((address_space(4))) int32_t *ctab_t;
+        const ctab_t trow = (ctab_t)(p.bt + (size_t)n * p.max_blocks);
         const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
         const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
         const size_t block_bytes = (size_t)PAGE * Hkv;
         // Pages go through LDS in pairs: 32 keys per PV step feed the
-        // 16x16x32 MFMA (the 16x16x16 form runs at half its rate).  A pair's
-        // second page may not exist (odd page count): it is not loaded and
-        // its keys lie past every row's limit.
-        auto issue = [&]<bool FULL>(int pj, int s) {
+        // 16x16x32 MFMA (the 16x16x16 form runs at half its rate).  Wave w
+        // loads page w of every pair into the pair's stage.  A missing second
+        // page (odd page count) is loaded as a copy of the first, so both
+        // waves issue the same loads per pair; its keys lie past every row's
+        // limit and its V rows are zeroed below.
+        auto issue = [&](int pj) {
+            const int stg = pj & (kStages - 1);
+            const int blk = trow[min(2 * pj + w, np - 1)];
+            const char *kp = kbase + (size_t)blk * block_bytes;
+            const char *vp = vbase + (size_t)blk * block_bytes;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int pi = 2 * pj + h;
-                if (FULL || pi < np) {
-                    const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
-                    const char *kp = kbase + (size_t)blk * block_bytes;
-                    const char *vp = vbase + (size_t)blk * block_bytes;
+            for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[stg][w][0] + 1024 * j));
 #pragma unroll
-                    for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[s][h][0] + 1024 * j));
-#pragma unroll
-                    for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[s][h][1] + 1024 * j));
-                }
-            }
+            for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[stg][w][1] + 1024 * j));
         };
         f32x4 o[DT][T];
         // m: the rows' reference max (log2 units); lsum: every element of
@@ -364,33 +365,38 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
         // missing second page (its LDS holds another page's bytes, which may
         // not even be finite as fp8)
         const int vlim = min(eff, np * BS);
-        // MASK: the pair holds keys some row of the tile may not see (the
+        // MASK: the pair holds keys some row of the item may not see (the
         // diagonal pages, stale rows past the context, a missing second
         // page); the pairs before run without the per-element compares.
-        // FULL: this pair and the two behind it hold two pages each, so the
-        // wait and the next issue take no branch and the whole pair up to
-        // the rescale test is one scheduling region.
-        auto pair = [&]<bool MASK, bool FULL>(int pj, int s) {
-            const int left = np - 2 * (pj + 1);  // pages of the pair in flight behind this one
-            if (FULL || left >= 2) wait_vmcnt<2 * LPP>();
-            else if (left == 1) wait_vmcnt<LPP>();
+        // FULL: pair pj + kStages - 1 exists and two pairs are in flight
+        // behind this one, so the wait and the refill take no branch and the
+        // whole pair up to the rescale test is one scheduling region.
+        auto pair = [&]<bool MASK, bool FULL>(int pj) {
+            // this wave's half of pair pj is in (the pairs behind it may still
+            // fly); the barrier brings the other wave's half and says both
+            // waves have left pair pj - 1, whose stage takes pair pj + 3
+            const int behind = npair - 1 - pj;
+            if (FULL || behind >= kStages - 2) wait_vmcnt<(kStages - 2) * LPW>();
+            else if (behind == 1) wait_vmcnt<LPW>();
             else wait_vmcnt<0>();
+            wg_barrier();
+            const int stg = pj & (kStages - 1);
             uint32_t kw[2][KBYTES / 4];
             vtrow_t vt[2][4];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
                 for (int f = 0; f < KCH; ++f) {
-                    const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[s][h][0] + kl[f]);
+                    const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[stg][h][0] + kl[f]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) kw[h][4 * f + j] = c4[j];
                 }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) vt[h][i] = *reinterpret_cast<const vtrow_t *>(lds[s][h][1] + vt_off + i * RB);
+                for (int i = 0; i < 4; ++i) vt[h][i] = *reinterpret_cast<const vtrow_t *>(lds[stg][h][1] + vt_off + i * RB);
             }
-            wait_lgkmcnt0();
-            if constexpr (FULL) issue.template operator()<true>(pj + 2, s);
-            else if (pj + 2 < npair) issue.template operator()<false>(pj + 2, s);
+            // the refill goes to another stage; issued after this stage's
+            // reads, so no read here waits for it
+            if (FULL || pj + kStages - 1 < npair) issue(pj + kStages - 1);
 
             bf16x8 kop[2][KK];
 #pragma unroll
@@ -518,24 +524,25 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
                 }
             __builtin_amdgcn_sched_group_barrier(0x008, DT + 1, 1);
         };
-        if (npair > 0) issue.template operator()<false>(0, 0);
-        if (lane == 0) next = claim();  // overlaps the first pair's round trip
-        if (npair > 1) issue.template operator()<false>(1, 1);
-        // pairs every row sees whole: both pages below the first row's limit
-        // (rows are token-major, limits grow with the row)
+        if (npair > 0) issue(0);
+        if (threadIdx.x == 0) next = claim();  // overlaps the first pairs' round trip
+        if (npair > 1) issue(1);
+        if (npair > 2) issue(2);
+        // pairs every row sees whole: both pages below the item's first row's
+        // limit (rows are token-major, limits grow with the row)
         const int open = min(p.causal ? st + qt * p.tq + 1 : st + len, eff) / BS;
-        const int full = np / 2 - 2;  // pairs pj < full have two whole pairs behind them
-        int pj = 0, s = 0;
-        for (; pj < min(open / 2, full); ++pj, s ^= 1) pair.template operator()<false, true>(pj, s);
-        for (; pj < min(open / 2, npair); ++pj, s ^= 1) pair.template operator()<false, false>(pj, s);
-        for (; pj < npair; ++pj, s ^= 1) pair.template operator()<true, false>(pj, s);
+        const int full = npair - (kStages - 1);  // pairs pj < full refill without a test
+        int pj = 0;
+        for (; pj < min(open / 2, full); ++pj) pair.template operator()<false, true>(pj);
+        for (; pj < min(open / 2, npair); ++pj) pair.template operator()<false, false>(pj);
+        for (; pj < npair; ++pj) pair.template operator()<true, false>(pj);
 
-        // rows of this lane: dims DT*(4*grp+i)+dt of row 16 t + col
+        // rows of this lane: dims DT*(4*grp+i)+dt of item row 64 w + 16 t + col
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float lt = lsum[t][0];  // the row's total (every element holds it)
             if (!real[t]) continue;
-            const int r = 16 * t + col;
+            const int r = kWaveRows * w + 16 * t + col;
             const float inv = lt > 0.0f ? vscale / lt : 0.0f;
             const size_t ob = ((size_t)(row0 + r / G) * H + qhead_of(p, kvh, r % G, G)) * D;
 #pragma unroll
@@ -553,27 +560,28 @@ __global__ void __launch_bounds__(kWave) prefill_mfma_kernel(PParams p) {
                 }
             }
         }
-        item = __builtin_amdgcn_readfirstlane(next);
+        item = bcast(next);
     }
 }
 
 template <int KV, int D>
 bool launch_g(const PParams &p, hipStream_t s, int G) {
     switch (G) {
-        case 1: prefill_mfma_kernel<KV, D, 1><<<p.num_waves, kWave, 0, s>>>(p); return true;
-        case 2: prefill_mfma_kernel<KV, D, 2><<<p.num_waves, kWave, 0, s>>>(p); return true;
-        case 4: prefill_mfma_kernel<KV, D, 4><<<p.num_waves, kWave, 0, s>>>(p); return true;
-        case 8: prefill_mfma_kernel<KV, D, 8><<<p.num_waves, kWave, 0, s>>>(p); return true;
+        case 1: prefill_mfma_kernel<KV, D, 1><<<p.num_groups, kWave * kWaves, 0, s>>>(p); return true;
+        case 2: prefill_mfma_kernel<KV, D, 2><<<p.num_groups, kWave * kWaves, 0, s>>>(p); return true;
+        case 4: prefill_mfma_kernel<KV, D, 4><<<p.num_groups, kWave * kWaves, 0, s>>>(p); return true;
+        case 8: prefill_mfma_kernel<KV, D, 8><<<p.num_groups, kWave * kWaves, 0, s>>>(p); return true;
         default: return false;
     }
 }
 
-int persistent_waves() {
+// persistent workgroups: one wave per SIMD
+int persistent_groups() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    return cus * 4;
+    return cus * (4 / kWaves);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -698,7 +706,7 @@ int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void
     p.block_size = block_size;
     p.max_blocks = max_blocks_per_seq;
     p.tq = kRows / G;
-    p.num_waves = persistent_waves();
+    p.num_groups = persistent_groups();
     p.max_items = max_items_for(num_seqs, total_q, num_heads, num_kv_heads);
     p.num_blocks = num_blocks;
     p.scale_log2 = scale * kLog2e;
