@@ -49,7 +49,7 @@ constexpr int kWaves = 2;             // waves per workgroup, one per SIMD
 constexpr int kWaveRows = 64;         // query rows per wave (4 MFMA tiles)
 constexpr int kRows = kWaves * kWaveRows;  // query rows per item
 constexpr int kTiles = kWaveRows / 16;
-constexpr int kStages = 4;            // page pairs in LDS: the one computed on, three in flight
+constexpr int kStages = 4;            // page pairs in LDS: the one computed on, the rest in flight
 static_assert((kStages & (kStages - 1)) == 0 && kStages >= 3, "stage ring");
 constexpr int kMaxBins = zk::kPrefillMaxPages;  // LDS block ids per item; plan-kernel bins
 constexpr int kXcds = 8;                         // XCDs of an MI355X
@@ -224,7 +224,8 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
     constexpr int CPR = RB / 16;      // 16-byte chunks per row
     constexpr int PAGE = BS * RB;     // bytes per (block, kv-head) page
     constexpr int LPK = PAGE / 1024;  // global_load_lds per page of K (or V)
-    constexpr int LPW = 2 * LPK;      // loads per wave and pair: K and V of one page
+    constexpr int PARTS = 4 / kWaves;  // (page, K|V) parts of a pair each wave loads
+    constexpr int LPW = PARTS * LPK;   // loads per wave and pair
     constexpr int KBYTES = DG * ELT;
     constexpr int KCH = KBYTES / 16;
     constexpr int VTB = DT * ELT;
@@ -339,13 +340,15 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         // limit and its V rows are zeroed below.
         auto issue = [&](int pj) {
             const int stg = pj & (kStages - 1);
-            const int blk = trow[min(2 * pj + w, np - 1)];
-            const char *kp = kbase + (size_t)blk * block_bytes;
-            const char *vp = vbase + (size_t)blk * block_bytes;
 #pragma unroll
-            for (int j = 0; j < LPK; ++j) g2l16(kp + kg[j], (lds_void *)(lds[stg][w][0] + 1024 * j));
+            for (int q = 0; q < PARTS; ++q) {
+                const int part = PARTS * w + q, h = part >> 1, kind = part & 1;  // page of the pair, K or V
+                const int blk = trow[min(2 * pj + h, np - 1)];
+                const char *src = (kind ? vbase : kbase) + (size_t)blk * block_bytes;
 #pragma unroll
-            for (int j = 0; j < LPK; ++j) g2l16(vp + vg[j], (lds_void *)(lds[stg][w][1] + 1024 * j));
+                for (int j = 0; j < LPK; ++j)
+                    g2l16(src + (kind ? vg[j] : kg[j]), (lds_void *)(lds[stg][h][kind] + 1024 * j));
+            }
         };
         f32x4 o[DT][T];
         // m: the rows' reference max (log2 units); lsum: every element of
@@ -373,8 +376,9 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         // whole pair up to the rescale test is one scheduling region.
         auto pair = [&]<bool MASK, bool FULL>(int pj) {
             // this wave's half of pair pj is in (the pairs behind it may still
-            // fly); the barrier brings the other wave's half and says both
-            // waves have left pair pj - 1, whose stage takes pair pj + 3
+            // fly); the barrier brings the other waves' parts and says all
+            // waves have left pair pj - 1, whose stage takes pair
+            // pj + kStages - 1
             const int behind = npair - 1 - pj;
             if (FULL || behind >= kStages - 2) wait_vmcnt<(kStages - 2) * LPW>();
             else if (behind == 1) wait_vmcnt<LPW>();
@@ -526,8 +530,7 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         };
         if (npair > 0) issue(0);
         if (threadIdx.x == 0) next = claim();  // overlaps the first pairs' round trip
-        if (npair > 1) issue(1);
-        if (npair > 2) issue(2);
+        for (int i = 1; i < min(npair, kStages - 1); ++i) issue(i);
         // pairs every row sees whole: both pages below the item's first row's
         // limit (rows are token-major, limits grow with the row)
         const int open = min(p.causal ? st + qt * p.tq + 1 : st + len, eff) / BS;
