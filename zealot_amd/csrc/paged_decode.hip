@@ -841,6 +841,65 @@ __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
         if (lane + 64 * c < D) store_out(p, (qrow(p, n) * p.num_heads + h) * D + lane + 64 * c, acc[c] * inv);
 }
 
+// The same merge for D = 4 * LP (D in {64, 128, 256}): LP lanes hold a
+// partition's partial output as one float4 each, so one load instruction
+// covers 64 / LP partitions and all of a sequence's partitions are in flight
+// at once (the loop above waits for each group of eight).  Lane i reads
+// partition i's (m, l) once for the maximum, the sum and its weight.
+template <int D>
+__global__ void __launch_bounds__(kWave) decode_reduce_vec_kernel(Params p) {
+    constexpr int LP = D / 4, P = kWave / LP, U = 16;  // lanes per partition, partitions per load, loads per lane
+    static_assert(D % 4 == 0 && kWave % LP == 0, "partition layout");
+    const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
+    const int ns = shared_parts_of(p, n);
+    const int nparts = ns + private_parts_of(p, n);
+    if (ns == 0 && nparts <= 1) return;  // written by the partition kernel
+    const size_t base = ((size_t)n * p.num_heads + h) * p.max_parts;
+    const float2 none = make_float2(-INFINITY, 0.0f);
+    const float2 ml0 = lane < nparts ? p.ml[base + lane] : none;
+    float M = ml0.x;
+    for (int i = lane + kWave; i < nparts; i += kWave) M = fmaxf(M, p.ml[base + i].x);
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    auto weight = [&](float2 v) { return v.x == -INFINITY ? 0.0f : exp2f(v.x - M); };
+    float L = ml0.y * weight(ml0);
+    for (int i = lane + kWave; i < nparts; i += kWave) {
+        const float2 v = p.ml[base + i];
+        L += v.y * weight(v);
+    }
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const int sub = lane / LP, j = lane % LP;  // partition slot within a load, float4 index
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nparts; c0 += kWave) {  // weights of partitions c0 .. c0 + 63 in lanes
+        const float w = weight(c0 == 0 ? ml0 : (c0 + lane < nparts ? p.ml[base + c0 + lane] : none));
+        const int cnt = min(kWave, nparts - c0);
+        for (int i0 = 0; i0 < cnt; i0 += P * U) {
+            f32x4 x[U];
+            float wi[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int i = i0 + P * u + sub;
+                wi[u] = __shfl(w, min(i, kWave - 1));
+                x[u] = i < cnt ? *reinterpret_cast<const f32x4 *>(p.po + (base + c0 + i) * D + 4 * j)
+                               : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (i0 + P * u + sub < cnt)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[c] = fmaf(wi[u], x[u][c], acc[c]);
+        }
+    }
+    // the P partition slots of a load sit LP lanes apart
+#pragma unroll
+    for (int off = LP; off < kWave; off <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += __shfl_xor(acc[c], off);
+    if (sub == 0)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) store_out(p, (qrow(p, n) * p.num_heads + h) * D + 4 * j + c, acc[c] * inv);
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
@@ -1079,7 +1138,10 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     if (max_parts > 1 || shared) {
         dim3 rgrid(num_heads, num_seqs);
         KernelTimer timer("decode_reduce", s);
-        decode_reduce_kernel<<<rgrid, kWave, 0, s>>>(p);
+        if (head_dim == 128) decode_reduce_vec_kernel<128><<<rgrid, kWave, 0, s>>>(p);
+        else if (head_dim == 64) decode_reduce_vec_kernel<64><<<rgrid, kWave, 0, s>>>(p);
+        else if (head_dim == 256) decode_reduce_vec_kernel<256><<<rgrid, kWave, 0, s>>>(p);
+        else decode_reduce_kernel<<<rgrid, kWave, 0, s>>>(p);
         if (int rc = check_launch("zk_paged_decode reduce")) return rc;
     }
     return ZK_OK;
