@@ -204,6 +204,7 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2_t));
 }
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 template <int BYTES>
 struct LdsVec;
 template <>
@@ -245,7 +246,9 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
     for (int j = 0; j < LPK; ++j) {
         const int q = 64 * j + lane, row = q / CPR, c = (q % CPR) ^ (row % CPR);
         kg[j] = row * RB + c * 16;
-        vg[j] = q * 16;
+        // bf16 V: chunk c of row r sits at slot c ^ 2 (r mod CPR/2), so the
+        // transposed reads below hit distinct banks; fp8 V stays natural
+        vg[j] = KV == ZK_BF16 ? row * RB + ((q % CPR) ^ ((row % (CPR / 2)) << 1)) * 16 : q * 16;
     }
     uint32_t kl[KCH];
 #pragma unroll
@@ -254,6 +257,14 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         kl[f] = (row * CPR + (c ^ (row % CPR))) * 16;
     }
     const uint32_t vt_off = (uint32_t)((4 * grp) * RB + col * VTB);
+    // bf16 V^T fragments by ds_read_b64_tr_b16: in each 16-lane group, lane
+    // j names 4 dims of key 4 grp + j / 4 and lane c receives dim c of those
+    // 4 keys.  Dim tile dt of a page: vtr_base ^ (32 dt) (the XOR only moves
+    // the swizzled slot).
+    const uint32_t vtr_base = [&] {
+        const int j = col, r = 4 * grp + j / 4;
+        return (uint32_t)(r * RB + 32 * (r % (CPR / 2)) + 16 * ((j % 4) / 2) + 8 * (j % 2));
+    }();
 
     // this wave's XCD queue (round-robin dispatch); its first item is static
     const int xcd = blockIdx.x % kXcds;
@@ -387,6 +398,8 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
             const int stg = pj & (kStages - 1);
             uint32_t kw[2][KBYTES / 4];
             vtrow_t vt[2][4];
+            u32x4 va[DT];  // V^T operand: k slots 8 grp + i (i < 4) are keys 4 grp + i of the first page,
+                           // 8 grp + 4 + i those of the second, as in P^T below
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -395,8 +408,20 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) kw[h][4 * f + j] = c4[j];
                 }
+                if constexpr (KV == ZK_BF16) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) vt[h][i] = *reinterpret_cast<const vtrow_t *>(lds[stg][h][1] + vt_off + i * RB);
+                    for (int dt = 0; dt < DT; ++dt) {
+                        const u32x2 t2 = __builtin_bit_cast(
+                            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (__attribute__((address_space(3))) v4i16 *)(lds[stg][h][1] + (vtr_base ^ (32 * dt)))));
+                        va[dt][2 * h] = t2[0];
+                        va[dt][2 * h + 1] = t2[1];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        vt[h][i] = *reinterpret_cast<const vtrow_t *>(lds[stg][h][1] + vt_off + i * RB);
+                }
             }
             // the refill goes to another stage; issued after this stage's
             // reads, so no read here waits for it
@@ -428,17 +453,23 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                     for (int kk = 0; kk < KK; ++kk)
                         sacc[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[h][kk], qf[t][kk], sacc[h][t], 0, 0, 0);
                 }
-            // V^T operand: k slots 8 grp + i (i < 4) are keys 4 grp + i of the
-            // first page, 8 grp + 4 + i those of the second, as in P^T below
-            u32x4 va[DT];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                uint32_t w[4][DT / 2];  // V rows as bf16 pairs
+                const int key0 = (2 * pj + h) * BS + 4 * grp;  // position of this lane's first key
+                if constexpr (KV == ZK_BF16) {
+                    if (MASK && key0 + 4 > vlim) {  // stale rows past the context, a missing page: keep out of O
+                        const uint32_t lo = (key0 >= vlim ? 0u : 0xffffu) | (key0 + 1 >= vlim ? 0u : 0xffff0000u);
+                        const uint32_t hi = (key0 + 2 >= vlim ? 0u : 0xffffu) | (key0 + 3 >= vlim ? 0u : 0xffff0000u);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if constexpr (KV == ZK_BF16) {
-                        __builtin_memcpy(w[i], &vt[h][i], 2 * DT);
-                    } else {
+                        for (int dt = 0; dt < DT; ++dt) {
+                            va[dt][2 * h] &= lo;
+                            va[dt][2 * h + 1] &= hi;
+                        }
+                    }
+                } else {
+                    uint32_t w[4][DT / 2];  // V rows as bf16 pairs
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
                         uint32_t b8[DT / 4];
                         __builtin_memcpy(b8, &vt[h][i], DT);
 #pragma unroll
@@ -448,21 +479,20 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                             w[i][2 * j + 1] = c2[1];
                         }
                     }
-                }
-                const int key0 = (2 * pj + h) * BS + 4 * grp;  // position of this lane's first key
-                if (MASK && key0 + 4 > vlim) {  // stale rows past the context, a missing page: keep out of O
+                    if (MASK && key0 + 4 > vlim) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (key0 + i >= vlim)
+                        for (int i = 0; i < 4; ++i)
+                            if (key0 + i >= vlim)
 #pragma unroll
-                            for (int j = 0; j < DT / 2; ++j) w[i][j] = 0u;
-                }
+                                for (int j = 0; j < DT / 2; ++j) w[i][j] = 0u;
+                    }
 #pragma unroll
-                for (int j = 0; j < DT / 2; ++j) {
-                    va[2 * j][2 * h] = __builtin_amdgcn_perm(w[1][j], w[0][j], 0x05040100u);
-                    va[2 * j][2 * h + 1] = __builtin_amdgcn_perm(w[3][j], w[2][j], 0x05040100u);
-                    va[2 * j + 1][2 * h] = __builtin_amdgcn_perm(w[1][j], w[0][j], 0x07060302u);
-                    va[2 * j + 1][2 * h + 1] = __builtin_amdgcn_perm(w[3][j], w[2][j], 0x07060302u);
+                    for (int j = 0; j < DT / 2; ++j) {
+                        va[2 * j][2 * h] = __builtin_amdgcn_perm(w[1][j], w[0][j], 0x05040100u);
+                        va[2 * j][2 * h + 1] = __builtin_amdgcn_perm(w[3][j], w[2][j], 0x05040100u);
+                        va[2 * j + 1][2 * h] = __builtin_amdgcn_perm(w[1][j], w[0][j], 0x07060302u);
+                        va[2 * j + 1][2 * h + 1] = __builtin_amdgcn_perm(w[3][j], w[2][j], 0x07060302u);
+                    }
                 }
             }
             const int key0a = 2 * pj * BS + 4 * grp, key0b = key0a + BS;
@@ -540,7 +570,8 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         for (; pj < min(open / 2, npair); ++pj) pair.template operator()<false, false>(pj);
         for (; pj < npair; ++pj) pair.template operator()<true, false>(pj);
 
-        // rows of this lane: dims DT*(4*grp+i)+dt of item row 64 w + 16 t + col
+        // rows of this lane: item row 64 w + 16 t + col, dims 16 dt + 4 grp + i
+        // (bf16 pools, transposed V reads) or DT (4 grp + i) + dt (fp8 pools)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float lt = lsum[t][0];  // the row's total (every element holds it)
@@ -548,18 +579,34 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
             const int r = kWaveRows * w + 16 * t + col;
             const float inv = lt > 0.0f ? vscale / lt : 0.0f;
             const size_t ob = ((size_t)(row0 + r / G) * H + qhead_of(p, kvh, r % G, G)) * D;
+            if constexpr (KV == ZK_BF16) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (p.q_f32) {
-                    float v[DT];
+                for (int dt = 0; dt < DT; ++dt) {
+                    const size_t od = ob + 16 * dt + 4 * grp;
+                    if (p.q_f32) {
+                        const f32x4 v = o[dt][t] * inv;
+                        __builtin_memcpy((float *)p.out + od, &v, sizeof(v));
+                    } else {
+                        const uint32_t v[2] = {bf16x2_rne(o[dt][t][0] * inv, o[dt][t][1] * inv),
+                                               bf16x2_rne(o[dt][t][2] * inv, o[dt][t][3] * inv)};
+                        __builtin_memcpy((uint16_t *)p.out + od, v, sizeof(v));
+                    }
+                }
+            } else {
 #pragma unroll
-                    for (int dt = 0; dt < DT; ++dt) v[dt] = o[dt][t][i] * inv;
-                    __builtin_memcpy((float *)p.out + ob + DT * (4 * grp + i), v, sizeof(v));
-                } else {
-                    uint32_t v[DT / 2];
+                for (int i = 0; i < 4; ++i) {
+                    if (p.q_f32) {
+                        float v[DT];
 #pragma unroll
-                    for (int j = 0; j < DT / 2; ++j) v[j] = bf16x2_rne(o[2 * j][t][i] * inv, o[2 * j + 1][t][i] * inv);
-                    __builtin_memcpy((uint16_t *)p.out + ob + DT * (4 * grp + i), v, sizeof(v));
+                        for (int dt = 0; dt < DT; ++dt) v[dt] = o[dt][t][i] * inv;
+                        __builtin_memcpy((float *)p.out + ob + DT * (4 * grp + i), v, sizeof(v));
+                    } else {
+                        uint32_t v[DT / 2];
+#pragma unroll
+                        for (int j = 0; j < DT / 2; ++j)
+                            v[j] = bf16x2_rne(o[2 * j][t][i] * inv, o[2 * j + 1][t][i] * inv);
+                        __builtin_memcpy((uint16_t *)p.out + ob + DT * (4 * grp + i), v, sizeof(v));
+                    }
                 }
             }
         }
