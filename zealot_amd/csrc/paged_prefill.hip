@@ -331,6 +331,12 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                 for (int kk = 0; kk < KK; ++kk) qf[t][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
             }
         }
+        // Q fragments live in AGPRs (MFMA reads its A/B operands from either
+        // file): VGPRs hold the accumulators and the page temporaries
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+a"(qf[t][kk]));
         float sl2 = p.scale_log2, vscale = 1.0f;
         if constexpr (KV == ZK_FP8_E4M3) {
             sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
