@@ -385,35 +385,44 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         // missing second page (its LDS holds another page's bytes, which may
         // not even be finite as fp8)
         const int vlim = min(eff, np * BS);
-        // MASK: the pair holds keys some row of the item may not see (the
-        // diagonal pages, stale rows past the context, a missing second
-        // page); the pairs before run without the per-element compares.
-        // FULL: pair pj + kStages - 1 exists and two pairs are in flight
-        // behind this one, so the wait and the refill take no branch and the
-        // whole pair up to the rescale test is one scheduling region.
-        auto pair = [&]<bool MASK, bool FULL>(int pj) {
-            // this wave's half of pair pj is in (the pairs behind it may still
-            // fly); the barrier brings the other waves' parts and says all
-            // waves have left pair pj - 1, whose stage takes pair
-            // pj + kStages - 1
-            const int behind = npair - 1 - pj;
-            if (FULL || behind >= kStages - 2) wait_vmcnt<(kStages - 2) * LPW>();
-            else if (behind == 1) wait_vmcnt<LPW>();
-            else wait_vmcnt<0>();
-            wg_barrier();
+        // pairs every row sees whole: both pages below the item's first row's
+        // limit (rows are token-major, limits grow with the row)
+        const int open = min(p.causal ? st + qt * p.tq + 1 : st + len, eff) / BS / 2;
+
+        // K of pair pj as MFMA A operands (AGPRs: the MFMAs read them there)
+        auto read_k = [&](int pj, bf16x8 (&kop)[2][KK]) {
             const int stg = pj & (kStages - 1);
-            uint32_t kw[2][KBYTES / 4];
-            vtrow_t vt[2][4];
-            u32x4 va[DT];  // V^T operand: k slots 8 grp + i (i < 4) are keys 4 grp + i of the first page,
-                           // 8 grp + 4 + i those of the second, as in P^T below
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
+                uint32_t kw[KBYTES / 4];
 #pragma unroll
                 for (int f = 0; f < KCH; ++f) {
                     const u32x4 c4 = *reinterpret_cast<const u32x4 *>(lds[stg][h][0] + kl[f]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) kw[h][4 * f + j] = c4[j];
+                    for (int j = 0; j < 4; ++j) kw[4 * f + j] = c4[j];
                 }
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    u32x4 w4;
+                    if constexpr (KV == ZK_BF16) {
+                        w4 = u32x4{kw[4 * kk], kw[4 * kk + 1], kw[4 * kk + 2], kw[4 * kk + 3]};
+                    } else {
+                        const u32x2 lo2 = e4m3x4_to_bf16x4(kw[2 * kk]), hi2 = e4m3x4_to_bf16x4(kw[2 * kk + 1]);
+                        w4 = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+                    }
+                    kop[h][kk] = __builtin_bit_cast(bf16x8, w4);
+                    asm volatile("" : "+a"(kop[h][kk]));
+                }
+            }
+        };
+        // V^T of pair pj as MFMA A operands: k slots 8 grp + i (i < 4) are
+        // keys 4 grp + i of the first page, 8 grp + 4 + i those of the second,
+        // as in P^T.  ZERO: rows at or past vlim are zeroed.
+        auto read_v = [&]<bool ZERO>(int pj, u32x4 (&va)[DT]) {
+            const int stg = pj & (kStages - 1);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int key0 = (2 * pj + h) * BS + 4 * grp;  // position of this lane's first key
                 if constexpr (KV == ZK_BF16) {
 #pragma unroll
                     for (int dt = 0; dt < DT; ++dt) {
@@ -423,47 +432,7 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                         va[dt][2 * h] = t2[0];
                         va[dt][2 * h + 1] = t2[1];
                     }
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        vt[h][i] = *reinterpret_cast<const vtrow_t *>(lds[stg][h][1] + vt_off + i * RB);
-                }
-            }
-            // the refill goes to another stage; issued after this stage's
-            // reads, so no read here waits for it
-            if (FULL || pj + kStages - 1 < npair) issue(pj + kStages - 1);
-
-            bf16x8 kop[2][KK];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    u32x4 w;
-                    if constexpr (KV == ZK_BF16) {
-                        w = u32x4{kw[h][4 * kk], kw[h][4 * kk + 1], kw[h][4 * kk + 2], kw[h][4 * kk + 3]};
-                    } else {
-                        const u32x2 lo2 = e4m3x4_to_bf16x4(kw[h][2 * kk]), hi2 = e4m3x4_to_bf16x4(kw[h][2 * kk + 1]);
-                        w = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
-                    }
-                    kop[h][kk] = __builtin_bit_cast(bf16x8, w);
-                }
-            // tile-major, so each tile's maximum can start while the next
-            // tile's scores are still in the MFMA pipe
-            f32x4 sacc[2][T];
-#pragma unroll
-            for (int t = 0; t < T; ++t)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    sacc[h][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int kk = 0; kk < KK; ++kk)
-                        sacc[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[h][kk], qf[t][kk], sacc[h][t], 0, 0, 0);
-                }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int key0 = (2 * pj + h) * BS + 4 * grp;  // position of this lane's first key
-                if constexpr (KV == ZK_BF16) {
-                    if (MASK && key0 + 4 > vlim) {  // stale rows past the context, a missing page: keep out of O
+                    if (ZERO && key0 + 4 > vlim) {
                         const uint32_t lo = (key0 >= vlim ? 0u : 0xffffu) | (key0 + 1 >= vlim ? 0u : 0xffff0000u);
                         const uint32_t hi = (key0 + 2 >= vlim ? 0u : 0xffffu) | (key0 + 3 >= vlim ? 0u : 0xffff0000u);
 #pragma unroll
@@ -473,11 +442,15 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                         }
                     }
                 } else {
+                    vtrow_t vt[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        vt[i] = *reinterpret_cast<const vtrow_t *>(lds[stg][h][1] + vt_off + i * RB);
                     uint32_t w[4][DT / 2];  // V rows as bf16 pairs
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         uint32_t b8[DT / 4];
-                        __builtin_memcpy(b8, &vt[h][i], DT);
+                        __builtin_memcpy(b8, &vt[i], DT);
 #pragma unroll
                         for (int j = 0; j < DT / 4; ++j) {
                             const u32x2 c2 = e4m3x4_to_bf16x4(b8[j]);
@@ -485,7 +458,7 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                             w[i][2 * j + 1] = c2[1];
                         }
                     }
-                    if (MASK && key0 + 4 > vlim) {
+                    if (ZERO && key0 + 4 > vlim) {
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
                             if (key0 + i >= vlim)
@@ -501,80 +474,148 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                     }
                 }
             }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) asm volatile("" : "+a"(va[dt]));
+        };
+        // raw scores of the pair being turned into weights (the scale sits in
+        // the exponent); -inf past a row's limit
+        float sc[T][8];
+        // masks of pair pj's raw scores (pairs from open on): keys at or past a
+        // row's limit get -inf
+        auto mask_scores = [&](int pj, const f32x4 (&sacc)[2][T], float (&out)[T][8]) {
             const int key0a = 2 * pj * BS + 4 * grp, key0b = key0a + BS;
-            float sc[T][8];  // raw scores; the scale is applied inside the exponent
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    out[t][i] = key0a + i < lim[t] ? sacc[0][t][i] : -INFINITY;
+                    out[t][4 + i] = key0b + i < lim[t] ? sacc[1][t][i] : -INFINITY;
+                }
+        };
+        auto lane_max = [&](const float (&v)[8]) {
+            return fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
+        };
+        if (npair > 0) issue(0);
+        if (threadIdx.x == 0) next = claim();  // overlaps the first pairs' round trip
+        for (int i = 1; i < min(npair, kStages - 1); ++i) issue(i);
+        // pair 0's scores set the rows' reference maxima (key 0 is visible to
+        // every row, so they are finite)
+        if (npair > 0) {
+            const int behind = min(npair - 1, kStages - 2);
+            if (behind >= 2) wait_vmcnt<2 * LPW>();
+            else if (behind == 1) wait_vmcnt<LPW>();
+            else wait_vmcnt<0>();
+            wg_barrier();
+            bf16x8 kop[2][KK];
+            read_k(0, kop);
+            f32x4 sacc[2][T];
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    sacc[h][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk)
+                        sacc[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[h][kk], qf[t][kk], sacc[h][t], 0, 0, 0);
+                }
+            mask_scores(0, sacc, sc);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float cm = lane_max(sc[t]) * sl2;
+                cm = fmaxf(cm, xor16(cm));
+                m[t] = fmaxf(cm, xor32(cm));
+            }
+        }
+        // Iteration j: the weights of pair j (P) go through PV while pair
+        // j + 1's scores run on the MFMA pipe -- the exponentials of one pair
+        // issue between the score MFMAs of the next, the next pair's maxima
+        // between this pair's PV MFMAs.  A rescale, when a maximum grew, is
+        // applied after PV and before the next pair's weights.  IN: pairs j
+        // and j + 1 are open and pair j + 3 exists (no masks, no tests).
+        auto iter = [&]<bool IN>(int j) {
+            const bool nxt = IN || j + 1 < npair;
+            if (nxt) {
+                // this wave's part of pair j + 1 is in once only pair j + 2's
+                // loads may fly; the barrier brings the other wave's part and
+                // says both have left pair j - 1, whose stage takes pair j + 3
+                if (IN || j + 2 < npair) wait_vmcnt<LPW>();
+                else wait_vmcnt<0>();
+                wg_barrier();
+            }
+            u32x4 va[DT];
+            if (IN || 2 * (j + 1) * BS <= vlim) read_v.template operator()<false>(j, va);
+            else read_v.template operator()<true>(j, va);
+            bf16x8 kop[2][KK];
+            if (nxt) read_k(j + 1, kop);
+            if (IN || j + kStages - 1 < npair) issue(j + kStages - 1);
+
+            f32x4 sacc[2][T];  // pair j + 1's scores
+            bf16x8 pb[T];      // pair j's weights
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                if (nxt)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        sacc[h][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int kk = 0; kk < KK; ++kk)
+                            sacc[h][t] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[h][kk], qf[t][kk], sacc[h][t], 0, 0, 0);
+                    }
+                float pr[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pr[i] = exp2_fast(fmaf(sc[t][i], sl2, -m[t]));
+                pb[t] = __builtin_bit_cast(bf16x8, u32x4{bf16x2_rne(pr[0], pr[1]), bf16x2_rne(pr[2], pr[3]),
+                                                         bf16x2_rne(pr[4], pr[5]), bf16x2_rne(pr[6], pr[7])});
+            }
             float mx[T];
             bool grow = false;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
+                lsum[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[t], lsum[t], 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    sc[t][i] = !MASK || key0a + i < lim[t] ? sacc[0][t][i] : -INFINITY;
-                    sc[t][4 + i] = !MASK || key0b + i < lim[t] ? sacc[1][t][i] : -INFINITY;
+                for (int dt = 0; dt < DT; ++dt)
+                    o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, va[dt]), pb[t], o[dt][t],
+                                                                       0, 0, 0);
+            }
+            if (nxt) {
+                if constexpr (IN) {
+#pragma unroll
+                    for (int t = 0; t < T; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            sc[t][i] = sacc[0][t][i];
+                            sc[t][4 + i] = sacc[1][t][i];
+                        }
+                } else {
+                    mask_scores(j + 1, sacc, sc);
                 }
-                mx[t] = fmaxf(fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])),
-                              fmaxf(fmaxf(sc[t][4], sc[t][5]), fmaxf(sc[t][6], sc[t][7]))) * sl2;
-                grow |= mx[t] > m[t] + kRescaleSlack;
-            }
-            // a single wave per SIMD issues in order: spread the VALU work
-            // (V transposes, maxima) between the score MFMAs so both pipes run
 #pragma unroll
-            for (int i = 0; i < 2 * KK * T; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                for (int t = 0; t < T; ++t) {
+                    mx[t] = lane_max(sc[t]) * sl2;
+                    grow |= mx[t] > m[t] + kRescaleSlack;
+                }
             }
-            // one branch for the whole pair (it is rare past the first pages),
-            // so the tiles' exponentials and MFMAs below schedule as one block
+            // lazy rescale (rare past the first pairs): O and the sums follow
+            // the new maxima before pair j + 1's weights are formed
             if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
                 for (int t = 0; t < T; ++t) {
                     float cm = fmaxf(mx[t], xor16(mx[t]));
                     cm = fmaxf(cm, xor32(cm));
                     const float m_new = fmaxf(m[t], cm);
-                    const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[t] - m_new);
+                    const float alpha = exp2_fast(m[t] - m_new);
                     lsum[t] *= alpha;
 #pragma unroll
                     for (int dt = 0; dt < DT; ++dt) o[dt][t] *= alpha;
                     m[t] = m_new;
                 }
             }
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                float pr[8];  // m is finite (key 0 is visible to every row)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) pr[i] = exp2_fast(fmaf(sc[t][i], sl2, -m[t]));
-                const bf16x8 pb = __builtin_bit_cast(
-                    bf16x8, u32x4{bf16x2_rne(pr[0], pr[1]), bf16x2_rne(pr[2], pr[3]), bf16x2_rne(pr[4], pr[5]),
-                                  bf16x2_rne(pr[6], pr[7])});
-                lsum[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb, lsum[t], 0, 0, 0);
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
-                    o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, va[dt]), pb, o[dt][t],
-                                                                       0, 0, 0);
-            }
-            // the next tile's exponentials run under this tile's PV MFMAs
-            __builtin_amdgcn_sched_group_barrier(0x002, 20, 1);
-#pragma unroll
-            for (int t = 0; t + 1 < T; ++t)
-#pragma unroll
-                for (int i = 0; i < DT + 1; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-                    if (i < 2) __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);
-                    else __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);
-                }
-            __builtin_amdgcn_sched_group_barrier(0x008, DT + 1, 1);
         };
-        if (npair > 0) issue(0);
-        if (threadIdx.x == 0) next = claim();  // overlaps the first pairs' round trip
-        for (int i = 1; i < min(npair, kStages - 1); ++i) issue(i);
-        // pairs every row sees whole: both pages below the item's first row's
-        // limit (rows are token-major, limits grow with the row)
-        const int open = min(p.causal ? st + qt * p.tq + 1 : st + len, eff) / BS;
-        const int full = npair - (kStages - 1);  // pairs pj < full refill without a test
-        int pj = 0;
-        for (; pj < min(open / 2, full); ++pj) pair.template operator()<false, true>(pj);
-        for (; pj < min(open / 2, npair); ++pj) pair.template operator()<false, false>(pj);
-        for (; pj < npair; ++pj) pair.template operator()<true, false>(pj);
+        const int in_end = min(open - 1, npair - (kStages - 1));  // iterations j < in_end are IN
+        int j = 0;
+        for (; j < in_end; ++j) iter.template operator()<true>(j);
+        for (; j < npair; ++j) iter.template operator()<false>(j);
 
         // rows of this lane: item row 64 w + 16 t + col, dims 16 dt + 4 grp + i
         // (bf16 pools, transposed V reads) or DT (4 grp + i) + dt (fp8 pools)
