@@ -472,8 +472,9 @@ def bench_prefill(args, torch, ops, lib):
     flops = 4 * D * H * keys
     tflops = flops / (ms * 1e-3) / 1e12
     k_tflops = flops / (k_ms * 1e-3) / 1e12
-    # K/V bytes the kernel streams: every (tile, kv-head) reads its pages once
-    tq = 64 // (H // Hkv)
+    # K/V bytes the kernel streams into LDS: every item (128 query rows, the
+    # two waves of a workgroup sharing each page) reads its pages once
+    tq = 128 // (H // Hkv)
     kv_bytes = sum(((int(s) + min(C, (t + 1) * tq) + BS - 1) // BS) * BS * 2 * D * 2 * Hkv
                    for s in starts for t in range((C + tq - 1) // tq))
     res = {"ms_per_step": ms, "tflops": tflops, "frac_of_peak": tflops / PEAK_BF16_TFLOPS,

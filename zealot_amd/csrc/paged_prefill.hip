@@ -19,14 +19,16 @@
 //       sort on their last tile's pages) and a group's tiles back to back,
 //       longest first.
 //   prefill_mfma_kernel<KV, D, G>  bf16 / fp8 pools, D in {64, 128}, G in
-//       {1, 2, 4, 8}, block_size 16: persistent one-wave workgroups take items
+//       {1, 2, 4, 8}, block_size 16: persistent two-wave workgroups take items
 //       from their XCD's queue (workgroups are dispatched round-robin over the
-//       8 XCDs), then from the others' when it runs dry.  An item holds 64 query rows -- TQ = 64/G chunk
-//       tokens x the G heads of one kv-head, token-major -- as four 16-column
-//       MFMA tiles, so each K/V page read serves all 64 rows.  Pages stream
-//       through LDS as in the decode (global_load_lds, two stages); QK^T and PV
-//       run on MFMA with a lazily rescaled softmax (see paged_decode.hip);
-//       every column carries its own visibility limit.
+//       8 XCDs), then from the others' when it runs dry.  An item holds 128
+//       query rows -- TQ = 128/G chunk tokens x the G heads of one kv-head,
+//       token-major -- and each wave computes 64 of them as four 16-column
+//       MFMA tiles, so each K/V page read into LDS serves all 128 rows.  Pages
+//       stream through LDS in pairs (global_load_lds, a ring of four stages,
+//       each wave loading one page of every pair); QK^T and PV run on MFMA with
+//       a lazily rescaled softmax (see paged_decode.hip), software-pipelined
+//       one pair deep; every column carries its own visibility limit.
 // Rows write their outputs directly (no split over keys): an item reads the
 // pages up to its last row's limit, so the causal triangle costs half.
 #include <hip/hip_runtime.h>
