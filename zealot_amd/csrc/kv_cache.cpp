@@ -143,6 +143,9 @@ struct zk_kv_cache {
     DevBuf d_tblupd;   // block-table updates (offset, value)
     CachedBuf d_tbl;   // decode batch block tables [n][stride]
     CachedBuf d_batch; // decode batch lengths + scales
+    // what the last decode plan was made from (shapes, lengths, prefix
+    // groups, tables and workspace); a call with the same bytes reuses it
+    std::vector<char> plan_sig;
     CachedBuf d_pre;   // prefill batch tables, row offsets, lengths, starts, scales
     DevBuf d_pws;      // prefill workspace
     DevBuf d_ws;     // decode workspace
@@ -1099,11 +1102,26 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
     c->last_sg = nsg;
     c->last_sg_pages = sp.total_pages;
     const int32_t *drows = q_rows ? (const int32_t *)(d + len_bytes + sc_bytes + share_bytes) : nullptr;
-    return zk::paged_decode(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
-                            (const int32_t *)c->d_tbl.dev.p, (const int32_t *)d, n, num_heads, (int)H,
-                            (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
-                            mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr, drows,
-                            q_stride, /*trusted_tables=*/true);  // built from the sequences' handles
+    // The plan (work items over sequence indices and page ranges, in the
+    // workspace) depends on the shapes, the lengths and the prefix groups,
+    // not on the tables' contents, the layer's pools, q or scales: the
+    // layers of one step share it.
+    const uintptr_t hdr[] = {(uintptr_t)n,      (uintptr_t)num_heads,     stride,
+                             (uintptr_t)nsg,    (uintptr_t)sp.total_pages, (uintptr_t)c->d_ws.p,
+                             (uintptr_t)c->d_ws.cap};
+    std::vector<char> sig((const char *)hdr, (const char *)hdr + sizeof(hdr));
+    sig.insert(sig.end(), host.data(), host.data() + len_bytes);
+    sig.insert(sig.end(), host.data() + len_bytes + sc_bytes, host.data() + len_bytes + sc_bytes + share_bytes);
+    const bool reuse = sig == c->plan_sig;
+    c->plan_sig.clear();
+    int rc = zk::paged_decode(q, q_dtype, c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, out,
+                              (const int32_t *)c->d_tbl.dev.p, (const int32_t *)d, n, num_heads, (int)H,
+                              (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
+                              mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr, drows,
+                              q_stride, /*trusted_tables=*/true,  // built from the sequences' handles
+                              reuse);
+    if (rc == ZK_OK) c->plan_sig = std::move(sig);
+    return rc;
 }
 
 // Looks up ids[0..n) (each must be registered; fp8 caches need scales).

@@ -275,6 +275,7 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
     if (t == 0) {
         p.work[0] = total_pairs * p.num_kv_heads;  // total items
         p.work[1] = p.num_waves;                   // queue head: items below are taken statically
+        p.work[2] = 0;                             // waves done (the last one resets the head)
     }
 }
 
@@ -662,6 +663,13 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         }
         item = __builtin_amdgcn_readfirstlane(next);
     }
+    // The last wave to finish puts the queue back as the plan left it, so a
+    // launch with the same plan (the next layer of a step) can skip planning.
+    // Every wave's claims returned before it counts itself done.
+    if (lane == 0 && atomicAdd(&p.work[2], 1) == p.num_waves - 1) {
+        __hip_atomic_store(&p.work[1], p.num_waves, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&p.work[2], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ------------------------------------------------------------ generic kernel
@@ -1028,7 +1036,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                      int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                      float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                      void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
-                     const int32_t *q_rows, int64_t q_stride, bool trusted_tables) {
+                     const int32_t *q_rows, int64_t q_stride, bool trusted_tables, bool reuse_plan) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: q dtype must be f32 or bf16");
     if (!valid_dtype(kv_dtype))
@@ -1110,7 +1118,8 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.q_f32 = q_dtype == ZK_F32 ? 1 : 0;
 
     hipStream_t s = (hipStream_t)stream;
-    if (!(use_mfma && trusted_tables)) {  // trusted MFMA launches: the plan sets the lengths
+    reuse_plan = reuse_plan && use_mfma;
+    if (!(use_mfma && (trusted_tables || reuse_plan))) {  // trusted MFMA launches: the plan sets the lengths
         {
             KernelTimer timer("decode_seq_info", s);
             seq_info_kernel<<<num_seqs, kWave, 0, s>>>(p);
@@ -1118,11 +1127,13 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
         if (int rc = check_launch("zk_paged_decode seq_info")) return rc;
     }
     if (use_mfma) {
-        {
-            KernelTimer timer("decode_plan", s);
-            plan_kernel<<<1, 1024, 0, s>>>(p, num_seqs);
+        if (!reuse_plan) {
+            {
+                KernelTimer timer("decode_plan", s);
+                plan_kernel<<<1, 1024, 0, s>>>(p, num_seqs);
+            }
+            if (int rc = check_launch("zk_paged_decode plan")) return rc;
         }
-        if (int rc = check_launch("zk_paged_decode plan")) return rc;
         KernelTimer timer("decode_partials", s);
         const int grid = p.num_waves;
         if (kv_dtype == ZK_BF16) launch_mfma<ZK_BF16>(p, grid, s, G);

@@ -72,13 +72,15 @@ struct PrefixGroups {
 // q row stride in elements (0 = H * D; out rows stay H * D apart) and, for
 // callers that built the tables themselves (every entry below a length is a
 // valid block id), trusted_tables: the page walk that finds the first
-// invalid entry is skipped.
+// invalid entry is skipped.  reuse_plan: the previous call on this workspace
+// and stream had the same lengths, tables, prefix groups and shapes (another
+// layer of the same step), so its work items stand and planning is skipped.
 int paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
                  void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                  float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                  void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
-                 const int32_t *q_rows, int64_t q_stride = 0, bool trusted_tables = false);
+                 const int32_t *q_rows, int64_t q_stride = 0, bool trusted_tables = false, bool reuse_plan = false);
 // zk_paged_prefill with the chunk rows of sequence n given as a device
 // offset and length (q_off[n], q_len[n]) instead of cu_seqlens_q; total_q is
 // an upper bound of the rows; q rows are q_stride elements apart (0 = H * D).
