@@ -9,23 +9,36 @@
 // dimension k.  Inputs f32 or bf16 (both operands alike), output f32 or bf16,
 // f32 accumulation.  A plan (descriptors + an algorithm) is cached per
 // (device, m, n, k, dtypes); one workspace per device.  On first use of a
-// shape the heuristic's first 16 candidates are timed on the caller's
-// operands and the fastest kept (zk_linear_tuning(0) keeps the heuristic's
-// first instead, e.g. under graph capture, where nothing may synchronize).
+// shape the heuristic's 16 first candidates are timed on the caller's
+// operands and the fastest kept.  Skinny products over large weights (m <=
+// 256, n k >= 4M: a decode step's projections, HBM-bound on the weights) get
+// a deeper search: every algorithm hipBLASLt has for the problem (sampled
+// down when the product is long) is timed with the weights warm in the
+// caches, and the 12 fastest again with the caches flushed before each run,
+// as the weights of a model's layers are when they stream from HBM; the
+// fastest cold one is kept.  zk_linear_tuning(0) keeps the heuristic's first
+// instead (e.g. under graph capture, where nothing may synchronize).
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
 #include <tuple>
+#include <utility>
+#include <vector>
 
 #include "zk_common.h"
 
 namespace {
 
 constexpr size_t kWorkspace = 64ull << 20;
-constexpr int kCandidates = 16;
+constexpr int kCandidates = 16;           // heuristic candidates
+constexpr int kFinalists = 12;            // re-timed with cold caches
+constexpr size_t kFlushBytes = 512ull << 20;  // > the 256 MiB MALL
+constexpr double kWarmBudgetMs = 400.0;   // warm timing budget per shape
 
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
@@ -67,36 +80,88 @@ int device_state(DeviceState **out) {
     return ZK_OK;
 }
 
-// Times each candidate (a warm-up call, then kReps calls between events) on
-// the stream and returns the fastest that ran.  Runs once per shape; the
-// output y is overwritten by every candidate and finally by the real call.
-int pick_fastest(DeviceState &d, Plan &p, const hipblasLtMatmulHeuristicResult_t *heur, int found, const void *x,
-                 const void *w, void *y, hipStream_t stream, int *best) {
-    constexpr int kReps = 5;
+// Reads a buffer larger than the last-level cache with ordinary (allocating)
+// loads, so the next GEMM finds its weights in HBM only.
+__global__ void __launch_bounds__(256) flush_kernel(const uint4 *__restrict__ p, size_t n16, uint32_t *sink) {
+    uint4 acc = {0u, 0u, 0u, 0u};
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) {
+        const uint4 v = p[i];
+        acc.x ^= v.x;
+        acc.y ^= v.y;
+        acc.z ^= v.z;
+        acc.w ^= v.w;
+    }
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u) sink[0] = 1u;
+}
+
+struct Cand {
+    hipblasLtMatmulAlgo_t algo;
+    size_t ws;
+};
+
+// Picks the candidate to keep (see the file comment).  The output y is
+// overwritten by every timed run and finally by the real call.
+int pick_fastest(DeviceState &d, Plan &p, const std::vector<Cand> &cands, const void *x, const void *w, void *y,
+                 hipStream_t stream, bool cold, int *best) {
     hipEvent_t e0, e1;
     ZK_HIP_CHECK(hipEventCreate(&e0), "zk_linear tuning");
     ZK_HIP_CHECK(hipEventCreate(&e1), "zk_linear tuning");
     const float alpha = 1.0f, beta = 0.0f;
-    float best_ms = 1e30f;
-    for (int i = 0; i < found; ++i) {
-        if (heur[i].state != HIPBLAS_STATUS_SUCCESS || heur[i].workspaceSize > kWorkspace) continue;
-        auto run = [&]() {
-            return hipblasLtMatmul(d.handle, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.c, y, p.c, &heur[i].algo,
-                                   d.workspace, heur[i].workspaceSize, stream);
-        };
-        if (run() != HIPBLAS_STATUS_SUCCESS) continue;
+    auto run = [&](const Cand &c) {
+        return hipblasLtMatmul(d.handle, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.c, y, p.c, &c.algo, d.workspace,
+                               c.ws, stream) == HIPBLAS_STATUS_SUCCESS;
+    };
+    auto timed = [&](const Cand &c, int reps, float *ms) {
         (void)hipEventRecord(e0, stream);
         bool ok = true;
-        for (int r = 0; r < kReps && ok; ++r) ok = run() == HIPBLAS_STATUS_SUCCESS;
+        for (int r = 0; r < reps && ok; ++r) ok = run(c);
         (void)hipEventRecord(e1, stream);
-        if (hipEventSynchronize(e1) != hipSuccess || !ok) continue;
+        if (hipEventSynchronize(e1) != hipSuccess || !ok) return false;
+        return hipEventElapsedTime(ms, e0, e1) == hipSuccess;
+    };
+    // warm: the heuristic's candidates first; the rest sampled evenly when
+    // all of them would take longer than the budget
+    std::vector<std::pair<float, int>> warm;
+    size_t stride = 1;
+    for (size_t i = 0; i < cands.size(); i += (i < (size_t)kCandidates ? 1 : stride)) {
         float ms = 0.0f;
-        (void)hipEventElapsedTime(&ms, e0, e1);
-        if (ms < best_ms) {
-            best_ms = ms;
-            *best = i;
+        if (!run(cands[i]) || !timed(cands[i], 2, &ms)) continue;
+        warm.push_back({ms / 2, (int)i});
+        if (warm.size() == 1) {
+            const double runs = kWarmBudgetMs / std::max(1e-3, 3.0 * ms / 2);
+            stride = std::max<size_t>(1, (size_t)((double)cands.size() / std::max(1.0, runs)));
         }
     }
+    if (warm.empty()) {
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        return zk::set_error(ZK_ERR_HIP, "Internal error: zk_linear: no hipBLASLt algorithm ran");
+    }
+    std::sort(warm.begin(), warm.end());
+    *best = warm[0].second;
+    // cold: flush the caches before each run of the finalists
+    void *flush = nullptr;
+    if (cold && warm.size() > 1 && hipMalloc(&flush, kFlushBytes) == hipSuccess) {
+        float best_ms = 1e30f;
+        for (size_t f = 0; f < std::min<size_t>(kFinalists, warm.size()); ++f) {
+            float total = 0.0f;
+            bool ok = true;
+            for (int r = 0; r < 3 && ok; ++r) {
+                flush_kernel<<<1024, 256, 0, stream>>>((const uint4 *)flush, kFlushBytes / 16,
+                                                       (uint32_t *)((char *)flush + kFlushBytes - 16));
+                float ms = 0.0f;
+                ok = timed(cands[warm[f].second], 1, &ms);
+                total += ms;
+            }
+            if (ok && total < best_ms) {
+                best_ms = total;
+                *best = warm[f].second;
+            }
+        }
+        (void)hipStreamSynchronize(stream);
+        (void)hipFree(flush);
+    }
+    (void)hipGetLastError();
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     return ZK_OK;
@@ -131,14 +196,34 @@ int make_plan(DeviceState &d, int64_t m, int64_t n, int64_t k, zk_dtype in, zk_d
     hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS || found == 0)
         return fail("no hipBLASLt algorithm for this shape", st == HIPBLAS_STATUS_SUCCESS ? HIPBLAS_STATUS_NOT_SUPPORTED : st);
+    std::vector<Cand> cands;
+    for (int i = 0; i < found; ++i)
+        if (heur[i].state == HIPBLAS_STATUS_SUCCESS && heur[i].workspaceSize <= kWorkspace)
+            cands.push_back({heur[i].algo, heur[i].workspaceSize});
+    if (cands.empty()) return fail("no hipBLASLt algorithm fits the workspace", HIPBLAS_STATUS_NOT_SUPPORTED);
     int best = 0;
-    if (found > 1 && tune) {
+    const bool deep = m <= 256 && n * k >= (int64_t)1 << 22;
+    if (tune && deep) {
         // the heuristic's order is not the fastest for the skinny (decode)
-        // shapes: time every candidate on the caller's operands once
-        if (int rc = pick_fastest(d, p, heur, found, x, w, y, stream, &best)) return rc;
+        // shapes: every algorithm the library has for the problem is a candidate
+        std::vector<hipblasLtMatmulHeuristicResult_t> all;
+        if (hipblaslt_ext::getAllAlgos(d.handle, hipblaslt_ext::GemmType::HIPBLASLT_GEMM, ta, tb, hip_type(in),
+                                       hip_type(in), hip_type(out), hip_type(out), HIPBLAS_COMPUTE_32F,
+                                       all) == HIPBLAS_STATUS_SUCCESS) {
+            const float alpha = 1.0f, beta = 0.0f;
+            for (auto &r : all) {
+                size_t wsz = 0;
+                if (hipblaslt_ext::matmulIsAlgoSupported(d.handle, p.desc, &alpha, p.a, p.b, &beta, p.c, p.c, r.algo,
+                                                         wsz) == HIPBLAS_STATUS_SUCCESS &&
+                    wsz <= kWorkspace)
+                    cands.push_back({r.algo, wsz});
+            }
+        }
     }
-    p.algo = heur[best].algo;
-    p.ws = heur[best].workspaceSize;
+    if (tune && cands.size() > 1)
+        if (int rc = pick_fastest(d, p, cands, x, w, y, stream, deep, &best)) return rc;
+    p.algo = cands[best].algo;
+    p.ws = cands[best].ws;
     *res = &(d.plans[key] = p);
     return ZK_OK;
 }
