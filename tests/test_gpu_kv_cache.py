@@ -325,3 +325,49 @@ def test_forked_prefix_decode_shares_pages(G, D, qdt, mapping):
     for sid in ids:
         cache.release_seq(sid)
     assert bm.free_blocks == NB
+
+
+def test_decode_plan_reuse_across_layers_and_batches():
+    """The cache plans a decode once and reuses the plan while the shapes,
+    lengths and prefix groups stay the same (the layers of a step): the work
+    items name sequence indices and page ranges, not blocks, so another batch
+    with the same lengths may reuse it too; a length that changes in one
+    layer makes a new plan.  Every call is checked against the oracle."""
+    import zealot_amd as ze
+    from zealot_amd import KVCache
+    rng = np.random.default_rng(77)
+    L, H, Hkv, D, BS, NB = 3, 8, 2, 128, 16, 160
+    lens = {"a": 300, "b": 40, "c": 300, "d": 40}
+    bm = ze.BlockManager(NB, BS)
+    cache = KVCache(NB, BS, L, Hkv, D, dtype=torch.bfloat16, max_seqs=8, max_blocks_per_seq=24)
+    for sid, T in lens.items():
+        cache.register_seq(sid, 24)
+        for _ in range((T + 1 + BS - 1) // BS):
+            cache.alloc_block(sid, bm)
+        for layer in range(L):
+            cache.store_kv(layer, sid, to_dev(normal(rng, (T, Hkv, D), oracle.BF16)),
+                           to_dev(normal(rng, (T, Hkv, D), oracle.BF16)), 0, T)
+    scale = np.float32(1 / math.sqrt(D))
+
+    def check(layer, ids, seq_lens):
+        q = normal(rng, (len(ids), H, D), oracle.BF16)
+        out = to_host(cache.paged_decode(layer, ids, to_dev(q)))
+        kp, vp = to_host(cache.k_pool(layer)), to_host(cache.v_pool(layer))
+        bt = -np.ones((len(ids), 24), np.int32)
+        for i, sid in enumerate(ids):
+            b = cache.seq_state(sid).block_ids
+            bt[i, :len(b)] = b
+        exp = oracle.paged_decode(as_f32(q, oracle.BF16), kp, vp, oracle.BF16, bt, seq_lens, Hkv, D, BS, scale)
+        assert max_abs_err(as_f32(out, oracle.BF16), exp) <= 2e-2, (layer, ids)
+
+    announce("decode plan reuse")
+    check(0, ["a", "b"], [300, 40])
+    check(1, ["a", "b"], [300, 40])  # the next layer: same plan
+    check(1, ["c", "d"], [300, 40])  # other sequences, same lengths: same plan, other tables
+    # one more token in layer 2 only: a new plan there, and again for layer 0
+    cache.store_kv(2, "a", to_dev(normal(rng, (1, Hkv, D), oracle.BF16)),
+                   to_dev(normal(rng, (1, Hkv, D), oracle.BF16)), 300, 1)
+    check(2, ["a", "b"], [301, 40])
+    check(0, ["a", "b"], [300, 40])
+    check(2, ["b", "a"], [40, 301])  # order matters: sequence indices change
+    torch.cuda.synchronize()
