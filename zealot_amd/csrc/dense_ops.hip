@@ -96,12 +96,16 @@ rms_norm_kernel(const T *__restrict__ x, const T *residual, const T *__restrict_
     const int64_t r_in = rows ? rows[blockIdx.x] : (int64_t)blockIdx.x;
     const T *xr = x + (size_t)r_in * dim;
     const T *rr = residual ? residual + (size_t)r_in * dim : nullptr;
-    float v[MAXV][VEC];
+    float v[MAXV][VEC], wv[MAXV][VEC];
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
         const int i = (j * kThreads + (int)threadIdx.x) * VEC;
         if (i < dim) {
+            // the weights load with the row (not after the reduction): one
+            // memory round trip per launch instead of two
+            if (VEC > 1) load_vec(w + i, wv[j]);
+            else wv[j][0] = load1(w + i);
             if (VEC > 1) {
                 load_vec(xr + i, v[j]);
                 if (rr) {
@@ -128,11 +132,9 @@ rms_norm_kernel(const T *__restrict__ x, const T *residual, const T *__restrict_
     for (int j = 0; j < MAXV; ++j) {
         const int i = (j * kThreads + (int)threadIdx.x) * VEC;
         if (i < dim) {
-            float wv[VEC], o[VEC];
-            if (VEC > 1) load_vec(w + i, wv);
-            else wv[0] = load1(w + i);
+            float o[VEC];
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) o[e] = v[j][e] * inv * wv[e];
+            for (int e = 0; e < VEC; ++e) o[e] = v[j][e] * inv * wv[j][e];
             if (VEC > 1) store_vec(orow + i, o);
             else store1(orow + i, o[0]);
         }
