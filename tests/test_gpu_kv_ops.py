@@ -105,6 +105,23 @@ def test_append_skips_negative_slots_and_converts_dtypes():
     assert np.array_equal(gk, rk) and np.array_equal(gv, rv)
 
 
+@pytest.mark.parametrize("H,D,BS", [(8, 128, 16), (6, 96, 16), (8, 64, 32), (4, 128, 8), (3, 64, 16)])
+def test_append_copy_shapes_bitexact(H, D, BS):
+    """Same-dtype appends: power-of-two heads, rows and blocks take the
+    shift-and-mask kernel, the others the general one; both bit-exact,
+    slots of -1 skipped."""
+    rng = np.random.default_rng(H * 1000 + D + BS)
+    NB, T = 40, 250
+    slots = rng.permutation(NB * BS)[:T].astype(np.int64)
+    slots[::9] = -1
+    k = normal(rng, (T, H, D), oracle.BF16)
+    v = normal(rng, (T, H, D), oracle.BF16)
+    kp0 = np.full((NB, H, BS, D), CANARY16, np.uint16)
+    announce(f"append copy H={H} D={D} BS={BS}")
+    gk, gv, rk, rv = _append_both(kp0, kp0.copy(), k, v, slots, oracle.BF16, oracle.BF16, H, D, BS, NB)
+    assert np.array_equal(gk, rk) and np.array_equal(gv, rv)
+
+
 def test_fp8_append_bitexact_including_saturation_and_nan():
     from zealot_amd import ops
     rng = np.random.default_rng(33)

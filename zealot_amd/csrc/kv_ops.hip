@@ -64,6 +64,32 @@ append_copy_kernel(const char *__restrict__ k, const char *__restrict__ v, char 
             data);
 }
 
+// The same copy when the chunks per row, the kv-heads, the row bytes and the
+// block size are all powers of two (16-token blocks, 2^k heads, 256-byte bf16
+// rows: the usual paged layout): shifts and masks instead of the divisions,
+// which left the copy VALU-bound.
+__global__ void __launch_bounds__(kThreads)
+append_copy_pow2_kernel(const char *__restrict__ k, const char *__restrict__ v, char *__restrict__ k_pool,
+                        char *__restrict__ v_pool, const int64_t *__restrict__ slots, uint32_t total, uint32_t cpr_log2,
+                        uint32_t hkv_log2, uint32_t row_log2, uint32_t bs_log2, int64_t num_slots,
+                        uint64_t src_token_bytes) {
+    const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= total) return;
+    const uint32_t c = idx & ((1u << cpr_log2) - 1u);
+    uint32_t r = idx >> cpr_log2;
+    const uint32_t h = r & ((1u << hkv_log2) - 1u);
+    r >>= hkv_log2;
+    const uint32_t kv = r & 1u;
+    const uint32_t t = r >> 1;
+    const int64_t slot = slots[t];
+    const size_t src_off = (size_t)t * src_token_bytes + ((size_t)h << row_log2) + (size_t)c * 16;
+    const uint4 data = ld16_nt((kv ? v : k) + src_off);
+    if (slot < 0 || slot >= num_slots) return;
+    const uint64_t blk = (uint64_t)slot >> bs_log2, tib = (uint64_t)slot & ((1u << bs_log2) - 1u);
+    const uint64_t row = (((blk << hkv_log2) + h) << bs_log2) + tib;
+    st16_nt((kv ? v_pool : k_pool) + (row << row_log2) + (size_t)c * 16, data);
+}
+
 // Quantising append into an fp8 pool: one 16-element chunk per index; the
 // source chunk is 32 B (bf16) or 64 B (f32), the destination chunk 16 B.
 template <int SRC>  // ZK_BF16 or ZK_F32
@@ -419,11 +445,18 @@ int zk::append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, 
         uint32_t cpr = row_bytes / 16;
         uint32_t total = (uint32_t)(total_rows * cpr);
         uint32_t grid = (total + kThreads - 1) / kThreads;
+        auto pow2 = [](uint64_t x) { return x > 0 && (x & (x - 1)) == 0; };
+        auto log2u = [](uint64_t x) { return (uint32_t)__builtin_ctzll(x); };
         KernelTimer timer("append", s);
-        append_copy_kernel<<<grid, kThreads, 0, s>>>((const char *)k, (const char *)v, (char *)k_pool,
-                                                     (char *)v_pool, slot_mapping, total, cpr,
-                                                     num_kv_heads, row_bytes, block_size, num_slots,
-                                                     src_token_bytes);
+        if (pow2(cpr) && pow2((uint64_t)num_kv_heads) && pow2(block_size))
+            append_copy_pow2_kernel<<<grid, kThreads, 0, s>>>(
+                (const char *)k, (const char *)v, (char *)k_pool, (char *)v_pool, slot_mapping, total, log2u(cpr),
+                log2u((uint64_t)num_kv_heads), log2u(row_bytes), log2u((uint64_t)block_size), num_slots,
+                src_token_bytes);
+        else
+            append_copy_kernel<<<grid, kThreads, 0, s>>>((const char *)k, (const char *)v, (char *)k_pool,
+                                                         (char *)v_pool, slot_mapping, total, cpr, num_kv_heads,
+                                                         row_bytes, block_size, num_slots, src_token_bytes);
         return check_launch("zk_append");
     }
     if (aligned && fp8 && (head_dim % 16) == 0 && total_rows * (head_dim / 16) < (1ull << 31)) {
