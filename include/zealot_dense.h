@@ -50,6 +50,17 @@ int zk_embedding(const int64_t *ids, const void *table, void *out, int64_t num_t
  * out BF16 or F32 (e.g. f32 logits). */
 int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype in_dtype,
               zk_dtype out_dtype, void *stream);
+/* No counterpart in the reference: the weight-streaming kernel zk_linear's
+ * tuning may pick for bf16 products with m <= 64, called directly (for
+ * tests, and callers that want it without tuning).  x, w bf16, y f32 or bf16,
+ * all 16-byte aligned.  Workgroups own tile_rows (64 or 128) weight rows and
+ * k / splits of k: needs n % tile_rows == 0, k % (128 * splits) == 0,
+ * splits <= 64 and splits * m * n * 4 <= 32 MiB.  With splits > 1 the
+ * ranges' sums are added in range order by a second kernel (the result does
+ * not depend on scheduling); calls on one device share that workspace, so
+ * they must not overlap in time (one stream, or synchronized streams). */
+int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype out_dtype,
+                     int tile_rows, int splits, void *stream);
 /* On (default): the first call of each (m, n, k, dtypes) times hipBLASLt's
  * candidate algorithms on its operands (synchronizing the stream once) and
  * keeps the fastest.  Off: the heuristic's first choice, no synchronization

@@ -136,3 +136,45 @@ def test_linear_bf16(m, n, k, out_f32):
     ref = xs.astype(np.float64) @ ws[cols].astype(np.float64).T
     assert np.abs(got[:, cols] - ref).max() <= 1e-2 * np.abs(ref).max()
 
+
+
+@pytest.mark.parametrize("m,n,k,rows,splits,out_f32", [(1, 64, 1024, 64, 1, False), (16, 4096, 4096, 128, 1, False),
+                                                       (37, 6144, 4096, 64, 2, False), (64, 4096, 14336, 128, 7, False),
+                                                       (64, 4096, 4096, 64, 4, True), (50, 1024, 2048, 128, 2, True),
+                                                       (17, 192, 4096, 64, 8, False), (33, 256, 512, 128, 1, True)])
+def test_linear_skinny_kernel(m, n, k, rows, splits, out_f32):
+    """The weight-streaming kernel at each m-tile count and split of k, against
+    the float64 product of the same bf16 operands; splits > 1 add the ranges
+    in a fixed order, so two calls agree bit for bit."""
+    from zealot_amd import dense
+    rng = np.random.default_rng(m * 7 + splits + rows)
+    x = normal(rng, (m, k), oracle.BF16)
+    w = oracle.bf16_bits_from_f32((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)).reshape(n, k)
+    announce(f"linear_skinny {m}x{n}x{k} rows={rows} splits={splits}")
+    xd, wd = to_dev(x), to_dev(w)
+    y1 = dense.linear_skinny(xd, wd, splits, rows, out_dtype=torch.float32 if out_f32 else None)
+    y2 = dense.linear_skinny(xd, wd, splits, rows, out_dtype=torch.float32 if out_f32 else None)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16) if not out_f32 else y1, y2.view(torch.int16) if not out_f32 else y2)
+    got = to_host(y1) if out_f32 else as_f32(to_host(y1), oracle.BF16)
+    ref = as_f32(x, oracle.BF16).astype(np.float64) @ as_f32(w, oracle.BF16).astype(np.float64).T
+    tol = (1e-5 if out_f32 else 1e-2) * np.abs(ref).max()
+    assert np.abs(got - ref).max() <= tol
+    if m * n * k <= 4 * 10 ** 6:  # the oracle's scalar product on small shapes
+        ref32 = oracle.linear(as_f32(x, oracle.BF16), as_f32(w, oracle.BF16))
+        assert np.abs(got - ref32).max() <= tol
+
+
+def test_linear_skinny_rejects_unsupported_shapes():
+    from zealot_amd import dense
+    from zealot_amd._lib import ZealotError
+    x = torch.zeros((65, 1024), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((64, 1024), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ZealotError):
+        dense.linear_skinny(x, w)  # m > 64
+    with pytest.raises(ZealotError):
+        dense.linear_skinny(x[:8], w, splits=16, tile_rows=64)  # k % (128 * splits) != 0
+    with pytest.raises(ZealotError):
+        dense.linear_skinny(x[:8], w[:48], tile_rows=64)  # n % tile_rows != 0
+    with pytest.raises(ZealotError):
+        dense.linear_skinny(x[:8], w, tile_rows=128)  # n % tile_rows != 0

@@ -16,8 +16,12 @@
 // down when the product is long) is timed with the weights warm in the
 // caches, and the 12 fastest again with the caches flushed before each run,
 // as the weights of a model's layers are when they stream from HBM; the
-// fastest cold one is kept.  zk_linear_tuning(0) keeps the heuristic's first
-// instead (e.g. under graph capture, where nothing may synchronize).
+// fastest cold one is kept.  For bf16 products with m <= 64 the candidates
+// also hold this library's weight-streaming kernel (skinny_gemm.hip) at each
+// split of k it supports; when it wins, the fastest hipBLASLt algorithm is
+// kept beside it for operands that are not 16-byte aligned.
+// zk_linear_tuning(0) keeps the heuristic's first instead (e.g. under graph
+// capture, where nothing may synchronize).
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
@@ -39,17 +43,23 @@ constexpr int kCandidates = 16;           // heuristic candidates
 constexpr int kFinalists = 12;            // re-timed with cold caches
 constexpr size_t kFlushBytes = 512ull << 20;  // > the 256 MiB MALL
 constexpr double kWarmBudgetMs = 400.0;   // warm timing budget per shape
+constexpr size_t kSkinnyPartial = 32ull << 20;  // split-k sums of the skinny kernel
+const int kSkinnySplits[] = {1, 2, 4, 7, 8, 14, 16, 28};
+const int kSkinnyRows[] = {64, 128};
 
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
+    hipblasLtMatmulAlgo_t algo{};  // hipBLASLt's fastest
     size_t ws = 0;
+    int splits = 0;                // > 0: the skinny kernel with this split of k
+    int tile_rows = 0;             // and tiles of this many weight rows
 };
 
 struct DeviceState {
     hipblasLtHandle_t handle = nullptr;
     void *workspace = nullptr;
+    void *skinny_partial = nullptr;
     std::map<std::tuple<int64_t, int64_t, int64_t, int, int>, Plan> plans;
 };
 
@@ -80,6 +90,30 @@ int device_state(DeviceState **out) {
     return ZK_OK;
 }
 
+int skinny_workspace(DeviceState &d) {
+    if (d.skinny_partial) return ZK_OK;
+    ZK_HIP_CHECK(hipMalloc(&d.skinny_partial, kSkinnyPartial), "zk_linear skinny workspace");
+    return ZK_OK;
+}
+
+// The problem of one zk_linear call.
+struct Problem {
+    const void *x, *w;
+    void *y;
+    int64_t m, n, k;
+    bool f32_out;
+};
+
+int run_skinny(DeviceState &d, const Problem &q, int tile_rows, int splits, hipStream_t stream) {
+    return zk::skinny_linear(q.x, q.w, q.y, q.m, q.n, q.k, q.f32_out, tile_rows, splits, d.skinny_partial,
+                             kSkinnyPartial, stream);
+}
+
+bool skinny_fits(int64_t m, int64_t n, int64_t k, int tile_rows, int splits) {
+    return zk::skinny_linear_ok(m, n, k, tile_rows, splits) &&
+           zk::skinny_linear_partial_bytes(m, n, splits) <= kSkinnyPartial;
+}
+
 // Reads a buffer larger than the last-level cache with ordinary (allocating)
 // loads, so the next GEMM finds its weights in HBM only.
 __global__ void __launch_bounds__(256) flush_kernel(const uint4 *__restrict__ p, size_t n16, uint32_t *sink) {
@@ -97,19 +131,24 @@ __global__ void __launch_bounds__(256) flush_kernel(const uint4 *__restrict__ p,
 struct Cand {
     hipblasLtMatmulAlgo_t algo;
     size_t ws;
+    int splits;     // > 0: the skinny kernel
+    int tile_rows;
 };
 
-// Picks the candidate to keep (see the file comment).  The output y is
-// overwritten by every timed run and finally by the real call.
-int pick_fastest(DeviceState &d, Plan &p, const std::vector<Cand> &cands, const void *x, const void *w, void *y,
-                 hipStream_t stream, bool cold, int *best) {
+// Picks the candidate to keep (see the file comment) and the fastest
+// hipBLASLt one (best_blas, -1 if none ran).  The first n_always candidates
+// are always timed.  The output y is overwritten by every timed run and
+// finally by the real call.
+int pick_fastest(DeviceState &d, Plan &p, const std::vector<Cand> &cands, const Problem &q, size_t n_always,
+                 hipStream_t stream, bool cold, int *best, int *best_blas) {
     hipEvent_t e0, e1;
     ZK_HIP_CHECK(hipEventCreate(&e0), "zk_linear tuning");
     ZK_HIP_CHECK(hipEventCreate(&e1), "zk_linear tuning");
     const float alpha = 1.0f, beta = 0.0f;
     auto run = [&](const Cand &c) {
-        return hipblasLtMatmul(d.handle, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.c, y, p.c, &c.algo, d.workspace,
-                               c.ws, stream) == HIPBLAS_STATUS_SUCCESS;
+        if (c.splits) return run_skinny(d, q, c.tile_rows, c.splits, stream) == ZK_OK;
+        return hipblasLtMatmul(d.handle, p.desc, &alpha, q.w, p.a, q.x, p.b, &beta, q.y, p.c, q.y, p.c, &c.algo,
+                               d.workspace, c.ws, stream) == HIPBLAS_STATUS_SUCCESS;
     };
     auto timed = [&](const Cand &c, int reps, float *ms) {
         (void)hipEventRecord(e0, stream);
@@ -123,7 +162,7 @@ int pick_fastest(DeviceState &d, Plan &p, const std::vector<Cand> &cands, const 
     // all of them would take longer than the budget
     std::vector<std::pair<float, int>> warm;
     size_t stride = 1;
-    for (size_t i = 0; i < cands.size(); i += (i < (size_t)kCandidates ? 1 : stride)) {
+    for (size_t i = 0; i < cands.size(); i += (i < n_always ? 1 : stride)) {
         float ms = 0.0f;
         if (!run(cands[i]) || !timed(cands[i], 2, &ms)) continue;
         warm.push_back({ms / 2, (int)i});
@@ -139,23 +178,43 @@ int pick_fastest(DeviceState &d, Plan &p, const std::vector<Cand> &cands, const 
     }
     std::sort(warm.begin(), warm.end());
     *best = warm[0].second;
+    *best_blas = -1;
+    for (auto &t : warm)
+        if (!cands[t.second].splits) {
+            *best_blas = t.second;
+            break;
+        }
     // cold: flush the caches before each run of the finalists
     void *flush = nullptr;
     if (cold && warm.size() > 1 && hipMalloc(&flush, kFlushBytes) == hipSuccess) {
-        float best_ms = 1e30f;
-        for (size_t f = 0; f < std::min<size_t>(kFinalists, warm.size()); ++f) {
+        // the finalists: the warm fastest, and the skinny kernel's three
+        // fastest configurations (warm, the weights partly sit in the
+        // last-level cache, which flatters other algorithms more)
+        std::vector<std::pair<float, int>> fin(warm.begin(), warm.begin() + std::min<size_t>(kFinalists, warm.size()));
+        int skinny_added = 0;
+        for (size_t i = 0; i < warm.size() && skinny_added < 3; ++i)
+            if (cands[warm[i].second].splits) {
+                ++skinny_added;
+                if (i >= fin.size()) fin.push_back(warm[i]);
+            }
+        float best_ms = 1e30f, blas_ms = 1e30f;
+        for (size_t f = 0; f < fin.size(); ++f) {
             float total = 0.0f;
             bool ok = true;
             for (int r = 0; r < 3 && ok; ++r) {
                 flush_kernel<<<1024, 256, 0, stream>>>((const uint4 *)flush, kFlushBytes / 16,
                                                        (uint32_t *)((char *)flush + kFlushBytes - 16));
                 float ms = 0.0f;
-                ok = timed(cands[warm[f].second], 1, &ms);
+                ok = timed(cands[fin[f].second], 1, &ms);
                 total += ms;
             }
             if (ok && total < best_ms) {
                 best_ms = total;
-                *best = warm[f].second;
+                *best = fin[f].second;
+            }
+            if (ok && !cands[fin[f].second].splits && total < blas_ms) {
+                blas_ms = total;
+                *best_blas = fin[f].second;
             }
         }
         (void)hipStreamSynchronize(stream);
@@ -199,10 +258,17 @@ int make_plan(DeviceState &d, int64_t m, int64_t n, int64_t k, zk_dtype in, zk_d
     std::vector<Cand> cands;
     for (int i = 0; i < found; ++i)
         if (heur[i].state == HIPBLAS_STATUS_SUCCESS && heur[i].workspaceSize <= kWorkspace)
-            cands.push_back({heur[i].algo, heur[i].workspaceSize});
+            cands.push_back({heur[i].algo, heur[i].workspaceSize, 0, 0});
     if (cands.empty()) return fail("no hipBLASLt algorithm fits the workspace", HIPBLAS_STATUS_NOT_SUPPORTED);
-    int best = 0;
+    int best = 0, best_blas = 0;
     const bool deep = m <= 256 && n * k >= (int64_t)1 << 22;
+    const Problem q{x, w, y, m, n, k, out == ZK_F32};
+    const bool aligned = (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0;
+    if (tune && deep && in == ZK_BF16 && aligned && skinny_workspace(d) == ZK_OK)
+        for (int rows : kSkinnyRows)
+            for (int sp : kSkinnySplits)
+                if (skinny_fits(m, n, k, rows, sp)) cands.push_back({hipblasLtMatmulAlgo_t{}, 0, sp, rows});
+    const size_t n_always = cands.size();  // the heuristic's and the skinny kernel's
     if (tune && deep) {
         // the heuristic's order is not the fastest for the skinny (decode)
         // shapes: every algorithm the library has for the problem is a candidate
@@ -216,14 +282,17 @@ int make_plan(DeviceState &d, int64_t m, int64_t n, int64_t k, zk_dtype in, zk_d
                 if (hipblaslt_ext::matmulIsAlgoSupported(d.handle, p.desc, &alpha, p.a, p.b, &beta, p.c, p.c, r.algo,
                                                          wsz) == HIPBLAS_STATUS_SUCCESS &&
                     wsz <= kWorkspace)
-                    cands.push_back({r.algo, wsz});
+                    cands.push_back({r.algo, wsz, 0, 0});
             }
         }
     }
     if (tune && cands.size() > 1)
-        if (int rc = pick_fastest(d, p, cands, x, w, y, stream, deep, &best)) return rc;
-    p.algo = cands[best].algo;
-    p.ws = cands[best].ws;
+        if (int rc = pick_fastest(d, p, cands, q, n_always, stream, deep, &best, &best_blas)) return rc;
+    if (best_blas < 0) best_blas = 0;  // candidate 0 is the heuristic's first
+    p.splits = cands[best].splits;
+    p.tile_rows = cands[best].tile_rows;
+    p.algo = cands[best_blas].algo;
+    p.ws = cands[best_blas].ws;
     *res = &(d.plans[key] = p);
     return ZK_OK;
 }
@@ -249,10 +318,30 @@ int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64
     if (int rc = make_plan(*d, m, n, k, in_dtype, out_dtype, x, w, y, (hipStream_t)stream, g_tune, &p)) return rc;
     const float alpha = 1.0f, beta = 0.0f;
     zk::KernelTimer timer("linear", (hipStream_t)stream);
+    if (p->splits && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0)
+        return run_skinny(*d, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, p->tile_rows, p->splits,
+                          (hipStream_t)stream);
     hipblasStatus_t st = hipblasLtMatmul(d->handle, p->desc, &alpha, w, p->a, x, p->b, &beta, y, p->c, y, p->c,
                                          &p->algo, d->workspace, p->ws, (hipStream_t)stream);
     if (st != HIPBLAS_STATUS_SUCCESS) return fail("hipblasLtMatmul", st);
     return ZK_OK;
+}
+
+int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype out_dtype,
+                     int tile_rows, int splits, void *stream) {
+    if (out_dtype != ZK_F32 && out_dtype != ZK_BF16)
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_skinny: out dtype must be f32 or bf16");
+    if (m == 0 && n > 0 && k > 0) return ZK_OK;
+    if (!skinny_fits(m, n, k, tile_rows, splits))
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT,
+                             "Internal error: zk_linear_skinny: needs 1 <= m <= 64, tile_rows 64 or 128, "
+                             "n % tile_rows == 0, k % (128 * splits) == 0 and splits * m * n * 4 <= 32 MiB");
+    std::lock_guard<std::mutex> g(g_mu);
+    DeviceState *d;
+    if (int rc = device_state(&d)) return rc;
+    if (int rc = skinny_workspace(*d)) return rc;
+    zk::KernelTimer timer("linear", (hipStream_t)stream);
+    return run_skinny(*d, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, tile_rows, splits, (hipStream_t)stream);
 }
 
 int zk_linear_tuning(int on) {

@@ -90,6 +90,16 @@ int paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, cons
                        int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks, float scale,
                        int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                        void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride = 0);
+// Weight-streaming product y[m, n] = x[m, k] . w[n, k]^T for bf16 x / w and
+// m <= 64, output f32 or bf16: workgroups own tiles of tile_rows (64 or 128)
+// weight rows and k / splits of k; needs n % tile_rows == 0 and
+// k % (128 * splits) == 0.  With splits > 1 the ranges' sums go through
+// `partial` (at least skinny_linear_partial_bytes) and are added in range
+// order by a second kernel; calls sharing a workspace must not overlap.
+bool skinny_linear_ok(int64_t m, int64_t n, int64_t k, int tile_rows, int splits);
+size_t skinny_linear_partial_bytes(int64_t m, int64_t n, int splits);
+int skinny_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, bool f32_out, int tile_rows,
+                  int splits, void *partial, size_t partial_bytes, hipStream_t stream);
 size_t paged_decode_workspace(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq, int block_size,
                               bool shared);
 // Whether paged_decode runs shared-prefix items for this shape (otherwise pg

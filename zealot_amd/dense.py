@@ -77,3 +77,17 @@ def linear(x, weight, out=None, out_dtype=None, stream=None):
     _lib.check(_lib.lib().zk_linear(_dev(x, "x"), _dev(weight, "weight"), _dev(out, "out"), m, n, k, _dt(x),
                                     zk_dtype(out), _stream(stream)))
     return out
+
+
+def linear_skinny(x, weight, splits=1, tile_rows=128, out=None, out_dtype=None, stream=None):
+    """The weight-streaming kernel zk_linear may choose for bf16 and m <= 64,
+    called directly: tiles of tile_rows weight rows, k split in `splits`."""
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or weight.dtype != torch.bfloat16 or x.dtype != torch.bfloat16:
+        raise ValueError("x and weight must be bf16, weight [n, k]")
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype or x.dtype, device=x.device)
+    _lib.check(_lib.lib().zk_linear_skinny(_dev(x, "x"), _dev(weight, "weight"), _dev(out, "out"), m, n, k,
+                                           zk_dtype(out), tile_rows, splits, _stream(stream)))
+    return out
