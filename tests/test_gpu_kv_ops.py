@@ -191,3 +191,45 @@ def test_copy_blocks_all_layers_bitexact():
     oracle.copy_blocks(ref, H * BS * D * 2, src, dst)
     for g, r in zip(pools, ref):
         assert np.array_equal(to_host(g), r)
+
+
+@pytest.mark.parametrize("H,D,BS", [(8, 128, 16), (1, 64, 16), (3, 96, 16), (2, 128, 8)])
+def test_copy_blocks_block_sizes_bitexact(H, D, BS):
+    """Blocks of whole 4 KiB pieces (32 KiB, 4 KiB) take the one-chunk-per-
+    thread kernel, the rest (2 KiB, 9 KiB) the per-block loop; ids outside
+    the pool skip their pair in both."""
+    from zealot_amd import ops
+    rng = np.random.default_rng(H * 1000 + D + BS)
+    NB = 24
+    pools_h = [rng.integers(0, 65535, (NB, H, BS, D), dtype=np.uint16) for _ in range(6)]
+    pools = [to_dev(p) for p in pools_h]
+    src = np.array([3, 7, -1, 20, 5, 40], np.int32)
+    dst = np.array([10, 11, 12, 23, NB, 0], np.int32)
+    announce(f"copy_blocks block {H}x{BS}x{D} bf16")
+    ops.copy_blocks(pools, to_dev(src), to_dev(dst))
+    torch.cuda.synchronize()
+    ref = [p.copy() for p in pools_h]
+    keep = (src >= 0) & (src < NB) & (dst >= 0) & (dst < NB)
+    oracle.copy_blocks(ref, H * BS * D * 2, src[keep], dst[keep])
+    for g, r in zip(pools, ref):
+        assert np.array_equal(to_host(g), r)
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 16, (10 << 20) + 48])
+def test_stream_yardsticks(nbytes):
+    """The bandwidth yardsticks: the copy is bit-exact, the read leaves its
+    sink alone for an all-zero buffer (its fold is zero)."""
+    import ctypes
+    from zealot_amd import _lib
+    lib = _lib.lib()
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device="cuda")
+    dst = torch.zeros_like(src)
+    announce(f"stream copy/read {nbytes} bytes")
+    _lib.check(lib.zk_stream_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()), nbytes, None))
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src)
+    zeros = torch.zeros_like(src)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    _lib.check(lib.zk_stream_read(ctypes.c_void_p(zeros.data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()), None))
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
