@@ -178,3 +178,28 @@ def test_linear_skinny_rejects_unsupported_shapes():
         dense.linear_skinny(x[:8], w[:48], tile_rows=64)  # n % tile_rows != 0
     with pytest.raises(ZealotError):
         dense.linear_skinny(x[:8], w, tile_rows=128)  # n % tile_rows != 0
+
+
+def test_linear_misaligned_operands_after_tuning():
+    """A shape whose cached choice may be the skinny kernel (16-byte aligned
+    operands only) still runs for operands 2 bytes off alignment: zk_linear
+    falls back to the hipBLASLt algorithm kept beside it."""
+    from zealot_amd import dense
+    rng = np.random.default_rng(77)
+    m, n, k = 64, 4096, 4096
+    x = normal(rng, (m, k), oracle.BF16)
+    w = oracle.bf16_bits_from_f32((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)).reshape(n, k)
+    announce("linear bf16 aligned, then misaligned x / y")
+    xd, wd = to_dev(x), to_dev(w)
+    y_al = dense.linear(xd, wd)  # tunes the shape
+    xbuf = torch.empty(m * k + 8, dtype=torch.bfloat16, device="cuda")
+    x_mis = xbuf[1:1 + m * k].view(m, k)
+    x_mis.copy_(xd)
+    ybuf = torch.empty(m * n + 8, dtype=torch.bfloat16, device="cuda")
+    y_mis = ybuf[1:1 + m * n].view(m, n)
+    dense.linear(x_mis, wd, out=y_mis)
+    torch.cuda.synchronize()
+    ref = as_f32(x, oracle.BF16).astype(np.float64) @ as_f32(w, oracle.BF16).astype(np.float64).T
+    for y in (y_al, y_mis):
+        got = as_f32(to_host(y.contiguous()), oracle.BF16)
+        assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
