@@ -204,6 +204,50 @@ def bench_decode(args, torch, ops, lib, kv="bf16"):
 
 # ---------------------------------------------------------------- C3 append
 
+def bench_gather(args, torch, ops, lib):
+    """Block-table gather (zk_gather) at C2's shape: every sequence's pages
+    copied to contiguous [ctx, Hkv, D] K and V rows."""
+    N, lo, hi = 256, 512, 8192
+    H, Hkv, D, BS = 32, 8, 128, 16
+    rng = np.random.default_rng(SEED)
+    lens = rng.integers(lo, hi + 1, N)
+    bt, nb, _ = paged_tables(rng, lens, BS)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    total = int(lens.sum())
+    log(f"gather bf16: N={N} sum_ctx={total} blocks={nb}")
+    kp = torch.randn((nb, Hkv, BS, D), generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn((nb, Hkv, BS, D), generator=g, device=dev).to(torch.bfloat16)
+    btd = torch.from_numpy(bt).to(dev)
+    lensd = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    offd = torch.from_numpy(offs).to(dev)
+    ko = torch.empty((total, Hkv, D), dtype=torch.bfloat16, device=dev)
+    vo = torch.empty_like(ko)
+
+    def step(_):
+        ops.gather(kp, vp, btd, lensd, offd, ko, vo)
+
+    ms = timed(step, args.steps, args.warmup, torch)
+    lib.zk_timing_reset()
+    lib.zk_timing_enable(1)
+    timed(step, args.steps, 0, torch)
+    lib.zk_timing_enable(0)
+    k_ms, _ = kernel_ms(lib, "gather")
+    lib.zk_timing_reset()
+    # spot check two sequences against torch indexing of the pools
+    for n in (0, N - 1):
+        L = int(lens[n])
+        blocks = torch.from_numpy(bt[n, np.arange(L) // BS].astype(np.int64)).to(dev)
+        tib = torch.from_numpy((np.arange(L) % BS).astype(np.int64)).to(dev)
+        ref = kp[blocks, :, tib, :]
+        assert torch.equal(ko[offs[n]: offs[n] + L], ref), "gather spot check"
+    nbytes = 2 * 2 * total * Hkv * D * 2 + int(np.ceil(lens / BS).sum()) * 4  # K+V read and written, tables
+    return {"ms_per_step": ms, "gbps": nbytes / (ms * 1e-3) / 1e9, "kernel_ms": k_ms,
+            "kernel_gbps": nbytes / (k_ms * 1e-3) / 1e9, "algorithmic_bytes": nbytes, "sum_ctx": total,
+            "num_seqs": N}
+
+
 def bench_append(args, torch, ops, lib):
     Nseq, C, Hkv, D, BS = 64, 512, 8, 128, 16
     R = 4  # rotating buffer sets: 4 x 256 MiB moved > 256 MB Infinity Cache
@@ -736,7 +780,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "append", "fp8", "c4", "prefill", "mixed", "model", "swap"],
+    ap.add_argument("--only", choices=["decode", "gather", "append", "fp8", "c4", "prefill", "mixed", "model",
+                                       "swap"],
                     default=None,
                     help="run one workload (for profiler passes)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -756,10 +801,13 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     result = {}
-    dec = lens = app = fp8 = c4 = pre = mix = mdl = swp = None
+    dec = lens = gat = app = fp8 = c4 = pre = mix = mdl = swp = None
     if args.only in (None, "decode"):
         dec, lens = bench_decode(args, torch, ops, lib, "bf16")
         log(f"decode bf16: {dec['ms_per_step']:.4f} ms {dec['gbps']:.1f} GB/s")
+    if args.only in (None, "gather"):
+        gat = bench_gather(args, torch, ops, lib)
+        log(f"gather bf16: {gat['ms_per_step']:.4f} ms {gat['gbps']:.1f} GB/s (kernel {gat['kernel_gbps']:.1f})")
     if args.only in (None, "append"):
         app = bench_append(args, torch, ops, lib)
         log(f"append bf16: {app['ms_per_step'] * 1e3:.2f} us {app['gbps']:.1f} GB/s")
@@ -789,6 +837,8 @@ def main() -> int:
         cpu = cpu_baseline(lens, args.cpu_sample_seqs)
         log(f"cpu baseline: {cpu['value']:.3f} GB/s (1 core), {cpu['omp_value']:.2f} GB/s ({cpu['omp_cores']} cores)")
     head = next((x for x in (dec, app, fp8) if x is not None), None)
+    if head is None and gat is not None:  # --only gather
+        head = {"gbps": gat["gbps"], "ms_per_step": gat["ms_per_step"], "roofline": None}
     if head is None and c4 is not None:  # --only c4
         head = {"gbps": c4["decode_step"]["logical_gbps"], "ms_per_step": c4["decode_step"]["ms_per_step"],
                 "roofline": None}
@@ -820,6 +870,7 @@ def main() -> int:
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "decode_bf16": dec,
+        "gather_bf16": gat,
         "append_bf16": app,
         "decode_fp8": fp8,
         "prefix_cow_c4": c4,
