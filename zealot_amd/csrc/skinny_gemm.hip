@@ -6,13 +6,16 @@
 // streaming w from HBM once.  The kernel is built around that stream:
 //  - a workgroup owns a tile of 64 or 128 weight rows (four waves of one or
 //    two 16-row MFMA tiles each) and a range of k / splits;
-//  - the waves load their weight rows straight into MFMA operand registers
-//    (16 bytes per lane, nontemporal: every weight byte is used once),
-//    three chunks of 128 k ahead of the one they multiply;
-//  - the activations of a chunk, x[0:m, chunk], are read once per
-//    workgroup (as far ahead) and copied into LDS (16-byte units of each row XOR-swizzled by the row,
-//    so the operand reads of 16 rows hit 16 different banks) and shared by
-//    the four waves;
+//  - weights and activations move to LDS by DMA (global_load_lds) in chunks
+//    of 128 k, in a ring of three or four chunks (as deep as 160 KiB of LDS
+//    allows): each wave fetches its own weight rows (nontemporal: every
+//    weight byte is used once), and the chunk's x[0:m] is fetched once per
+//    workgroup and shared by the four waves;
+//  - every DMA reads whole 256-byte row segments, each lane fetching column
+//    c ^ (row % 16) of its segment, so the MFMA operand reads (16 rows, one
+//    column) hit 16 different bank groups;
+//  - waits are explicit (the chunks issued after the awaited one stay in
+//    flight), with one barrier per chunk;
 //  - splits == 1: the waves write y; splits > 1: each range's sums go to a
 //    workspace [splits][m][n] and skinny_reduce_kernel adds them in range
 //    order, so the result does not depend on scheduling.
