@@ -44,10 +44,12 @@ int zk_embedding(const int64_t *ids, const void *table, void *out, int64_t num_t
 
 /* Projection y[m, n] = x[m, k] . w[n, k]^T (w in nn.Linear layout), the
  * product of every cublasSgemm_v2 site (attention/cublas.rs:72-114;
- * cuda_runner.rs:331-369, :483-495, :531-559, :577-589, :627-639), on
- * hipBLASLt with f32 accumulation; the algorithm is chosen per shape (see
- * zk_linear_tuning).  in_dtype F32 -> out F32; in_dtype BF16 ->
- * out BF16 or F32 (e.g. f32 logits). */
+ * cuda_runner.rs:331-369, :483-495, :531-559, :577-589, :627-639), with
+ * f32 accumulation, on hipBLASLt or (bf16, m <= 64) on this library's
+ * weight-streaming kernel (zk_linear_skinny): the fastest is chosen per shape
+ * (see zk_linear_tuning).  in_dtype F32 -> out F32; in_dtype BF16 ->
+ * out BF16 or F32 (e.g. f32 logits).  Calls on one device share workspaces:
+ * they must not overlap in time (one stream, or synchronized streams). */
 int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype in_dtype,
               zk_dtype out_dtype, void *stream);
 /* No counterpart in the reference: the weight-streaming kernel zk_linear's
