@@ -789,7 +789,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the decode shards by sequence / kv-head with no exchange; see DESIGN.md)",
+              "(the decode would shard by sequence / kv-head with no exchange)",
               file=sys.stderr)
         return 2
     import torch
