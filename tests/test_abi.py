@@ -81,6 +81,25 @@ def test_append_rejects_bad_arguments_on_host():
                        None, None, None, None) == _lib.OK
 
 
+def test_linear_skinny_rejects_bad_shapes_on_host():
+    """The weight-streaming GEMM's limits are checked before any device call."""
+    L = _lib.lib()
+    d = ctypes.c_void_p(0x1000)
+    bad = [
+        (65, 4096, 4096, _lib.BF16, 128, 1),    # m > 64
+        (8, 4096 + 64, 4096, _lib.BF16, 128, 1),  # n not a multiple of the tile rows
+        (8, 4096, 4096 + 64, _lib.BF16, 64, 1),   # k not a multiple of 128 * splits
+        (8, 4096, 4096, _lib.BF16, 64, 64),     # k % (128 * splits) != 0
+        (8, 4096, 4096, _lib.BF16, 96, 1),      # tile rows neither 64 nor 128
+        (64, 524288, 4096, _lib.BF16, 128, 2),  # split sums beyond the 32 MiB workspace
+        (8, 4096, 4096, _lib.FP8_E4M3, 128, 1),  # output dtype
+    ]
+    for m, n, k, od, rows, splits in bad:
+        rc, msg = _err(L.zk_linear_skinny(d, d, d, m, n, k, od, rows, splits, None))
+        assert rc == _lib.ERR_INVALID_ARGUMENT, (m, n, k, rows, splits, msg)
+        assert "zk_linear_skinny" in msg
+
+
 def test_decode_rejects_bad_arguments_on_host():
     L = _lib.lib()
     d = ctypes.c_void_p(0x1000)
