@@ -48,8 +48,10 @@ int zk_embedding(const int64_t *ids, const void *table, void *out, int64_t num_t
  * f32 accumulation, on hipBLASLt or (bf16, m <= 64) on this library's
  * weight-streaming kernel (zk_linear_skinny): the fastest is chosen per shape
  * (see zk_linear_tuning).  in_dtype F32 -> out F32; in_dtype BF16 ->
- * out BF16 or F32 (e.g. f32 logits).  Calls on one device share workspaces:
- * they must not overlap in time (one stream, or synchronized streams). */
+ * out BF16 or F32 (e.g. f32 logits).  Each (device, stream) has its own
+ * workspaces (up to 8 streams a device; a ninth replaces the least recently
+ * used one after a device synchronization), so calls on different streams
+ * may overlap. */
 int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype in_dtype,
               zk_dtype out_dtype, void *stream);
 /* No counterpart in the reference: the weight-streaming kernel zk_linear's
@@ -59,8 +61,8 @@ int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64
  * k / splits of k: needs n % tile_rows == 0, k % (128 * splits) == 0,
  * splits <= 64 and splits * m * n * 4 <= 32 MiB.  With splits > 1 the
  * ranges' sums are added in range order by a second kernel (the result does
- * not depend on scheduling); calls on one device share that workspace, so
- * they must not overlap in time (one stream, or synchronized streams). */
+ * not depend on scheduling), in the stream's own workspace as for
+ * zk_linear. */
 int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype out_dtype,
                      int tile_rows, int splits, void *stream);
 /* On (default): the first call of each (m, n, k, dtypes) times hipBLASLt's

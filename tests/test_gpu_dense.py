@@ -203,3 +203,33 @@ def test_linear_misaligned_operands_after_tuning():
     for y in (y_al, y_mis):
         got = as_f32(to_host(y.contiguous()), oracle.BF16)
         assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
+
+
+def test_linear_on_two_streams_at_once():
+    """Each stream has its own workspaces: split-k products (whose sums pass
+    through a workspace) on two streams in flight together both come out
+    right."""
+    from zealot_amd import dense
+    rng = np.random.default_rng(91)
+    m, n, k = 64, 4096, 4096
+    ws = [oracle.bf16_bits_from_f32((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)).reshape(n, k)
+          for _ in range(2)]
+    xs = [normal(rng, (m, k), oracle.BF16) for _ in range(2)]
+    wd, xd = [to_dev(w) for w in ws], [to_dev(x) for x in xs]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]  # default priority
+    torch.cuda.synchronize()  # the operands were written on the default stream
+    announce("linear + linear_skinny(splits=4) on two streams")
+    outs = []
+    for rep in range(3):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+                dense.linear_skinny(xd[i], wd[i], 4, 64, out=y, stream=st)
+                z = dense.linear(xd[i], wd[i], stream=st)
+                outs.append((i, y, z))
+    torch.cuda.synchronize()
+    for i, y, z in outs:
+        ref = as_f32(xs[i], oracle.BF16).astype(np.float64) @ as_f32(ws[i], oracle.BF16).astype(np.float64).T
+        for t in (y, z):
+            got = as_f32(to_host(t), oracle.BF16)
+            assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()

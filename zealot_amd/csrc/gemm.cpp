@@ -8,7 +8,8 @@
 // op(W) = transpose of W stored k x n, X^T stored k x m, both with leading
 // dimension k.  Inputs f32 or bf16 (both operands alike), output f32 or bf16,
 // f32 accumulation.  A plan (descriptors + an algorithm) is cached per
-// (device, m, n, k, dtypes); one workspace per device.  On first use of a
+// (device, m, n, k, dtypes); the workspaces are per (device, stream), so
+// calls on different streams may overlap.  On first use of a
 // shape the heuristic's 16 first candidates are timed on the caller's
 // operands and the fastest kept.  Skinny products over large weights (m <=
 // 256, n k >= 4M: a decode step's projections, HBM-bound on the weights) get
@@ -56,10 +57,19 @@ struct Plan {
     int tile_rows = 0;             // and tiles of this many weight rows
 };
 
+// Workspaces of one stream: hipBLASLt's, and the skinny kernel's split-k
+// sums (allocated when a plan first needs them).
+struct Scratch {
+    void *blas = nullptr;
+    void *partial = nullptr;
+    uint64_t used = 0;  // last use, for eviction
+};
+constexpr size_t kMaxStreams = 8;  // streams per device that keep their workspaces
+
 struct DeviceState {
     hipblasLtHandle_t handle = nullptr;
-    void *workspace = nullptr;
-    void *skinny_partial = nullptr;
+    std::map<hipStream_t, Scratch> scratch;
+    uint64_t clock = 0;
     std::map<std::tuple<int64_t, int64_t, int64_t, int, int>, Plan> plans;
 };
 
@@ -84,15 +94,35 @@ int device_state(DeviceState **out) {
             d.handle = nullptr;
             return fail("hipblasLtCreate", st);
         }
-        ZK_HIP_CHECK(hipMalloc(&d.workspace, kWorkspace), "zk_linear workspace");
     }
     *out = &d;
     return ZK_OK;
 }
 
-int skinny_workspace(DeviceState &d) {
-    if (d.skinny_partial) return ZK_OK;
-    ZK_HIP_CHECK(hipMalloc(&d.skinny_partial, kSkinnyPartial), "zk_linear skinny workspace");
+// The workspaces of `stream` on this device, created on first use.  A ninth
+// stream takes the place of the least recently used one, whose memory is
+// freed once the device has drained (a synchronization: not for callers
+// under stream capture, who use one stream).
+int scratch_for(DeviceState &d, hipStream_t stream, bool partial, Scratch **out) {
+    auto it = d.scratch.find(stream);
+    if (it == d.scratch.end()) {
+        if (d.scratch.size() >= kMaxStreams) {
+            auto lru = d.scratch.begin();
+            for (auto j = d.scratch.begin(); j != d.scratch.end(); ++j)
+                if (j->second.used < lru->second.used) lru = j;
+            ZK_HIP_CHECK(hipDeviceSynchronize(), "zk_linear workspace eviction");
+            (void)hipFree(lru->second.blas);
+            if (lru->second.partial) (void)hipFree(lru->second.partial);
+            d.scratch.erase(lru);
+        }
+        Scratch sc;
+        ZK_HIP_CHECK(hipMalloc(&sc.blas, kWorkspace), "zk_linear workspace");
+        it = d.scratch.emplace(stream, sc).first;
+    }
+    Scratch &sc = it->second;
+    if (partial && !sc.partial) ZK_HIP_CHECK(hipMalloc(&sc.partial, kSkinnyPartial), "zk_linear skinny workspace");
+    sc.used = ++d.clock;
+    *out = &sc;
     return ZK_OK;
 }
 
@@ -104,9 +134,9 @@ struct Problem {
     bool f32_out;
 };
 
-int run_skinny(DeviceState &d, const Problem &q, int tile_rows, int splits, hipStream_t stream) {
-    return zk::skinny_linear(q.x, q.w, q.y, q.m, q.n, q.k, q.f32_out, tile_rows, splits, d.skinny_partial,
-                             kSkinnyPartial, stream);
+int run_skinny(const Scratch &sc, const Problem &q, int tile_rows, int splits, hipStream_t stream) {
+    return zk::skinny_linear(q.x, q.w, q.y, q.m, q.n, q.k, q.f32_out, tile_rows, splits, sc.partial,
+                             sc.partial ? kSkinnyPartial : 0, stream);
 }
 
 bool skinny_fits(int64_t m, int64_t n, int64_t k, int tile_rows, int splits) {
@@ -139,16 +169,16 @@ struct Cand {
 // hipBLASLt one (best_blas, -1 if none ran).  The first n_always candidates
 // are always timed.  The output y is overwritten by every timed run and
 // finally by the real call.
-int pick_fastest(DeviceState &d, Plan &p, const std::vector<Cand> &cands, const Problem &q, size_t n_always,
-                 hipStream_t stream, bool cold, int *best, int *best_blas) {
+int pick_fastest(DeviceState &d, const Scratch &sc, Plan &p, const std::vector<Cand> &cands, const Problem &q,
+                 size_t n_always, hipStream_t stream, bool cold, int *best, int *best_blas) {
     hipEvent_t e0, e1;
     ZK_HIP_CHECK(hipEventCreate(&e0), "zk_linear tuning");
     ZK_HIP_CHECK(hipEventCreate(&e1), "zk_linear tuning");
     const float alpha = 1.0f, beta = 0.0f;
     auto run = [&](const Cand &c) {
-        if (c.splits) return run_skinny(d, q, c.tile_rows, c.splits, stream) == ZK_OK;
+        if (c.splits) return run_skinny(sc, q, c.tile_rows, c.splits, stream) == ZK_OK;
         return hipblasLtMatmul(d.handle, p.desc, &alpha, q.w, p.a, q.x, p.b, &beta, q.y, p.c, q.y, p.c, &c.algo,
-                               d.workspace, c.ws, stream) == HIPBLAS_STATUS_SUCCESS;
+                               sc.blas, c.ws, stream) == HIPBLAS_STATUS_SUCCESS;
     };
     auto timed = [&](const Cand &c, int reps, float *ms) {
         (void)hipEventRecord(e0, stream);
@@ -226,7 +256,7 @@ int pick_fastest(DeviceState &d, Plan &p, const std::vector<Cand> &cands, const 
     return ZK_OK;
 }
 
-int make_plan(DeviceState &d, int64_t m, int64_t n, int64_t k, zk_dtype in, zk_dtype out, const void *x,
+int make_plan(DeviceState &d, Scratch &sc, int64_t m, int64_t n, int64_t k, zk_dtype in, zk_dtype out, const void *x,
               const void *w, void *y, hipStream_t stream, bool tune, Plan **res) {
     auto key = std::make_tuple(m, n, k, (int)in, (int)out);
     auto it = d.plans.find(key);
@@ -264,7 +294,8 @@ int make_plan(DeviceState &d, int64_t m, int64_t n, int64_t k, zk_dtype in, zk_d
     const bool deep = m <= 256 && n * k >= (int64_t)1 << 22;
     const Problem q{x, w, y, m, n, k, out == ZK_F32};
     const bool aligned = (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0;
-    if (tune && deep && in == ZK_BF16 && aligned && skinny_workspace(d) == ZK_OK)
+    if (tune && deep && in == ZK_BF16 && aligned &&
+        (sc.partial || hipMalloc(&sc.partial, kSkinnyPartial) == hipSuccess))
         for (int rows : kSkinnyRows)
             for (int sp : kSkinnySplits)
                 if (skinny_fits(m, n, k, rows, sp)) cands.push_back({hipblasLtMatmulAlgo_t{}, 0, sp, rows});
@@ -287,7 +318,7 @@ int make_plan(DeviceState &d, int64_t m, int64_t n, int64_t k, zk_dtype in, zk_d
         }
     }
     if (tune && cands.size() > 1)
-        if (int rc = pick_fastest(d, p, cands, q, n_always, stream, deep, &best, &best_blas)) return rc;
+        if (int rc = pick_fastest(d, sc, p, cands, q, n_always, stream, deep, &best, &best_blas)) return rc;
     if (best_blas < 0) best_blas = 0;  // candidate 0 is the heuristic's first
     p.splits = cands[best].splits;
     p.tile_rows = cands[best].tile_rows;
@@ -314,15 +345,21 @@ int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64
     std::lock_guard<std::mutex> g(g_mu);
     DeviceState *d;
     if (int rc = device_state(&d)) return rc;
+    Scratch *sc;
+    if (int rc = scratch_for(*d, (hipStream_t)stream, false, &sc)) return rc;
     Plan *p;
-    if (int rc = make_plan(*d, m, n, k, in_dtype, out_dtype, x, w, y, (hipStream_t)stream, g_tune, &p)) return rc;
+    if (int rc = make_plan(*d, *sc, m, n, k, in_dtype, out_dtype, x, w, y, (hipStream_t)stream, g_tune, &p))
+        return rc;
     const float alpha = 1.0f, beta = 0.0f;
-    zk::KernelTimer timer("linear", (hipStream_t)stream);
-    if (p->splits && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0)
-        return run_skinny(*d, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, p->tile_rows, p->splits,
+    if (p->splits && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0) {
+        if (int rc = scratch_for(*d, (hipStream_t)stream, p->splits > 1, &sc)) return rc;
+        zk::KernelTimer timer("linear", (hipStream_t)stream);
+        return run_skinny(*sc, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, p->tile_rows, p->splits,
                           (hipStream_t)stream);
+    }
+    zk::KernelTimer timer("linear", (hipStream_t)stream);
     hipblasStatus_t st = hipblasLtMatmul(d->handle, p->desc, &alpha, w, p->a, x, p->b, &beta, y, p->c, y, p->c,
-                                         &p->algo, d->workspace, p->ws, (hipStream_t)stream);
+                                         &p->algo, sc->blas, p->ws, (hipStream_t)stream);
     if (st != HIPBLAS_STATUS_SUCCESS) return fail("hipblasLtMatmul", st);
     return ZK_OK;
 }
@@ -339,9 +376,10 @@ int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n
     std::lock_guard<std::mutex> g(g_mu);
     DeviceState *d;
     if (int rc = device_state(&d)) return rc;
-    if (int rc = skinny_workspace(*d)) return rc;
+    Scratch *sc;
+    if (int rc = scratch_for(*d, (hipStream_t)stream, splits > 1, &sc)) return rc;
     zk::KernelTimer timer("linear", (hipStream_t)stream);
-    return run_skinny(*d, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, tile_rows, splits, (hipStream_t)stream);
+    return run_skinny(*sc, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, tile_rows, splits, (hipStream_t)stream);
 }
 
 int zk_linear_tuning(int on) {
