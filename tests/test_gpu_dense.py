@@ -233,3 +233,29 @@ def test_linear_on_two_streams_at_once():
         for t in (y, z):
             got = as_f32(to_host(t), oracle.BF16)
             assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
+
+
+def test_linear_on_more_streams_than_kept_workspaces():
+    """Ten streams in turn: the ninth and tenth take the workspaces of the
+    least recently used streams (after the device drains), and every product
+    is still right, including on a stream whose workspace was replaced."""
+    from zealot_amd import dense
+    rng = np.random.default_rng(93)
+    m, n, k = 64, 4096, 4096
+    w = oracle.bf16_bits_from_f32((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)).reshape(n, k)
+    x = normal(rng, (m, k), oracle.BF16)
+    wd, xd = to_dev(w), to_dev(x)
+    ref = as_f32(x, oracle.BF16).astype(np.float64) @ as_f32(w, oracle.BF16).astype(np.float64).T
+    streams = [torch.cuda.Stream() for _ in range(10)]  # default priority
+    torch.cuda.synchronize()
+    announce("linear_skinny(splits=4) on 10 streams, then the first again")
+    outs = []
+    for st in streams + streams[:1]:
+        with torch.cuda.stream(st):
+            y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+            dense.linear_skinny(xd, wd, 4, 64, out=y, stream=st)
+            outs.append(y)
+        st.synchronize()
+    for y in outs:
+        got = as_f32(to_host(y), oracle.BF16)
+        assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
