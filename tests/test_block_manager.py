@@ -264,3 +264,25 @@ def test_forged_handle_for_free_block_is_rejected():
     assert bm.free_blocks == 2
     h = bm.allocate()
     assert (h.block_id, h.generation) == (0, 1)
+
+
+def test_bm_microbench_builds_and_runs(tmp_path):
+    """The C-ABI latency bench (zealot_amd/bm_microbench.c) builds with gcc
+    against the header and the library and reports every case."""
+    import os
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    lib_dir = os.path.join(root, "zealot_amd")
+    exe = str(tmp_path / "bm_microbench")
+    subprocess.run([gcc, "-O2", "-Wall", "-I", os.path.join(root, "include"),
+                    os.path.join(lib_dir, "bm_microbench.c"), "-L", lib_dir, "-lzealot_kv",
+                    f"-Wl,-rpath,{lib_dir}", "-o", exe], check=True)
+    out = subprocess.run([exe, "50"], check=True, capture_output=True, text=True).stdout.split()
+    got = dict(zip(out[0::2], map(float, out[1::2])))
+    assert set(got) == {"bm_allocate_1", "bm_free_last_ref", "bm_reference", "bm_stale_handle",
+                        "bm_allocate_full"}
+    assert all(v > 0 for v in got.values())

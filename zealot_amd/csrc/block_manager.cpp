@@ -38,14 +38,11 @@ namespace {
 
 int check(zk_block_manager *bm, zk_block_handle h) {
     if (h.block_id >= bm->num_gpu_blocks)
-        return zk::set_error(ZK_ERR_BLOCK_NOT_ALLOCATED,
-                             "Block " + std::to_string(h.block_id) + " is not allocated");
+        return zk::set_error_deferred(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::DeferredError::BlockNotAllocated, h.block_id);
     uint64_t cur = bm->generation[h.block_id].load(std::memory_order_acquire);
     if (h.generation != cur)
-        return zk::set_error(ZK_ERR_STALE_HANDLE,
-                             "Stale handle: block " + std::to_string(h.block_id) +
-                                 " was freed (gen " + std::to_string(h.generation) +
-                                 ", current " + std::to_string(cur) + ")");
+        return zk::set_error_deferred(ZK_ERR_STALE_HANDLE, zk::DeferredError::StaleHandle, h.block_id,
+                                      h.generation, cur);
     return ZK_OK;
 }
 
@@ -87,7 +84,7 @@ int zk_bm_allocate(zk_block_manager *bm, zk_block_handle *out) {
     {
         std::lock_guard<std::mutex> g(bm->mu);
         if (bm->free_list.empty())
-            return zk::set_error(ZK_ERR_OUT_OF_BLOCKS, "Out of blocks: requested 1, available 0");
+            return zk::set_error_deferred(ZK_ERR_OUT_OF_BLOCKS, zk::DeferredError::OutOfBlocks, 1, 0);
         id = bm->free_list.back();
         bm->free_list.pop_back();
     }
@@ -104,8 +101,8 @@ int zk_bm_free(zk_block_manager *bm, zk_block_handle h) {
     uint64_t prev = bm->refcount[h.block_id].load(std::memory_order_acquire);
     do {
         if (prev == 0)
-            return zk::set_error(ZK_ERR_BLOCK_NOT_ALLOCATED,
-                                 "Block " + std::to_string(h.block_id) + " is not allocated");
+            return zk::set_error_deferred(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::DeferredError::BlockNotAllocated,
+                                          h.block_id);
     } while (!bm->refcount[h.block_id].compare_exchange_weak(prev, prev - 1,
                                                               std::memory_order_acq_rel));
     if (prev == 1) {
@@ -122,8 +119,8 @@ int zk_bm_reference(zk_block_manager *bm, zk_block_handle h) {
     uint64_t prev = bm->refcount[h.block_id].load(std::memory_order_acquire);
     do {
         if (prev == 0)
-            return zk::set_error(ZK_ERR_BLOCK_NOT_ALLOCATED,
-                                 "Block " + std::to_string(h.block_id) + " is not allocated");
+            return zk::set_error_deferred(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::DeferredError::BlockNotAllocated,
+                                          h.block_id);
     } while (!bm->refcount[h.block_id].compare_exchange_weak(prev, prev + 1,
                                                               std::memory_order_acq_rel));
     return ZK_OK;
@@ -133,7 +130,7 @@ int zk_bm_check(zk_block_manager *bm, zk_block_handle h) {
     if (!bm) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_bm_check: NULL manager");
     if (int rc = check(bm, h)) return rc;
     if (bm->refcount[h.block_id].load(std::memory_order_acquire) == 0)
-        return zk::set_error(ZK_ERR_BLOCK_NOT_ALLOCATED, "Block " + std::to_string(h.block_id) + " is not allocated");
+        return zk::set_error_deferred(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::DeferredError::BlockNotAllocated, h.block_id);
     return ZK_OK;
 }
 

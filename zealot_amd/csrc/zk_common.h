@@ -14,6 +14,11 @@ namespace zk {
 // Thread-local last-error message (zk_last_error); set_error returns the code
 // so call sites read `return set_error(ZK_ERR_..., "...")`.
 int set_error(int code, const std::string &msg);
+// The same for the BlockManager's rejections, with the message built from
+// the arguments only when zk_last_error is called (a, b, c: block id and
+// generations, or requested and available blocks).
+enum class DeferredError { None, BlockNotAllocated, StaleHandle, OutOfBlocks };
+int set_error_deferred(int code, DeferredError kind, uint64_t a, uint64_t b = 0, uint64_t c = 0);
 void clear_error();
 
 #define ZK_HIP_CHECK(expr, ctx)                                                         \
