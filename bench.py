@@ -22,10 +22,12 @@ duration from the hipEvents the library records around each launch (on the
 launch stream) during a second timed region of the same steps; `value` comes
 from the first timed region, which has no per-kernel events.
 
-cpu_baseline: the CPU oracle's faithful scalar decode (oracle/zk_oracle.c,
-restating src/attention/mod.rs:64-98 over the pages) timed on this host on a
-bounded sample of the same workload (the first 128 sequences' context lengths),
-single-threaded; the OpenMP figure over all host cores is reported beside it.
+cpu_baseline: the CPU oracle's faithful restatement of the reference CPU path
+(oracle/zk_oracle.c) timed on this host, single-threaded and with OpenMP over
+the CPUs this process may use: the scalar decode (src/attention/mod.rs:64-98
+over the pages) on a bounded sample of C2 (the first 128 sequences' context
+lengths; the top-level value) and the per-(token, head) memcpy append
+(src/kv_cache.rs:229-274) over C3's whole workload (legs.append).
 """
 from __future__ import annotations
 
@@ -78,6 +80,23 @@ def timed(fn, steps, warmup, torch):
     e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def median_step_ms(fn, n, torch):
+    """Median (and spread) of n individually event-timed steps on the current
+    stream: the per-iteration protocol (>= 50 iterations, median) beside the
+    contract's mean over the K bracketed steps."""
+    s = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(ev):
+        a.record(s)
+        fn(i)
+        b.record(s)
+    torch.cuda.synchronize()
+    t = np.array([a.elapsed_time(b) for a, b in ev])
+    return {"median_ms": float(np.median(t)), "p10_ms": float(np.percentile(t, 10)),
+            "p90_ms": float(np.percentile(t, 90)), "iterations": n}
 
 
 def measured_traffic(key):
@@ -152,6 +171,7 @@ def bench_decode(args, torch, ops, lib, kv="bf16"):
         ops.paged_decode(q, kp, vp, btd, lensd, k_scales=ks, v_scales=vs, out=out, workspace=ws)
 
     ms = timed(step, args.steps, args.warmup, torch)
+    per_iter = median_step_ms(step, max(50, args.steps), torch)
     # second timed region with the library's per-kernel hipEvents on the same stream
     lib.zk_timing_reset()
     lib.zk_timing_enable(1)
@@ -190,6 +210,7 @@ def bench_decode(args, torch, ops, lib, kv="bf16"):
         "kernel_ms": {"decode_partials": k_ms, "decode_reduce": r_ms, "decode_seq_info": i_ms,
                       "decode_plan": p_ms},
         "ms_per_step_with_kernel_events": ms_ev,
+        "per_iteration": per_iter, "gbps_at_median": alg / (per_iter["median_ms"] * 1e-3) / 1e9,
         "read_ceiling_gbps": read_gbps,
         "kernel_frac_of_read_ceiling": (alg_kernel / (k_ms * 1e-3) / 1e9) / read_gbps,
         "roofline": {"bound": "hbm", "achieved": kgbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
@@ -287,6 +308,7 @@ def bench_append(args, torch, ops, lib):
         ops.append(kp, vp, k, v, s)
 
     ms = timed(step, args.steps, args.warmup, torch)
+    per_iter = median_step_ms(step, max(50, args.steps), torch)
     lib.zk_timing_reset()
     lib.zk_timing_enable(1)
     timed(step, args.steps, 0, torch)
@@ -314,6 +336,7 @@ def bench_append(args, torch, ops, lib):
     copy_gbps = 2 * nbytes / (cms * 1e-3) / 1e9
     res = {"ms_per_step": ms, "gbps": gbps, "frac_of_peak": gbps / PEAK_HBM_GBPS,
            "tokens_per_s": T / (ms * 1e-3), "algorithmic_bytes": alg,
+           "per_iteration": per_iter, "gbps_at_median": alg / (per_iter["median_ms"] * 1e-3) / 1e9,
            "stream_copy_gbps": copy_gbps, "frac_of_stream_copy": gbps / copy_gbps,
            "roofline": {"bound": "hbm", "achieved": kgbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                         "frac": kgbps / PEAK_HBM_GBPS, "traffic": measured_traffic("append_bf16"),
@@ -386,7 +409,12 @@ def bench_c4(args, torch, lib):
             for cid in children:
                 cache.release_seq(cid)
     lib.zk_timing_reset()
-    cow_bytes = 2 * n * 2 * L * BS * Hkv * D * 2  # read + write, every pool
+    # logical bytes: every fork's tail read and written in every pool; HBM
+    # bytes: each prefix's shared tail read once (its 8 forks copy the same
+    # block) and every copy written
+    block_bytes = BS * Hkv * D * 2
+    cow_logical = 2 * n * 2 * L * block_bytes
+    cow_hbm = (P + n) * 2 * L * block_bytes
     cow_ms = float(np.median(cow_kernel_ms))
     pos = [int(plen[p]) for p in parent]  # next token position of each fork
     nblk = [(x + BS - 1) // BS for x in pos]
@@ -450,9 +478,11 @@ def bench_c4(args, torch, lib):
         cache.release_seq(f"p{p}")
     assert bm.free_blocks == NB
     res = {
-        "cow": {"forks": n, "pools": 2 * L, "bytes": cow_bytes, "kernel_ms": cow_ms,
-                "gbps": cow_bytes / (cow_ms * 1e-3) / 1e9, "first_append_call_ms": float(np.median(cow_call_ms)),
-                "reps": COW_REPS},
+        "cow": {"forks": n, "pools": 2 * L, "hbm_bytes": cow_hbm, "kernel_ms": cow_ms,
+                "gbps": cow_hbm / (cow_ms * 1e-3) / 1e9, "frac_of_peak": cow_hbm / (cow_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                "logical_bytes": cow_logical, "logical_gbps": cow_logical / (cow_ms * 1e-3) / 1e9,
+                "traffic": measured_traffic("cow_c4"),
+                "first_append_call_ms": float(np.median(cow_call_ms)), "reps": COW_REPS},
         "decode_step": {"steps": STEPS, "ms_per_step": ms, "wall_ms_per_step": wall_ms,
                         "layers": L, "seqs": n,
                         "logical_ctx_per_layer": logical_ctx, "unique_ctx_per_layer": unique_ctx,
@@ -738,17 +768,41 @@ def bench_swap(args, torch, lib):
 
 # ---------------------------------------------------------------- CPU baseline
 
-def cpu_model() -> str:
+def host_cpu() -> dict:
+    """Model string, family/model/stepping and the core counts of this host."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k in ("model name", "cpu family", "model", "stepping", "vendor_id") and k not in info:
+                info[k] = v
+            if len(info) == 5:
+                break
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core"):
+                info["lscpu " + k.strip()] = v.strip()
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    info["os.cpu_count"] = os.cpu_count()
+    info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    return info
 
 
-def cpu_baseline(lens_all, sample_seqs):
+def cpu_threads() -> int:
+    """Threads for the OpenMP legs: the CPUs this process may run on."""
+    return max(1, len(os.sched_getaffinity(0)))
+
+
+def cpu_decode_leg(lens_all, sample_seqs, threads):
+    """The oracle's scalar decode (attention/mod.rs:64-98 over the pages) on
+    the first sample_seqs of the C2 context lengths."""
     import oracle
     H, Hkv, D, BS = 32, 8, 128, 16
     rng = np.random.default_rng(SEED + 2)
@@ -763,14 +817,63 @@ def cpu_baseline(lens_all, sample_seqs):
     t0 = time.perf_counter()
     oracle.paged_decode(q, kp, vp, oracle.BF16, bt, lens, Hkv, D, BS, scale, threads=1)
     t1 = time.perf_counter() - t0
-    cores = os.cpu_count() or 1
     t0 = time.perf_counter()
-    oracle.paged_decode(q, kp, vp, oracle.BF16, bt, lens, Hkv, D, BS, scale, threads=cores)
+    oracle.paged_decode(q, kp, vp, oracle.BF16, bt, lens, Hkv, D, BS, scale, threads=threads)
     tn = time.perf_counter() - t0
-    return {"value": alg / t1 / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"C2 decode, first {len(lens)} of the 256 context lengths (sum_ctx={sum(lens)}), "
-                      f"bf16 KV, scalar fp32 loops of oracle/zk_oracle.c, {t1:.2f} s",
-            "omp_value": alg / tn / 1e9, "omp_cores": cores, "host_cpu": cpu_model()}
+    return {"value": alg / t1 / 1e9, "unit": "GB/s", "cores": 1, "seconds": t1,
+            "omp_value": alg / tn / 1e9, "omp_cores": threads, "omp_seconds": tn,
+            "sample": f"C2 decode, first {len(lens)} of the 256 context lengths (sum_ctx={sum(lens)}), bf16 KV, "
+                      f"scalar fp32 loops of oracle/zk_oracle.c (or_paged_decode)"}
+
+
+def cpu_append_leg(threads, reps):
+    """The oracle's faithful store_kv (kv_cache.rs:229-274: one memcpy of D
+    elements per (token, kv-head) for K and for V) over C3's whole workload:
+    64 sequences x 512 tokens at unaligned starts, bf16, block tables drawn as
+    in bench_append; median of `reps` passes."""
+    import oracle
+    Nseq, C, Hkv, D, BS = 64, 512, 8, 128, 16
+    rng = np.random.default_rng(SEED + 1)
+    starts = rng.integers(0, 4096, Nseq)
+    starts[starts % BS == 0] += 1
+    pages = [(int(st) + C + BS - 1) // BS for st in starts]
+    nb = int(sum(pages) * 1.1) + 1
+    perm = rng.permutation(nb)
+    lists, o = [], 0
+    for pg in pages:
+        lists.append(perm[o:o + pg])
+        o += pg
+    T = Nseq * C
+    k = rng.integers(0, 1 << 16, (T, Hkv, D), dtype=np.uint16)
+    v = rng.integers(0, 1 << 16, (T, Hkv, D), dtype=np.uint16)
+    kp = np.zeros((nb, Hkv, BS, D), np.uint16)
+    vp = np.zeros_like(kp)
+    alg = 2 * (2 * T * Hkv * D * 2) + T * 8  # as the GPU leg: K+V read and written, slot per token
+    res = {}
+    for nthr in (1, threads):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            rc = oracle.store_kv_batch(kp, vp, oracle.BF16, k, v, lists, starts, [C] * Nseq, Hkv, D, BS, nthr)
+            ts.append(time.perf_counter() - t0)
+            assert rc == 0
+        res[nthr] = float(np.median(ts))
+    return {"value": alg / res[1] / 1e9, "unit": "GB/s", "cores": 1, "seconds_per_pass": res[1],
+            "omp_value": alg / res[threads] / 1e9, "omp_cores": threads, "omp_seconds_per_pass": res[threads],
+            "tokens_per_s": T / res[1],
+            "sample": f"C3 append, the whole workload (64 x 512 tokens, bf16, 8 x 128), median of {reps} passes "
+                      f"of oracle/zk_oracle.c or_store_kv (per-(token, head) memcpy), one call per sequence"}
+
+
+def cpu_baseline(lens_all, sample_seqs, reps=20):
+    threads = cpu_threads()
+    dec = cpu_decode_leg(lens_all, sample_seqs, threads)
+    app = cpu_append_leg(threads, reps)
+    # the headline metric is the decode's GB/s, so the top-level figures are its leg
+    return {"value": dec["value"], "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": dec["sample"] + f" ({dec['seconds']:.2f} s); append leg: " + app["sample"],
+            "omp_value": dec["omp_value"], "omp_cores": threads,
+            "legs": {"decode": dec, "append": app}, "host_cpu": host_cpu()}
 
 
 # ---------------------------------------------------------------- main
@@ -835,7 +938,9 @@ def main() -> int:
     cpu = None
     if args.only is None and not args.no_cpu_baseline:
         cpu = cpu_baseline(lens, args.cpu_sample_seqs)
-        log(f"cpu baseline: {cpu['value']:.3f} GB/s (1 core), {cpu['omp_value']:.2f} GB/s ({cpu['omp_cores']} cores)")
+        a = cpu["legs"]["append"]
+        log(f"cpu baseline: decode {cpu['value']:.3f} GB/s (1 core), {cpu['omp_value']:.2f} GB/s "
+            f"({cpu['omp_cores']} cores); append {a['value']:.2f} GB/s (1 core), {a['omp_value']:.2f} GB/s")
     head = next((x for x in (dec, app, fp8) if x is not None), None)
     if head is None and gat is not None:  # --only gather
         head = {"gbps": gat["gbps"], "ms_per_step": gat["ms_per_step"], "roofline": None}

@@ -66,6 +66,20 @@ typedef enum zk_gqa_mapping { ZK_GQA_GROUPED = 0, ZK_GQA_MODULO = 1 } zk_gqa_map
 
 /* Message of the last failure on this thread ("" if none). */
 const char *zk_last_error(void);
+/* Status code of the last failure on this thread (ZK_OK if none) and the
+ * fields of its ZealotError variant (src/error.rs:4-37), so a caller can
+ * rebuild the typed error without parsing the message:
+ *   ZK_ERR_STALE_HANDLE             {block_id, handle_gen, current_gen}
+ *   ZK_ERR_OUT_OF_BLOCKS            {requested, available, 0}
+ *   ZK_ERR_SEQUENCE_TOO_LONG        {required, capacity, 0}
+ *   ZK_ERR_BLOCK_NOT_ALLOCATED,
+ *   ZK_ERR_BLOCK_ALREADY_ALLOCATED,
+ *   ZK_ERR_INVALID_BLOCK_SIZE       {value, 0, 0}
+ *   every other code                {0, 0, 0} (the message carries the text)
+ * fields may be NULL.  A failure that a call re-raises after cleaning up
+ * (for example a BlockManager rejection inside a KVCache call) keeps its
+ * code and fields. */
+int zk_last_error_detail(uint64_t fields[3]);
 int zk_abi_version(void);
 
 /* ======================================================= BlockManager

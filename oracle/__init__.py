@@ -91,6 +91,8 @@ def _declare(L):
     L.or_f32_from_e4m3.argtypes = [ctypes.c_uint8]
     L.or_store_kv.restype = _I
     L.or_store_kv.argtypes = [_P, _P, _I, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I]
+    L.or_store_kv_batch.restype = _I
+    L.or_store_kv_batch.argtypes = [_P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
     L.or_append_slots.restype = _I
     L.or_append_slots.argtypes = [_P, _P, _I, _P, _P, _I, _P, _I64, _I, _I, _I, _I64, _P, _P, _P]
     L.or_fp8_scales.restype = None
@@ -169,6 +171,20 @@ def store_kv(k_pool, v_pool, dtype, k, v, block_ids, start_token, n_tokens, num_
     bids = np.ascontiguousarray(block_ids, dtype=np.int64)
     return lib().or_store_kv(_ptr(k_pool), _ptr(v_pool), dtype, _ptr(k), _ptr(v), _ptr(bids),
                              len(bids), start_token, n_tokens, num_kv_heads, head_dim, block_size)
+
+
+def store_kv_batch(k_pool, v_pool, dtype, k, v, block_lists, start_tokens, n_tokens, num_kv_heads, head_dim,
+                   block_size, threads=1) -> int:
+    """store_kv for each sequence n: n_tokens[n] rows of k/v (packed in batch
+    order) at start_tokens[n] through block_lists[n]; threads > 1 runs the
+    sequences on OpenMP threads."""
+    bids = np.ascontiguousarray(np.concatenate([np.asarray(b, np.int64) for b in block_lists]), dtype=np.int64)
+    boff = np.concatenate([[0], np.cumsum([len(b) for b in block_lists])]).astype(np.int64)
+    toff = np.concatenate([[0], np.cumsum(n_tokens)]).astype(np.int64)
+    st = np.ascontiguousarray(start_tokens, dtype=np.int64)
+    return lib().or_store_kv_batch(_ptr(k_pool), _ptr(v_pool), dtype, _ptr(k), _ptr(v), _ptr(bids), _ptr(boff),
+                                   _ptr(toff), _ptr(st), len(block_lists), num_kv_heads, head_dim, block_size,
+                                   threads)
 
 
 def append_slots(k_pool, v_pool, cache_dtype, k, v, src_dtype, slot_mapping, num_kv_heads,

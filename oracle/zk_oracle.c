@@ -104,6 +104,30 @@ int or_store_kv(void *k_pool, void *v_pool, int dtype, const void *k, const void
     return 0;
 }
 
+/* The CPU baseline's append leg: or_store_kv for each of num_seqs sequences
+ * (sequence n: its block ids block_ids[blk_off[n] .. blk_off[n+1]), tokens
+ * k/v rows tok_off[n] .. tok_off[n+1] at start_token[n]), as the reference
+ * runner would call KVCache::store_kv once per sequence
+ * (cuda_runner.rs:405-431).  threads > 1 spreads the sequences over OpenMP
+ * threads (the reference is single-threaded).  Returns the first failing
+ * sequence's status (-1) or 0. */
+int or_store_kv_batch(void *k_pool, void *v_pool, int dtype, const void *k, const void *v,
+                      const int64_t *block_ids, const int64_t *blk_off, const int64_t *tok_off,
+                      const int64_t *start_token, int num_seqs, int num_kv_heads, int head_dim,
+                      int block_size, int threads) {
+    size_t es = elt_size(dtype);
+    int64_t row = (int64_t)num_kv_heads * head_dim * (int64_t)es;
+    int rc = 0;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1) reduction(min : rc)
+    for (int n = 0; n < num_seqs; ++n) {
+        int r = or_store_kv(k_pool, v_pool, dtype, (const char *)k + tok_off[n] * row,
+                            (const char *)v + tok_off[n] * row, block_ids + blk_off[n], blk_off[n + 1] - blk_off[n],
+                            start_token[n], tok_off[n + 1] - tok_off[n], num_kv_heads, head_dim, block_size);
+        if (r < rc) rc = r;
+    }
+    return rc;
+}
+
 static void put_row(void *pool, int cache_dt, int64_t pool_off, const void *src, int src_dt,
                     int64_t src_off, int head_dim, float inv_scale) {
     if (cache_dt == src_dt && cache_dt != OR_FP8_E4M3) {

@@ -35,6 +35,13 @@ int or_store_kv(void *k_pool, void *v_pool, int dtype, const void *k, const void
                 const int64_t *block_ids, int64_t n_block_ids, int64_t start_token,
                 int64_t n_tokens, int num_kv_heads, int head_dim, int block_size);
 
+/* or_store_kv over a batch of sequences (the CPU baseline's append leg);
+ * threads > 1 runs the sequences on OpenMP threads. */
+int or_store_kv_batch(void *k_pool, void *v_pool, int dtype, const void *k, const void *v,
+                      const int64_t *block_ids, const int64_t *blk_off, const int64_t *tok_off,
+                      const int64_t *start_token, int num_seqs, int num_kv_heads, int head_dim,
+                      int block_size, int threads);
+
 /* Slot-mapping append (store/append of kv_cache.rs:229-274 and 316-344 with
  * slot = block_ids[g / bs] * bs + g % bs precomputed).  Negative slots skip. */
 int or_append_slots(void *k_pool, void *v_pool, int cache_dtype, const void *k, const void *v,

@@ -157,3 +157,4 @@ def test_product_does_not_import_the_oracle():
 def test_package_imports_without_gpu():
     from zealot_amd import HipAttention, KVCache, ops  # noqa: F401
     assert callable(ops.paged_decode) and callable(ops.append)
+

@@ -195,3 +195,29 @@ def test_c2_full_size_sampled_against_oracle():
         bt1 = np.arange(len(pages), dtype=np.int32)[None, :]
         ref = _oracle(to_host(q[n:n + 1]), kp, vp, bt1, [L], oracle.BF16, oracle.BF16, "grouped")
         assert max_abs_err(got[n:n + 1], ref) <= 2e-2, int(n)
+
+
+@pytest.mark.parametrize("H,Hkv,D,dt", [(4, 4, 32, oracle.F32), (32, 8, 128, oracle.BF16)])
+def test_hip_attention_paged_forward(H, Hkv, D, dt):
+    """HipAttention.paged_forward, the mirror of CudaAttention::paged_forward
+    (attention/cuda.rs:126-209): raw device addresses, scale 1/sqrt(D), grouped
+    mapping; equal to ops.paged_decode and within tolerance of the oracle."""
+    from zealot_amd import _lib
+    from zealot_amd.attention import HipAttention
+    lens = [1, 40, 300, 2049]
+    q, kp, vp, bt, nb = decode_case(60 + D, H, Hkv, D, lens, dt)
+    qd, kd, vd, btd = to_dev(q), to_dev(kp), to_dev(vp), to_dev(bt)
+    ld = to_dev(np.asarray(lens, np.int32))
+    o = torch.empty_like(qd)
+    zdt = _lib.F32 if dt == oracle.F32 else _lib.BF16
+    att = HipAttention()
+    for _ in range(2):  # the second call reuses the object's workspace
+        att.paged_forward(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), btd.data_ptr(), ld.data_ptr(), o.data_ptr(),
+                          len(lens), H, Hkv, D, 16, bt.shape[1], nb, q_dtype=zdt, kv_dtype=zdt)
+    torch.cuda.synchronize()
+    got = as_f32(to_host(o), dt)
+    assert np.array_equal(got, _run(q, kp, vp, bt, lens, dt))
+    assert max_abs_err(got, _oracle(q, kp, vp, bt, lens, dt, dt, "grouped")) <= TOL[dt]
+    with pytest.raises(RuntimeError, match="multiple of num_kv_heads"):
+        att.paged_forward(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), btd.data_ptr(), ld.data_ptr(),
+                          o.data_ptr(), len(lens), H + 1, Hkv, D, 16, bt.shape[1], nb, q_dtype=zdt, kv_dtype=zdt)

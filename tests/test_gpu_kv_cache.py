@@ -371,3 +371,32 @@ def test_decode_plan_reuse_across_layers_and_batches():
     check(0, ["a", "b"], [300, 40])
     check(2, ["b", "a"], [40, 301])  # order matters: sequence indices change
     torch.cuda.synchronize()
+
+
+def test_cow_out_of_blocks_keeps_typed_error():
+    """A BlockManager rejection raised inside a KVCache call (the copy-on-write
+    allocation) reaches the caller with its code and fields unchanged
+    (OutOfBlocks{requested: 1, available: 0}, src/error.rs:11-12), and nothing
+    is written."""
+    import zealot_amd as ze
+    from zealot_amd import KVCache
+    L, H, D, BS, NB = 2, 8, 128, 16, 3
+    bm = ze.BlockManager(NB, BS)
+    cache = KVCache(NB, BS, L, H, D, dtype=torch.bfloat16, max_seqs=4, max_blocks_per_seq=4)
+    cache.register_seq("p", 4)
+    for _ in range(3):
+        cache.alloc_block("p", bm)        # the pool is now empty
+    x = torch.ones((20, H, D), dtype=torch.bfloat16, device="cuda")
+    for layer in range(L):
+        cache.store_kv(layer, "p", x, x, 0, 20)
+    cache.fork_seq("p", "c")
+    one = torch.zeros((1, H, D), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ze.ZealotError) as e:
+        cache.append_kv(0, "c", one[0], one[0])  # needs a fresh block for the copy
+    assert e.value.code == ze._lib.ERR_OUT_OF_BLOCKS
+    assert e.value.fields == {"requested": 1, "available": 0}
+    assert str(e.value) == "Out of blocks: requested 1, available 0"
+    assert cache.seq_state("c").cached_tokens == 20
+    cache.release_seq("c")
+    cache.release_seq("p")
+    assert bm.free_blocks == NB

@@ -146,6 +146,35 @@ def test_store_kv_oob_is_an_error():
     assert oracle.store_kv(kp, kp.copy(), oracle.F32, k, k, [2], 0, 20, 1, 4, 16) == -1
 
 
+@pytest.mark.parametrize("threads", [1, 4])
+def test_store_kv_batch_is_store_kv_per_sequence(threads):
+    """The CPU baseline's append leg: the batched driver equals one
+    store_kv per sequence (index-tagged payloads, disjoint random blocks), on
+    one thread and on OpenMP threads; a sequence short of blocks fails."""
+    NB, H, BS, D = 64, 3, 16, 8
+    rng = np.random.default_rng(7)
+    starts, ns = [3, 17, 0, 40], [20, 33, 16, 9]
+    perm = rng.permutation(NB)
+    lists, o = [], 0
+    for s, n in zip(starts, ns):
+        nblk = (s + n + BS - 1) // BS
+        lists.append(perm[o:o + nblk])
+        o += nblk
+    k = oracle.bf16_bits_from_f32(_tagged(sum(ns), H, D, 5)).reshape(sum(ns), H, D)
+    v = oracle.bf16_bits_from_f32(_tagged(sum(ns), H, D, 6)).reshape(sum(ns), H, D)
+    kp1, vp1 = np.zeros((NB, H, BS, D), np.uint16), np.zeros((NB, H, BS, D), np.uint16)
+    row = 0
+    for b, s, n in zip(lists, starts, ns):
+        assert oracle.store_kv(kp1, vp1, oracle.BF16, k[row:row + n], v[row:row + n], b, s, n, H, D, BS) == 0
+        row += n
+    kp2, vp2 = np.zeros_like(kp1), np.zeros_like(vp1)
+    assert oracle.store_kv_batch(kp2, vp2, oracle.BF16, k, v, lists, starts, ns, H, D, BS, threads) == 0
+    assert np.array_equal(kp1, kp2) and np.array_equal(vp1, vp2)
+    assert np.count_nonzero(kp2) == np.count_nonzero(k)
+    short = [lists[0], lists[1][:1], lists[2], lists[3]]
+    assert oracle.store_kv_batch(kp2, vp2, oracle.BF16, k, v, short, starts, ns, H, D, BS, threads) == -1
+
+
 def test_append_slots_equals_store_kv_and_skips_negative():
     NB, H, BS, D, T, start = 10, 2, 16, 16, 40, 3
     ids = np.array([7, 2, 5, 9])

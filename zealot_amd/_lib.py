@@ -75,6 +75,7 @@ _CP = ctypes.c_char_p
 # name -> (restype, argtypes); every symbol declared in include/*.h.
 SIGNATURES = {
     "zk_last_error": (ctypes.c_char_p, []),
+    "zk_last_error_detail": (_I, [ctypes.POINTER(ctypes.c_uint64)]),
     "zk_abi_version": (_I, []),
     "zk_bm_create": (_I, [_SZ, _SZ, ctypes.POINTER(_P)]),
     "zk_bm_destroy": (None, [_P]),
@@ -156,12 +157,26 @@ SIGNATURES = {
 _lib = None
 
 
-class ZealotError(RuntimeError):
-    """Error raised from a zk_status; str() is the reference's message."""
+# Field names of the typed ZealotError variants (src/error.rs:4-37), in the
+# order zk_last_error_detail returns them.
+ERROR_FIELDS = {
+    ERR_BLOCK_ALREADY_ALLOCATED: ("block_id",),
+    ERR_BLOCK_NOT_ALLOCATED: ("block_id",),
+    ERR_OUT_OF_BLOCKS: ("requested", "available"),
+    ERR_INVALID_BLOCK_SIZE: ("block_size",),
+    ERR_STALE_HANDLE: ("block_id", "handle_gen", "current_gen"),
+    ERR_SEQUENCE_TOO_LONG: ("required", "capacity"),
+}
 
-    def __init__(self, code: int, message: str):
+
+class ZealotError(RuntimeError):
+    """Error raised from a zk_status; str() is the reference's message and
+    ``fields`` the variant's named fields (empty for untyped errors)."""
+
+    def __init__(self, code: int, message: str, fields: dict | None = None):
         super().__init__(message)
         self.code = code
+        self.fields = dict(fields or {})
 
 
 def lib() -> ctypes.CDLL:
@@ -180,7 +195,15 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+def last_error_detail() -> tuple[int, dict]:
+    """(status, named fields) of this thread's last failure (zk_last_error_detail)."""
+    raw = (ctypes.c_uint64 * 3)()
+    code = lib().zk_last_error_detail(raw)
+    return code, dict(zip(ERROR_FIELDS.get(code, ()), (int(x) for x in raw)))
+
+
 def check(rc: int) -> None:
     if rc != OK:
+        code, fields = last_error_detail()
         msg = lib().zk_last_error().decode("utf-8", "replace")
-        raise ZealotError(rc, msg)
+        raise ZealotError(rc, msg, fields if code == rc else {})

@@ -38,10 +38,10 @@ namespace {
 
 int check(zk_block_manager *bm, zk_block_handle h) {
     if (h.block_id >= bm->num_gpu_blocks)
-        return zk::set_error_deferred(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::DeferredError::BlockNotAllocated, h.block_id);
+        return zk::set_error_typed(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::ErrorKind::BlockNotAllocated, h.block_id);
     uint64_t cur = bm->generation[h.block_id].load(std::memory_order_acquire);
     if (h.generation != cur)
-        return zk::set_error_deferred(ZK_ERR_STALE_HANDLE, zk::DeferredError::StaleHandle, h.block_id,
+        return zk::set_error_typed(ZK_ERR_STALE_HANDLE, zk::ErrorKind::StaleHandle, h.block_id,
                                       h.generation, cur);
     return ZK_OK;
 }
@@ -54,7 +54,7 @@ int zk_bm_create(size_t num_gpu_blocks, size_t block_size, zk_block_manager **ou
     if (!out) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_bm_create: out is NULL");
     *out = nullptr;
     if (block_size == 0)
-        return zk::set_error(ZK_ERR_INVALID_BLOCK_SIZE, "Invalid block size: 0");
+        return zk::set_error_typed(ZK_ERR_INVALID_BLOCK_SIZE, zk::ErrorKind::InvalidBlockSize, 0);
     auto *bm = new (std::nothrow) zk_block_manager();
     if (!bm) return zk::set_error(ZK_ERR_INTERNAL, "Internal error: BlockManager allocation failed");
     try {
@@ -84,7 +84,7 @@ int zk_bm_allocate(zk_block_manager *bm, zk_block_handle *out) {
     {
         std::lock_guard<std::mutex> g(bm->mu);
         if (bm->free_list.empty())
-            return zk::set_error_deferred(ZK_ERR_OUT_OF_BLOCKS, zk::DeferredError::OutOfBlocks, 1, 0);
+            return zk::set_error_typed(ZK_ERR_OUT_OF_BLOCKS, zk::ErrorKind::OutOfBlocks, 1, 0);
         id = bm->free_list.back();
         bm->free_list.pop_back();
     }
@@ -101,7 +101,7 @@ int zk_bm_free(zk_block_manager *bm, zk_block_handle h) {
     uint64_t prev = bm->refcount[h.block_id].load(std::memory_order_acquire);
     do {
         if (prev == 0)
-            return zk::set_error_deferred(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::DeferredError::BlockNotAllocated,
+            return zk::set_error_typed(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::ErrorKind::BlockNotAllocated,
                                           h.block_id);
     } while (!bm->refcount[h.block_id].compare_exchange_weak(prev, prev - 1,
                                                               std::memory_order_acq_rel));
@@ -119,7 +119,7 @@ int zk_bm_reference(zk_block_manager *bm, zk_block_handle h) {
     uint64_t prev = bm->refcount[h.block_id].load(std::memory_order_acquire);
     do {
         if (prev == 0)
-            return zk::set_error_deferred(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::DeferredError::BlockNotAllocated,
+            return zk::set_error_typed(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::ErrorKind::BlockNotAllocated,
                                           h.block_id);
     } while (!bm->refcount[h.block_id].compare_exchange_weak(prev, prev + 1,
                                                               std::memory_order_acq_rel));
@@ -130,7 +130,7 @@ int zk_bm_check(zk_block_manager *bm, zk_block_handle h) {
     if (!bm) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_bm_check: NULL manager");
     if (int rc = check(bm, h)) return rc;
     if (bm->refcount[h.block_id].load(std::memory_order_acquire) == 0)
-        return zk::set_error_deferred(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::DeferredError::BlockNotAllocated, h.block_id);
+        return zk::set_error_typed(ZK_ERR_BLOCK_NOT_ALLOCATED, zk::ErrorKind::BlockNotAllocated, h.block_id);
     return ZK_OK;
 }
 

@@ -259,9 +259,9 @@ int cow_blocks(zk_kv_cache *c, const std::vector<std::pair<SeqState *, size_t>> 
     for (size_t i = 0; i < n; ++i) {
         SeqState &s = *targets[i].first;
         if (int rc = zk_bm_allocate(s.bm, &fresh[i])) {
-            std::string msg = zk_last_error();
+            const zk::ErrorSnapshot saved = zk::save_error();
             for (size_t j = 0; j < i; ++j) (void)zk_bm_free(targets[j].first->bm, fresh[j]);
-            return set_error(rc, msg);
+            return zk::restore_error(saved);
         }
         pairs[i] = (int32_t)s.handles[targets[i].second].block_id;
         pairs[n + i] = (int32_t)fresh[i].block_id;
@@ -279,25 +279,25 @@ int cow_blocks(zk_kv_cache *c, const std::vector<std::pair<SeqState *, size_t>> 
                             d, d + n, (int64_t)n, c->stream);
     }
     if (rc) {
-        std::string msg = zk_last_error();
+        const zk::ErrorSnapshot saved = zk::save_error();
         for (size_t j = 0; j < n; ++j) (void)zk_bm_free(targets[j].first->bm, fresh[j]);
-        return set_error(rc, msg);
+        return zk::restore_error(saved);
     }
     int first_rc = ZK_OK;
-    std::string first_msg;
+    zk::ErrorSnapshot first_err;
     for (size_t i = 0; i < n; ++i) {
         SeqState &s = *targets[i].first;
         size_t idx = targets[i].second;
         int frc = zk_bm_free(s.bm, s.handles[idx]);
         if (frc && !first_rc) {
             first_rc = frc;
-            first_msg = zk_last_error();
+            first_err = zk::save_error();
         }
         s.handles[idx] = fresh[i];
         queue_table_entry(c, s, idx, (int32_t)fresh[i].block_id);
     }
     rc = flush_tables(c);
-    if (first_rc) return set_error(first_rc, first_msg);
+    if (first_rc) return zk::restore_error(first_err);
     return rc;
 }
 
@@ -478,7 +478,7 @@ int zk_cache_create(size_t num_blocks, size_t block_size, size_t num_layers, siz
                     void *stream, zk_kv_cache **out) {
     if (!out) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_cache_create: out is NULL");
     *out = nullptr;
-    if (block_size == 0) return set_error(ZK_ERR_INVALID_BLOCK_SIZE, "Invalid block size: 0");
+    if (block_size == 0) return zk::set_error_typed(ZK_ERR_INVALID_BLOCK_SIZE, zk::ErrorKind::InvalidBlockSize, 0);
     if (!zk::valid_dtype(dtype) || num_blocks == 0 || num_layers == 0 || num_kv_heads == 0 ||
         head_dim == 0 || max_seqs == 0 || max_blocks_per_seq == 0 || num_blocks > 0x7fffffffu)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_cache_create: bad shape");
@@ -518,9 +518,8 @@ int zk_cache_register_seq(zk_kv_cache *c, const char *id, size_t max_blocks) {
     if (!c || !id) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache: NULL argument");
     if (c->seqs.count(id)) return set_error(ZK_ERR_ALREADY_EXISTS, std::string("Already exists: seq ") + id);
     if (max_blocks == 0 || max_blocks > c->max_blocks_per_seq)
-        return set_error(ZK_ERR_SEQUENCE_TOO_LONG,
-                         "Sequence too long: worst case needs " + std::to_string(max_blocks) +
-                             " blocks, pool capacity is " + std::to_string(c->max_blocks_per_seq));
+        return zk::set_error_typed(ZK_ERR_SEQUENCE_TOO_LONG, zk::ErrorKind::SequenceTooLong, max_blocks,
+                                   c->max_blocks_per_seq);
     if (c->free_slots.empty())
         return set_error(ZK_ERR_FAILED_PRECONDITION, "Failed precondition: KVCache: all sequence slots in use");
     DeviceGuard g(c->device);
@@ -572,13 +571,13 @@ int zk_cache_release_seq(zk_kv_cache *c, const char *id) {
     if (int rc = find_seq(c, id, &s)) return rc;
     DeviceGuard g(c->device);
     int first_rc = ZK_OK;
-    std::string first_msg;
+    zk::ErrorSnapshot first_err;
     for (const auto &h : s->handles) {
         if (s->borrowed) break;  // the caller frees its own handles
         int rc = zk_bm_free(s->bm, h);
         if (rc && !first_rc) {
             first_rc = rc;
-            first_msg = zk_last_error();
+            first_err = zk::save_error();
         }
     }
     release_host_slots(c, *s);
@@ -587,7 +586,7 @@ int zk_cache_release_seq(zk_kv_cache *c, const char *id) {
     c->free_slots.push_back(s->slot);
     c->seqs.erase(id);
     ++c->epoch;
-    if (first_rc) return set_error(first_rc, first_msg);
+    if (first_rc) return zk::restore_error(first_err);
     return rc;
 }
 
@@ -609,9 +608,9 @@ int zk_cache_fork_seq(zk_kv_cache *c, const char *parent, const char *child) {
     for (; done < p->handles.size(); ++done)
         if (zk_bm_reference(p->bm, p->handles[done])) break;
     if (done < p->handles.size()) {
-        std::string msg = zk_last_error();
+        const zk::ErrorSnapshot saved = zk::save_error();
         for (size_t i = 0; i < done; ++i) (void)zk_bm_free(p->bm, p->handles[i]);
-        return set_error(ZK_ERR_STALE_HANDLE, msg);
+        return zk::restore_error(saved);
     }
     SeqState s = *p;
     s.slot = c->free_slots.back();
@@ -754,9 +753,8 @@ int zk_cache_bind_blocks(zk_kv_cache *c, zk_block_manager *bm, const char *const
                 return set_error(ZK_ERR_INVALID_ARGUMENT,
                                  std::string("Internal error: KVCache bind_blocks: seq ") + ids[i] + " twice");
         if (num_blocks[i] > c->max_blocks_per_seq)
-            return set_error(ZK_ERR_SEQUENCE_TOO_LONG,
-                             "Sequence too long: worst case needs " + std::to_string(num_blocks[i]) +
-                                 " blocks, pool capacity is " + std::to_string(c->max_blocks_per_seq));
+            return zk::set_error_typed(ZK_ERR_SEQUENCE_TOO_LONG, zk::ErrorKind::SequenceTooLong, num_blocks[i],
+                                       c->max_blocks_per_seq);
         auto it = c->seqs.find(ids[i]);
         const size_t have = it == c->seqs.end() ? 0 : it->second.cached_tokens;
         if (it == c->seqs.end()) {
@@ -861,8 +859,7 @@ int zk_cache_swap_out(zk_kv_cache *c, const char *const *ids, int n) {
         need += nblk[i];
     }
     if (need > c->host_free.size())
-        return set_error(ZK_ERR_OUT_OF_BLOCKS, "Out of blocks: requested " + std::to_string(need) +
-                                                   ", available " + std::to_string(c->host_free.size()));
+        return zk::set_error_typed(ZK_ERR_OUT_OF_BLOCKS, zk::ErrorKind::OutOfBlocks, need, c->host_free.size());
     DeviceGuard g(c->device);
     std::vector<std::pair<int32_t, int32_t>> pairs;
     pairs.reserve(need);
@@ -883,7 +880,7 @@ int zk_cache_swap_out(zk_kv_cache *c, const char *const *ids, int n) {
     // the device blocks are free from here on; later writes into them are
     // queued after the staging copy on the same stream
     int first_rc = ZK_OK;
-    std::string first_msg;
+    zk::ErrorSnapshot first_err;
     for (int i = 0; i < n; ++i) {
         SeqState &s = *seqs[i];
         for (size_t j = 0; j < s.handles.size(); ++j) {
@@ -892,7 +889,7 @@ int zk_cache_swap_out(zk_kv_cache *c, const char *const *ids, int n) {
                 int r = zk_bm_free(s.bm, s.handles[j]);
                 if (r && !first_rc) {
                     first_rc = r;
-                    first_msg = zk_last_error();
+                    first_err = zk::save_error();
                 }
             }
         }
@@ -900,7 +897,7 @@ int zk_cache_swap_out(zk_kv_cache *c, const char *const *ids, int n) {
         s.swapped = true;
     }
     rc = flush_tables(c);
-    if (first_rc) return set_error(first_rc, first_msg);
+    if (first_rc) return zk::restore_error(first_err);
     return rc;
 }
 
@@ -941,10 +938,10 @@ int zk_cache_swap_in(zk_kv_cache *c, const char *const *ids, int n, zk_block_man
         for (size_t b = 0; b < s.host_slots.size(); ++b) {
             zk_block_handle h;
             if (int rc = zk_bm_allocate(m, &h)) {
-                std::string msg = zk_last_error();
+                const zk::ErrorSnapshot saved = zk::save_error();
                 for (int j = 0; j <= i; ++j)
                     for (const auto &x : fresh[j]) (void)zk_bm_free(seqs[j]->bm ? seqs[j]->bm : bm, x);
-                return set_error(rc, msg);
+                return zk::restore_error(saved);
             }
             fresh[i].push_back(h);
         }

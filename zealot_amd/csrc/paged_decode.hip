@@ -1031,12 +1031,12 @@ bool zk::paged_decode_shares_prefixes(int kv_dtype, int head_dim, int block_size
            mfma_supported(kv_dtype, head_dim, block_size, num_heads / num_kv_heads);
 }
 
-int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
-                     void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
-                     int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
-                     float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                     void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
-                     const int32_t *q_rows, int64_t q_stride, bool trusted_tables, bool reuse_plan) {
+namespace {
+
+// Host-side argument checks of zk_paged_decode (no device work).
+int check_decode_args(zk_dtype q_dtype, zk_dtype kv_dtype, int num_seqs, int num_heads, int num_kv_heads,
+                      int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
+                      zk_gqa_mapping mapping) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: q dtype must be f32 or bf16");
     if (!valid_dtype(kv_dtype))
@@ -1049,12 +1049,49 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                          "Internal error: zk_paged_decode: num_heads must be a multiple of num_kv_heads");
     if (mapping != ZK_GQA_GROUPED && mapping != ZK_GQA_MODULO)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: bad gqa mapping");
-    const int G = num_heads / num_kv_heads;
-    if (head_dim > 256 || G > kMaxG)
+    if (head_dim > 256 || num_heads / num_kv_heads > kMaxG)
         return set_error(ZK_ERR_INVALID_ARGUMENT,
                          "Internal error: zk_paged_decode: head_dim <= 256 and H/Hkv <= 16 required");
     if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffff)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: context too long");
+    return ZK_OK;
+}
+
+// Which kernel a call runs, how it cuts the contexts and the workspace it
+// needs (arguments already checked).
+struct DecodeShape {
+    bool use_mfma, shared;
+    int part_pages, shared_pages, max_parts;
+    WsLayout w;
+};
+DecodeShape decode_shape(zk_dtype kv_dtype, int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                         int block_size, int max_blocks_per_seq, const PrefixGroups *pg) {
+    DecodeShape d;
+    const int G = num_heads / num_kv_heads;
+    d.use_mfma = mfma_supported(kv_dtype, head_dim, block_size, G);
+    d.part_pages = d.use_mfma ? mfma_part_pages(num_seqs, num_kv_heads, max_blocks_per_seq)
+                              : part_pages_for(ZK_F32, head_dim, block_size);
+    d.shared = pg && pg->num_sg > 0 &&
+               paged_decode_shares_prefixes(kv_dtype, head_dim, block_size, num_heads, num_kv_heads);
+    d.shared_pages = d.shared ? shared_part_pages_for(pg->total_shared_pages, num_kv_heads) : 0;
+    // slot stride: a sequence's shared and private partitions together
+    d.max_parts = d.shared ? max_parts_for(max_blocks_per_seq, min_part_pages(head_dim, block_size)) + 1
+                           : max_parts_for(max_blocks_per_seq, d.part_pages);
+    d.w = ws_layout(num_seqs, num_heads, head_dim, d.max_parts);
+    return d;
+}
+
+}  // namespace
+
+int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
+                     void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
+                     int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
+                     float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
+                     void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
+                     const int32_t *q_rows, int64_t q_stride, bool trusted_tables, bool reuse_plan) {
+    if (int rc = check_decode_args(q_dtype, kv_dtype, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
+                                   max_blocks_per_seq, num_blocks, mapping))
+        return rc;
     if (num_seqs == 0) return ZK_OK;
     if (!q || !k_pool || !v_pool || !out || !block_tables || !seq_lens || !workspace)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode: NULL pointer");
@@ -1062,19 +1099,15 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     if (fp8 != (k_scales != nullptr && v_scales != nullptr))
         return set_error(ZK_ERR_INVALID_ARGUMENT,
                          "Internal error: zk_paged_decode: fp8 pools need k/v scales, other pools none");
-    const bool use_mfma = mfma_supported(kv_dtype, head_dim, block_size, G);
-    const int part_pages = use_mfma ? mfma_part_pages(num_seqs, num_kv_heads, max_blocks_per_seq)
-                                    : part_pages_for(ZK_F32, head_dim, block_size);
-    const bool shared = pg && pg->num_sg > 0 &&
-                        paged_decode_shares_prefixes(kv_dtype, head_dim, block_size, num_heads, num_kv_heads);
-    if (shared && (!pg->seq_pb || !pg->sg_members || !pg->sg_pages))
+    const int G = num_heads / num_kv_heads;
+    if (pg && pg->num_sg > 0 && (!pg->seq_pb || !pg->sg_members || !pg->sg_pages) &&
+        paged_decode_shares_prefixes(kv_dtype, head_dim, block_size, num_heads, num_kv_heads))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: paged decode: NULL prefix-group array");
-    const int shared_pages = shared ? shared_part_pages_for(pg->total_shared_pages, num_kv_heads) : 0;
-    // slot stride: a sequence's shared and private partitions together
-    const int max_parts =
-        shared ? max_parts_for(max_blocks_per_seq, min_part_pages(head_dim, block_size)) + 1
-               : max_parts_for(max_blocks_per_seq, part_pages);
-    WsLayout w = ws_layout(num_seqs, num_heads, head_dim, max_parts);
+    const DecodeShape ds =
+        decode_shape(kv_dtype, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, pg);
+    const bool use_mfma = ds.use_mfma, shared = ds.shared;
+    const int part_pages = ds.part_pages, shared_pages = ds.shared_pages, max_parts = ds.max_parts;
+    const WsLayout &w = ds.w;
     if (workspace_bytes < w.total || ((uintptr_t)workspace & 255u))
         return set_error(ZK_ERR_INVALID_ARGUMENT,
                          "Internal error: zk_paged_decode: workspace too small or not 256-B aligned (need " +

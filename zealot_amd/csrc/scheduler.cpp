@@ -229,9 +229,8 @@ int zk_sched_make_sequence(zk_scheduler *s, const char *id, const int64_t *promp
         return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_sched_make_sequence: bad priority");
     const size_t worst = blocks_for(prompt_len + max_tokens, s->cfg.block_size);  // scheduler.rs:234-240
     if (worst > s->cfg.num_gpu_blocks)
-        return zk::set_error(ZK_ERR_SEQUENCE_TOO_LONG, "Sequence too long: worst case needs " +
-                                                           std::to_string(worst) + " blocks, pool capacity is " +
-                                                           std::to_string(s->cfg.num_gpu_blocks));
+        return zk::set_error_typed(ZK_ERR_SEQUENCE_TOO_LONG, zk::ErrorKind::SequenceTooLong, worst,
+                                   s->cfg.num_gpu_blocks);
     auto *q = new (std::nothrow) zk_sequence();
     if (!q) return zk::set_error(ZK_ERR_INTERNAL, "Internal error: sequence allocation failed");
     q->s.id = id;
