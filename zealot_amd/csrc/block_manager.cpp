@@ -23,7 +23,7 @@
 #include <string>
 #include <vector>
 
-#include "zk_common.h"
+#include "zk_error.h"
 
 struct zk_block_manager {
     size_t num_gpu_blocks = 0;

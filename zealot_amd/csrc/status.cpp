@@ -2,7 +2,7 @@
 // fields of the reference's ZealotError variants, and the message.
 #include <string>
 
-#include "zk_common.h"
+#include "zk_error.h"
 
 namespace zk {
 namespace {
