@@ -177,6 +177,25 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
                     zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                     void *workspace, size_t workspace_bytes, void *stream);
 
+/* zk_paged_decode without the workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is the library's own device scratch of ZK_DECODE_SCRATCH_BYTES
+ * (64 MiB), one copy per GPU, held from the first call on a device until the
+ * process ends; the call allocates nothing and creates no events.  A call
+ * that needs more scratch than that (see zk_paged_decode_workspace_size; the
+ * exact need depends on the batch) fails with ZK_ERR_INVALID_ARGUMENT and
+ * launches nothing.  Every call on one GPU shares that GPU's scratch: calls
+ * that overlap on one GPU (different streams or host threads without
+ * ordering) race.  Inputs, outputs and results are those of zk_paged_decode. */
+#define ZK_DECODE_SCRATCH_BYTES (64u << 20)
+int zk_paged_decode_noalloc(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool,
+                            zk_dtype kv_dtype, void *out, const int32_t *block_tables,
+                            const int32_t *seq_lens, int num_seqs, int num_heads, int num_kv_heads,
+                            int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
+                            float scale, zk_gqa_mapping mapping, const float *k_scales,
+                            const float *v_scales, void *stream);
+
 /* ======================================================= KVCache (stateful)
  * src/kv_cache.rs:51-356.  Owns per-layer K/V pools (one HBM slab) and
  * per-sequence device block tables.  Sequence ids are NUL-terminated strings. */

@@ -158,3 +158,20 @@ def test_package_imports_without_gpu():
     from zealot_amd import HipAttention, KVCache, ops  # noqa: F401
     assert callable(ops.paged_decode) and callable(ops.append)
 
+
+def test_noalloc_decode_rejects_oversized_call_on_host():
+    """zk_paged_decode_noalloc checks the scratch it needs before touching a
+    device: 4096 sequences x 64 heads of fp32 partitions (the generic path
+    cuts 4096-page tables into 256 partitions) need far more than 64 MiB."""
+    L = _lib.lib()
+    dummy = ctypes.c_void_p(0x1000)
+    rc, msg = _err(L.zk_paged_decode_noalloc(dummy, _lib.F32, dummy, dummy, _lib.F32, dummy, dummy, dummy,
+                                             4096, 64, 4, 128, 16, 4096, 16, 0.1, _lib.GQA_GROUPED, None, None,
+                                             None))
+    assert rc == _lib.ERR_INVALID_ARGUMENT
+    assert "bytes of scratch, the maximum is 67108864" in msg
+    rc, msg = _err(L.zk_paged_decode_noalloc(dummy, _lib.F32, dummy, dummy, _lib.F32, dummy, dummy, dummy,
+                                             4, 30, 4, 128, 16, 64, 16, 0.1, _lib.GQA_GROUPED, None, None, None))
+    assert rc == _lib.ERR_INVALID_ARGUMENT and "multiple" in msg  # argument checks come first
+    assert L.zk_paged_decode_noalloc(None, _lib.F32, None, None, _lib.F32, None, None, None, 0, 4, 4, 128, 16,
+                                     64, 16, 0.1, _lib.GQA_GROUPED, None, None, None) == 0  # empty batch

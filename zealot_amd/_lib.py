@@ -94,6 +94,8 @@ SIGNATURES = {
     "zk_paged_decode_workspace_size": (_SZ, [_I, _I, _I, _I, _I]),
     "zk_paged_decode": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _F, _I,
                              _P, _P, _P, _SZ, _P]),
+    "zk_paged_decode_noalloc": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _F, _I,
+                                     _P, _P, _P]),
     "zk_paged_prefill_workspace_size": (_SZ, [_I, _I64, _I, _I]),
     "zk_paged_prefill": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _I64, _I, _I, _I, _I, _I, _I64, _F, _I,
                               _I, _P, _P, _P, _SZ, _P]),

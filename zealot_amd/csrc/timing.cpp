@@ -16,6 +16,7 @@ struct Record {
 };
 
 std::atomic<bool> g_on{false};
+thread_local int g_suspended = 0;
 std::mutex g_mu;
 std::vector<Record> g_records;
 std::vector<hipEvent_t> g_pool;
@@ -33,8 +34,11 @@ hipEvent_t take_event() {
 
 }  // namespace
 
+TimingSuspend::TimingSuspend() { ++g_suspended; }
+TimingSuspend::~TimingSuspend() { --g_suspended; }
+
 KernelTimer::KernelTimer(const char *name, hipStream_t stream) : name_(name), stream_(stream) {
-    if (!g_on.load(std::memory_order_relaxed)) return;
+    if (!g_on.load(std::memory_order_relaxed) || g_suspended) return;
     std::lock_guard<std::mutex> g(g_mu);
     start_ = take_event();
     stop_ = take_event();

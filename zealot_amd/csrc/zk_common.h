@@ -19,8 +19,17 @@ namespace zk {
                                                    ": " + hipGetErrorString(e_));       \
     } while (0)
 
+// While one exists on a thread, that thread's launches are not timed (entry
+// points that must not create hipEvents, such as the no-allocation decode).
+struct TimingSuspend {
+    TimingSuspend();
+    ~TimingSuspend();
+    TimingSuspend(const TimingSuspend &) = delete;
+    TimingSuspend &operator=(const TimingSuspend &) = delete;
+};
+
 // Brackets one kernel launch with hipEvents when timing is enabled
-// (zk_timing_enable); a no-op otherwise.
+// (zk_timing_enable) and not suspended on this thread; a no-op otherwise.
 class KernelTimer {
   public:
     KernelTimer(const char *name, hipStream_t stream);
