@@ -329,10 +329,10 @@ def test_forked_prefix_decode_shares_pages(G, D, qdt, mapping):
 
 def test_decode_plan_reuse_across_layers_and_batches():
     """The cache plans a decode once and reuses the plan while the shapes,
-    lengths and prefix groups stay the same (the layers of a step): the work
-    items name sequence indices and page ranges, not blocks, so another batch
-    with the same lengths may reuse it too; a length that changes in one
-    layer makes a new plan.  Every call is checked against the oracle."""
+    lengths, prefix groups and tables stay the same (the layers of a step);
+    the work items carry the block ids of their first pages, so another batch
+    with the same lengths but other tables, or a length that changes in one
+    layer, makes a new plan.  Every call is checked against the oracle."""
     import zealot_amd as ze
     from zealot_amd import KVCache
     rng = np.random.default_rng(77)
@@ -363,7 +363,7 @@ def test_decode_plan_reuse_across_layers_and_batches():
     announce("decode plan reuse")
     check(0, ["a", "b"], [300, 40])
     check(1, ["a", "b"], [300, 40])  # the next layer: same plan
-    check(1, ["c", "d"], [300, 40])  # other sequences, same lengths: same plan, other tables
+    check(1, ["c", "d"], [300, 40])  # other sequences, same lengths: other tables, a new plan
     # one more token in layer 2 only: a new plan there, and again for layer 0
     cache.store_kv(2, "a", to_dev(normal(rng, (1, Hkv, D), oracle.BF16)),
                    to_dev(normal(rng, (1, Hkv, D), oracle.BF16)), 300, 1)

@@ -144,8 +144,10 @@ struct zk_kv_cache {
     CachedBuf d_tbl;   // decode batch block tables [n][stride]
     CachedBuf d_batch; // decode batch lengths + scales
     // what the last decode plan was made from (shapes, lengths, prefix
-    // groups, tables and workspace); a call with the same bytes reuses it
+    // groups, the uploaded tables and workspace); a call with the same bytes
+    // reuses it
     std::vector<char> plan_sig;
+    uint64_t tbl_version = 0;  // bumped whenever d_tbl receives different tables
     CachedBuf d_pre;   // prefill batch tables, row offsets, lengths, starts, scales
     DevBuf d_pws;      // prefill workspace
     DevBuf d_ws;     // decode workspace
@@ -1047,6 +1049,9 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
             for (size_t j = 0; j < seqs[i]->handles.size(); ++j)
                 tbl[(size_t)i * stride + j] = (int32_t)seqs[i]->handles[j].block_id;
         c->dec_epoch = ~0ull;
+        const bool same = c->d_tbl.last.size() == tbl.size() * sizeof(int32_t) &&
+                          std::memcmp(c->d_tbl.last.data(), tbl.data(), c->d_tbl.last.size()) == 0;
+        if (!same) ++c->tbl_version;
         if (int rc = put(c, c->d_tbl, tbl.data(), tbl.size() * sizeof(int32_t), "KVCache decode tables")) return rc;
         c->dec_epoch = c->epoch;
         c->dec_ids = seqs;
@@ -1099,13 +1104,13 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
     c->last_sg = nsg;
     c->last_sg_pages = sp.total_pages;
     const int32_t *drows = q_rows ? (const int32_t *)(d + len_bytes + sc_bytes + share_bytes) : nullptr;
-    // The plan (work items over sequence indices and page ranges, in the
-    // workspace) depends on the shapes, the lengths and the prefix groups,
-    // not on the tables' contents, the layer's pools, q or scales: the
-    // layers of one step share it.
+    // The plan (work items over sequence indices and page ranges, each
+    // carrying the block ids of its first pages, in the workspace) depends on
+    // the shapes, the lengths, the prefix groups and the tables, not on the
+    // layer's pools, q or scales: the layers of one step share it.
     const uintptr_t hdr[] = {(uintptr_t)n,      (uintptr_t)num_heads,     stride,
                              (uintptr_t)nsg,    (uintptr_t)sp.total_pages, (uintptr_t)c->d_ws.p,
-                             (uintptr_t)c->d_ws.cap};
+                             (uintptr_t)c->d_ws.cap, (uintptr_t)c->tbl_version};
     std::vector<char> sig((const char *)hdr, (const char *)hdr + sizeof(hdr));
     sig.insert(sig.end(), host.data(), host.data() + len_bytes);
     sig.insert(sig.end(), host.data() + len_bytes + sc_bytes, host.data() + len_bytes + sc_bytes + share_bytes);

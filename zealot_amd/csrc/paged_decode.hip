@@ -72,6 +72,18 @@ int min_part_pages(int head_dim, int block_size) {
 
 constexpr int kSgStride = 32;  // member slots per prefix subgroup (query rows of one shared item)
 
+// Work queues of the persistent MFMA decode (Params::queues of them, 1 or
+// kQueues): item i belongs to queue i % queues, and workgroup w takes its
+// items from queue w % queues (with 8 queues, the XCD it runs on when
+// workgroups are dispatched round-robin over the 8 XCDs).  Each head sits on
+// its own 128-byte line.  One queue balances best (a global
+// longest-first order); batches of shared-prefix items, many of equal length
+// that finish at the same moment, use eight, so their claims go to eight
+// lines instead of one, whose atomics the L2 serialises.
+constexpr int kQueues = 8;
+constexpr int kQueueStride = 32;  // int32 slots between heads
+constexpr size_t kWorkBytes = sizeof(int32_t) * kQueueStride * (kQueues + 1);
+
 struct Params {
     const void *q;        // [rows, H, D]; sequence n's row is q_rows[n] (n when q_rows is null)
     const char *k_pool;
@@ -85,11 +97,13 @@ struct Params {
     int64_t q_stride;       // elements between consecutive q rows (out rows: H * D)
     int trusted;            // tables hold valid ids up to every length: no page walk
     int32_t *eff_len;     // [N] length after the page walk
-    int4 *items;          // [N * MP] work-item descriptors, longest first (MFMA path):
+    int4 *items;          // [N * MP][2] work-item descriptors, longest first (MFMA path):
                           //   {n, part, first page, pages} of a sequence's own pages or
-                          //   {-1 - g, part, member 0, pages} of subgroup g's shared pages
-    int32_t *work;        // [2] total items, queue head (MFMA path)
+                          //   {-1 - g, part, member 0, pages} of subgroup g's shared pages,
+                          //   then the block ids of the item's first kDescPages pages
+    int32_t *work;        // total items at [0]; the head of queue j at [kQueueStride * (j + 1)] (MFMA path)
     int num_waves;        // persistent grid: wave w starts with item w
+    int queues;           // work queues in use (1 or kQueues)
     float2 *ml;   // [N][H][MP] (m, l), log2 domain
     float *po;    // [N][H][MP][D]
     // Shared prefixes (MFMA bf16 path; all null when unused): sequence n's
@@ -169,11 +183,21 @@ __global__ void __launch_bounds__(kWave) seq_info_kernel(Params p) {
 }
 
 // ------------------------------------------------------------ helpers
+// Lane l ^ 16 / l ^ 32's value, on the VALU: v_permlane16_swap exchanges the
+// odd 16-lane rows of its first operand with the even rows of its second, and
+// v_permlane32_swap the upper half of the first with the lower half of the
+// second; with both operands v, a lane's partner value lands in the second
+// result on the even rows (lower half) and in the first elsewhere.  (Unlike
+// ds_swizzle / ds_bpermute they are not LDS instructions, so they never wait
+// behind outstanding LDS or scalar loads.)
 __device__ __forceinline__ float xor16(float v) {
-    // ds_swizzle bit mode: src = lane ^ 16 within 32-lane halves
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (0x10 << 10)));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
 }
-__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
+__device__ __forceinline__ float xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -197,6 +221,8 @@ constexpr float kRescaleSlack = 8.0f;
 // with one descriptor load.  Item i is pair i / Hkv, kv-head i % Hkv; wave w
 // takes item w first, then pulls from the queue, whose head the kernel sets.
 constexpr int kMaxItemPages = 1024;
+// Block ids carried in a work-item descriptor (the first pages of the item).
+constexpr int kDescPages = 4;
 
 // Pages in flight per wave in the MFMA decode (LDS stages of K + V).
 #ifndef ZK_DECODE_STAGES
@@ -255,12 +281,22 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
     hist[2 * t + 1] = base + a;
     const int total_pairs = sums[1023];
     __syncthreads();
+    // an item's descriptor carries the block ids of its first pages, so the
+    // decode issues them without waiting for the item's table entries
+    auto first_blocks = [&](const int32_t *row, int pages) {
+        int b[kDescPages];
+#pragma unroll
+        for (int j = 0; j < kDescPages; ++j) b[j] = j < pages ? row[j] : 0;
+        return make_int4(b[0], b[1], b[2], b[3]);
+    };
     for (int n = t; n < num_seqs; n += 1024) {
         const int np = private_items_of(p, n);
         for (int k = 0; k < np; ++k) {
             const int np = pair_pages(p, n, k);
             const int pos = atomicAdd(&hist[kMaxItemPages - np], 1);
-            p.items[pos] = make_int4(n, k, prefix_pages_of(p, n) + k * p.part_pages, np);
+            const int first = prefix_pages_of(p, n) + k * p.part_pages;
+            p.items[2 * pos] = make_int4(n, k, first, np);
+            p.items[2 * pos + 1] = first_blocks(p.bt + (size_t)n * p.max_blocks + first, np);
         }
     }
     for (int g = t; g < p.num_sg; g += 1024) {
@@ -271,12 +307,16 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
         for (int k = 0; k < np; ++k) {
             const int pos = atomicAdd(&hist[kMaxItemPages - shared_pair_pages(p, g, k)], 1);
             const int pages = max(0, min(p.shared_part_pages, valid - k * p.shared_part_pages));
-            p.items[pos] = make_int4(-1 - g, k, n0, pages);  // negative: subgroup item
+            p.items[2 * pos] = make_int4(-1 - g, k, n0, pages);  // negative: subgroup item
+            p.items[2 * pos + 1] =
+                first_blocks(p.bt + (size_t)n0 * p.max_blocks + (size_t)k * p.shared_part_pages, pages);
         }
     }
     if (t == 0) {
         p.work[0] = total_pairs * p.num_kv_heads;  // total items
-        p.work[1] = p.num_waves;                   // queue head: items below are taken statically
+    }
+    if (t < p.queues) {  // queue heads: wave w takes item w statically, w < num_waves
+        p.work[kQueueStride * (t + 1)] = (p.num_waves - t + p.queues - 1) / p.queues;
     }
 }
 
@@ -389,19 +429,42 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     };
 
     int next = 0;
-    // Claims the next item; called right after the item's first page loads
-    // are issued, so the atomic's round trip overlaps theirs.
+    // Claims the next item.  Called once per item, in the iteration that
+    // issues the item's last page (right after the first issues for items of
+    // at most kStages pages), so the atomic's round trip overlaps the item's
+    // last pages.  (Claiming at the start of an item instead lets every wave
+    // holding a long item reserve a short one it only starts much later,
+    // while waves that finish their short items find the queue empty: with
+    // mixed item lengths that left a tail of late short items.)
+    const int nq = p.queues, xq = blockIdx.x % nq;
+    auto head = [&](int q) { return p.work + kQueueStride * (q + 1); };
     auto claim_next = [&]() {
-        if (lane == 0) next = atomicAdd(&p.work[1], 1);
+        if (lane == 0) next = atomicAdd(head(xq), 1);
     };
 
-    // Block ids of an item's pages into LDS (eight independent loads in flight
-    // per lane).  The LDS writes wait for their loads, which retires the
-    // item's earlier register loads (Q fragments) too, so the page loop starts
-    // with no register loads pending.  (An explicit s_waitcnt here makes the
-    // compiler's wait insertion drain vmcnt before every page's LDS reads.)
+    // Data the kernel only reads (descriptors, subgroup members, lengths,
+    // scales) goes through constant-space views: scalar loads, counted by
+    // lgkmcnt, so they never hold up the page stream's vmcnt waits.
+    typedef const __attribute__((address_space(4))) int32_t *cint_t;
+    typedef const __attribute__((address_space(4))) float *cfloat_t;
+    const cint_t citems = (cint_t)p.items;
+    // descriptor of pair k: 8 ints (two int4)
+    auto load_desc = [&](int k, int4 &a, int4 &b) {
+        const cint_t c = citems + 8 * (size_t)k;
+        a = make_int4(c[0], c[1], c[2], c[3]);
+        b = make_int4(c[4], c[5], c[6], c[7]);
+    };
+
+    // Block ids of an item's pages kStages .. np-1 into LDS (bids[i] = table
+    // entry i; the first pages' ids come with the descriptor), eight
+    // independent loads in flight per lane.  The LDS writes wait for their
+    // loads, which retires every earlier load of the item (Q fragments, the
+    // first pages) too, so the page loop starts with nothing pending in the
+    // compiler's view.  (LDS-DMA staging of the ids, or register loads still
+    // pending at the loop, make the compiler wait for vmcnt(0) inside the
+    // page loop, which drains the page stream every page.)
     auto stage_bids = [&](const int32_t *row, int np) {
-        for (int i0 = 0; i0 < np; i0 += 8 * kWave) {
+        for (int i0 = kStages; i0 < np; i0 += 8 * kWave) {
             int32_t b[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -418,8 +481,8 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     };
 
     // B fragment of query row (n, qh): this lane group's DG dims as KK bf16x8.
-    auto load_q = [&](int n, int qh, bf16x8 *qf) {
-        const size_t qb = qrow(p, n) * (size_t)p.q_stride + (size_t)qh * D + (size_t)grp * DG;
+    auto load_q = [&](size_t qr, int qh, bf16x8 *qf) {
+        const size_t qb = qr * (size_t)p.q_stride + (size_t)qh * D + (size_t)grp * DG;
         if (p.q_f32) {
             const float *qq = (const float *)p.q + qb;
 #pragma unroll
@@ -436,18 +499,58 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         }
     };
 
+    const int total = *(cint_t)p.work;
+    // The next item and its descriptor, loaded while the current item's last
+    // page is computed (the claim has returned by then).  The scalar load is
+    // issued by inline asm: a plain load, whose result is only used after the
+    // page loop, is moved past the loop by the compiler; the asm keeps it in
+    // the last iteration, and desc_ready() waits for it (lgkmcnt) and hands
+    // the registers on.
+    typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+    int nx = 0;
+    i32x8 nraw = {0, 0, 0, 0, 0, 0, 0, 0};
+    bool have_next = false;
+    // (claims past the last item read a descriptor the item loop then
+    // ignores: the index is clamped to the descriptor array)
+    const int desc_cap = p.num_seqs * p.max_parts;
+    auto fetch_next = [&]() {
+        nx = __builtin_amdgcn_readfirstlane(next) * nq + xq;
+        if (nx >= total) {
+            // own queue done: take from the others (a plain load first, so
+            // exhausted queues cost no atomic)
+            int got = total;
+            if (lane == 0)
+                for (int j = 1; j < nq && got >= total; ++j) {
+                    const int q = (xq + j) % nq;
+                    if (__hip_atomic_load(head(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * nq + q >= total)
+                        continue;
+                    const int idx = atomicAdd(head(q), 1) * nq + q;
+                    if (idx < total) got = idx;
+                }
+            nx = __builtin_amdgcn_readfirstlane(got);
+        }
+        const int k = min(nx / Hkv, desc_cap - 1);
+        asm volatile("s_load_dwordx8 %0, %1, 0x0" : "=s"(nraw) : "s"(p.items + 2 * (size_t)k) : "memory");
+        have_next = true;
+    };
+    auto desc_ready = [&](int4 &a, int4 &b) {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(nraw)::"memory");
+        a = make_int4(nraw[0], nraw[1], nraw[2], nraw[3]);
+        b = make_int4(nraw[4], nraw[5], nraw[6], nraw[7]);
+    };
+
     // Attention of T tiles of query rows (qf) over pages [page0, page0 + np)
     // of table `trow` for kv-head kvh; tokens at positions >= len are masked.
+    // trow points at the table entry of page page0; blk0 holds the block ids
+    // of the first kDescPages pages.
     // Leaves O^T (o), the rows' reference max (m) and sum (l, all 4 lane
     // groups) for the caller to write.
-    auto attend = [&]<int T>(const bf16x8 (&qf)[T][KK], const int32_t *trow, int page0, int np, int len,
+    auto attend = [&]<int T>(const bf16x8 (&qf)[T][KK], const int32_t *trow, int4 blk0, int page0, int np, int len,
                              int kvh, float sl2, f32x4 (&o)[DT][T], float (&m)[T], float (&l)[T]) {
-        stage_bids(trow + page0, np);
         const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
         const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
         const size_t block_bytes = (size_t)PAGE * Hkv;
-        auto issue = [&](int pi, int s) {
-            const int blk = __builtin_amdgcn_readfirstlane(bids[pi]);
+        auto issue_blk = [&](int blk, int s) {
             const char *kp = kbase + (size_t)blk * block_bytes;
             const char *vp = vbase + (size_t)blk * block_bytes;
 #pragma unroll
@@ -474,8 +577,19 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             vtrow_t vt[4];  // token rows 4*grp+i, dims DT*col .. DT*col+DT-1
 #pragma unroll
             for (int i = 0; i < 4; ++i) vt[i] = *reinterpret_cast<const vtrow_t *>(lds[s][1] + vt_off + i * RB);
-            wait_lgkmcnt0();
-            if (pi + kStages < np) issue(pi + kStages, s);  // the stage is free again
+            const int nb = bids[min(pi + kStages, kMaxItemPages - 1)];
+            // The stage is free once its reads are done: the empty asm needs
+            // their results, so the compiler's own lgkmcnt wait lands here
+            // (it does not count an explicit s_waitcnt as completing them and
+            // would wait again at the MFMAs, behind the prefetch below).
+#pragma unroll
+            for (int j = 0; j < KBYTES / 4; ++j) asm volatile("" ::"v"(kw[j]));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" ::"v"(vt[i]));
+            asm volatile("" ::"v"(nb));
+            if (pi + kStages < np) issue_blk(__builtin_amdgcn_readfirstlane(nb), s);
+            if (pi == np - 1 - kStages) claim_next();
+            if (pi == np - 1) fetch_next();
 
             f32x4 sacc[T];
 #pragma unroll
@@ -557,8 +671,19 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
                     o[dt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt][t], 0, 0, 0);
             }
         };
-        for (int j = 0; j < kStages && j < np; ++j) issue(j, j);
-        claim_next();
+        // the first pages straight from the descriptor, then the other ids
+        static_assert(kStages <= kDescPages, "descriptor carries the first kStages block ids");
+        const int b0[4] = {blk0.x, blk0.y, blk0.z, blk0.w};
+#pragma unroll
+        for (int j = 0; j < kStages; ++j)
+            if (j < np) issue_blk(b0[j], j);
+        stage_bids(trow, np);
+        // Q is complete before the loop on every path (see stage_bids)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) asm volatile("" ::"v"(qf[t][kk]));
+        if (np <= kStages) claim_next();
         // one page per iteration (a single loop-carried accumulator set)
         for (int pi = 0, st = 0; pi < np; ++pi, st = (st + 1 == kStages ? 0 : st + 1)) page(pi, st);
 #pragma unroll
@@ -579,31 +704,44 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             __builtin_memcpy(dst + DT * (4 * grp + i), v, sizeof(v));
         }
     };
+    // q / out row of sequence n
+    auto q_row = [&](int n) -> size_t { return p.q_rows ? (size_t)((cint_t)p.q_rows)[n] : (size_t)n; };
 
-    const int total = p.work[0];
     int item = blockIdx.x;  // first item static, the rest from the queue
+    int4 d0 = make_int4(0, 0, 0, 0), d1 = make_int4(0, 0, 0, 0);
+    if (item < total) load_desc(item / Hkv, d0, d1);
     while (item < total) {
         const int kvh = item % Hkv;
-        const int4 desc = p.items[item / Hkv];
-        if (KV == ZK_BF16 && desc.x < 0) {
+        have_next = false;
+        if (KV == ZK_BF16 && d0.x < 0) {
             // shared-prefix partition of subgroup sg: up to 32 rows, member-major
-            const int sg = -1 - desc.x, part = desc.y, n0 = desc.z, np = desc.w;
-            const int32_t *mem = p.sg_members + (size_t)sg * kSgStride;
+            const int sg = -1 - d0.x, part = d0.y, n0 = d0.z, np = d0.w;
+            const int page0 = part * p.shared_part_pages;
+            // members (batch indices) of the subgroup, by scalar loads; lane
+            // (grp, col) serves row r = 16 t + col, member r / G
+            constexpr int NM = kSgStride / G;
+            const cint_t cmem = (cint_t)(p.sg_members + (size_t)sg * kSgStride);
+            int mem_s[NM];
+#pragma unroll
+            for (int j = 0; j < NM; ++j) mem_s[j] = cmem[j];
             bf16x8 qf[2][KK];
-            int nm[2];  // member (batch index) of this lane's row in tile t, or -1
+            int nm[2];  // member of this lane's row in tile t, or -1
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int r = 16 * t + col;
-                nm[t] = mem[r / G];
-                if (nm[t] >= 0) load_q(nm[t], qhead_of(p, kvh, r % G, G), qf[t]);
+                int v = mem_s[0];
+#pragma unroll
+                for (int j = 1; j < NM; ++j) v = r / G == j ? mem_s[j] : v;
+                nm[t] = v;
+                if (nm[t] >= 0) load_q(q_row(nm[t]), qhead_of(p, kvh, r % G, G), qf[t]);
                 else
 #pragma unroll
                     for (int kk = 0; kk < KK; ++kk) qf[t][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
             }
             f32x4 o[DT][2];
             float m[2], l[2];
-            attend.template operator()<2>(qf, p.bt + (size_t)n0 * p.max_blocks, part * p.shared_part_pages, np,
-                                          0x7fffffff, kvh, p.scale_log2, o, m, l);
+            attend.template operator()<2>(qf, p.bt + (size_t)n0 * p.max_blocks + page0, d1, page0, np, 0x7fffffff,
+                                          kvh, p.scale_log2, o, m, l);
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int r = 16 * t + col;
@@ -615,28 +753,32 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             }
         } else {
             // a sequence's own partition: rows 0..G-1 are its heads of kv-head kvh
-            const int n = desc.x, part = desc.y, page0 = desc.z, np = desc.w;
-            const int len = p.eff_len[n];  // walk already cut at the first invalid entry
-            const int ns = shared_parts_of(p, n);  // partial slots before this sequence's own
-            const int nparts = private_parts_of(p, n);
+            const int n = d0.x, part = d0.y, page0 = d0.z, np = d0.w;
+            const int len = ((cint_t)p.eff_len)[n];  // walk already cut at the first invalid entry
+            const int pb = p.seq_pb ? ((cint_t)p.seq_pb)[n] : 0;
+            const int ns = pb > 0 ? (pb + p.shared_part_pages - 1) / p.shared_part_pages : 0;
+            const int rest = (len + p.block_size - 1) / p.block_size - pb;
+            const int nparts = rest > 0 ? (rest + p.part_pages - 1) / p.part_pages : 0;
             const int qh = qhead_of(p, kvh, col % G, G);
+            const size_t qr = q_row(n);
             bf16x8 qf[1][KK];
-            if (col < G) load_q(n, qh, qf[0]);
+            if (col < G) load_q(qr, qh, qf[0]);
             else
 #pragma unroll
                 for (int kk = 0; kk < KK; ++kk) qf[0][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
             float sl2 = p.scale_log2, vscale = 1.0f;
             if constexpr (KV == ZK_FP8_E4M3) {
-                sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
-                vscale = p.v_scales[(size_t)n * Hkv + kvh];
+                sl2 *= ((cfloat_t)p.k_scales)[(size_t)n * Hkv + kvh];
+                vscale = ((cfloat_t)p.v_scales)[(size_t)n * Hkv + kvh];
             }
             f32x4 o[DT][1];
             float m[1], l[1];
-            attend.template operator()<1>(qf, p.bt + (size_t)n * p.max_blocks, page0, np, len, kvh, sl2, o, m, l);
+            attend.template operator()<1>(qf, p.bt + (size_t)n * p.max_blocks + page0, d1, page0, np, len, kvh, sl2,
+                                          o, m, l);
             if (col < G) {
                 if (ns == 0 && nparts <= 1) {  // the whole context: write the output row
                     const float inv = l[0] > 0.0f ? vscale / l[0] : 0.0f;
-                    const size_t ob = (qrow(p, n) * H + qh) * D;
+                    const size_t ob = (qr * H + qh) * D;
                     if (p.q_f32) {
                         f32x4 o2[DT][2];
 #pragma unroll
@@ -662,7 +804,9 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
                 }
             }
         }
-        item = __builtin_amdgcn_readfirstlane(next);
+        if (!have_next) fetch_next();  // an item without pages
+        item = nx;
+        desc_ready(d0, d1);
     }
 }
 
@@ -671,7 +815,8 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
 // the decode kernel's last wave instead measured 20 % slower on the fp8
 // decode: every wave then waits for its own stores before it exits.)
 __global__ void __launch_bounds__(64) queue_reset_kernel(Params p) {
-    if (threadIdx.x == 0) p.work[1] = p.num_waves;
+    const int t = threadIdx.x;
+    if (t < p.queues) p.work[kQueueStride * (t + 1)] = (p.num_waves - t + p.queues - 1) / p.queues;
 }
 
 // ------------------------------------------------------------ generic kernel
@@ -920,8 +1065,8 @@ WsLayout ws_layout(int num_seqs, int num_heads, int head_dim, int max_parts) {
     w.eff = 0;
     w.items = align256(sizeof(int32_t) * (size_t)num_seqs);
     w.map = w.items;
-    w.work = w.map + align256(sizeof(int4) * (size_t)num_seqs * max_parts);
-    w.ml = w.work + 256;
+    w.work = w.map + align256(2 * sizeof(int4) * (size_t)num_seqs * max_parts);
+    w.ml = w.work + align256(kWorkBytes);
     size_t slots = (size_t)num_seqs * num_heads * max_parts;
     w.po = w.ml + align256(sizeof(float2) * slots);
     w.total = w.po + align256(sizeof(float) * slots * head_dim);
@@ -1132,6 +1277,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.items = (int4 *)(ws + w.map);
     p.work = (int32_t *)(ws + w.work);
     p.num_waves = use_mfma ? persistent_grid() : 0;
+    p.queues = shared ? kQueues : 1;
     p.ml = (float2 *)(ws + w.ml);
     p.po = (float *)(ws + w.po);
     p.num_seqs = num_seqs;
