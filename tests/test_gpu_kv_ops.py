@@ -215,6 +215,33 @@ def test_copy_blocks_block_sizes_bitexact(H, D, BS):
         assert np.array_equal(to_host(g), r)
 
 
+@pytest.mark.parametrize("H,D,BS", [(8, 128, 16), (2, 128, 8)])
+def test_copy_blocks_runs_of_one_source_bitexact(H, D, BS):
+    """Forks copying one shared block give many pairs with the same source
+    (the copy-on-write of a forked prefix's tail): runs of 1, 3, 16, 17 and
+    40 pairs, a source repeated in two separate runs, an invalid source and
+    invalid destinations inside runs, bit-exact against the oracle's
+    pair-by-pair copy, for the piece kernel and the per-block kernel."""
+    from zealot_amd import ops
+    rng = np.random.default_rng(36 + H)
+    NB = 200
+    lengths = [1, 3, 16, 17, 40, 5, 2]
+    sources = [5, 9, 13, 17, 21, 9, -1]  # 9 appears in two runs; -1 is skipped
+    src = np.concatenate([np.full(n, s_, np.int32) for n, s_ in zip(lengths, sources)])
+    dst = (np.arange(len(src), dtype=np.int32) + 60)  # distinct, none a source
+    dst[[4, 30, 70]] = [NB, -3, NB + 1]              # skipped destinations inside runs
+    pools_h = [rng.integers(0, 65535, (NB, H, BS, D), dtype=np.uint16) for _ in range(4)]
+    pools = [to_dev(p) for p in pools_h]
+    announce(f"copy_blocks runs {lengths} block {H}x{BS}x{D}")
+    ops.copy_blocks(pools, to_dev(src), to_dev(dst))
+    torch.cuda.synchronize()
+    ref = [p.copy() for p in pools_h]
+    keep = (src >= 0) & (src < NB) & (dst >= 0) & (dst < NB)
+    oracle.copy_blocks(ref, H * BS * D * 2, src[keep], dst[keep])
+    for g, r in zip(pools, ref):
+        assert np.array_equal(to_host(g), r)
+
+
 @pytest.mark.parametrize("nbytes", [16, 4096 + 16, (10 << 20) + 48])
 def test_stream_yardsticks(nbytes):
     """The bandwidth yardsticks: the copy is bit-exact, the read leaves its

@@ -255,17 +255,24 @@ int cow_blocks(zk_kv_cache *c, const std::vector<std::pair<SeqState *, size_t>> 
             return set_error(ZK_ERR_FAILED_PRECONDITION,
                              "Failed precondition: KVCache: copy-on-write of a block whose handle the caller "
                              "owns (bound sequence)");
-    const size_t n = targets.size();
+    // pairs with the same source next to each other: the copy kernel then
+    // reads each shared block once per run of forks copying it
+    std::vector<std::pair<SeqState *, size_t>> sorted(targets);
+    std::stable_sort(sorted.begin(), sorted.end(), [](const auto &x, const auto &y) {
+        return x.first->handles[x.second].block_id < y.first->handles[y.second].block_id;
+    });
+    const auto &tg = sorted;
+    const size_t n = tg.size();
     std::vector<zk_block_handle> fresh(n);
     std::vector<int32_t> pairs(2 * n);
     for (size_t i = 0; i < n; ++i) {
-        SeqState &s = *targets[i].first;
+        SeqState &s = *tg[i].first;
         if (int rc = zk_bm_allocate(s.bm, &fresh[i])) {
             const zk::ErrorSnapshot saved = zk::save_error();
-            for (size_t j = 0; j < i; ++j) (void)zk_bm_free(targets[j].first->bm, fresh[j]);
+            for (size_t j = 0; j < i; ++j) (void)zk_bm_free(tg[j].first->bm, fresh[j]);
             return zk::restore_error(saved);
         }
-        pairs[i] = (int32_t)s.handles[targets[i].second].block_id;
+        pairs[i] = (int32_t)s.handles[tg[i].second].block_id;
         pairs[n + i] = (int32_t)fresh[i].block_id;
     }
     int rc = c->d_cow.ensure(pairs.size() * sizeof(int32_t), "KVCache cow scratch");
@@ -282,14 +289,14 @@ int cow_blocks(zk_kv_cache *c, const std::vector<std::pair<SeqState *, size_t>> 
     }
     if (rc) {
         const zk::ErrorSnapshot saved = zk::save_error();
-        for (size_t j = 0; j < n; ++j) (void)zk_bm_free(targets[j].first->bm, fresh[j]);
+        for (size_t j = 0; j < n; ++j) (void)zk_bm_free(tg[j].first->bm, fresh[j]);
         return zk::restore_error(saved);
     }
     int first_rc = ZK_OK;
     zk::ErrorSnapshot first_err;
     for (size_t i = 0; i < n; ++i) {
-        SeqState &s = *targets[i].first;
-        size_t idx = targets[i].second;
+        SeqState &s = *tg[i].first;
+        size_t idx = tg[i].second;
         int frc = zk_bm_free(s.bm, s.handles[idx]);
         if (frc && !first_rc) {
             first_rc = frc;
