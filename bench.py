@@ -707,10 +707,20 @@ def bench_model(args, torch, lib):
         if k_n:
             per[nm] = {"ms_per_step": k_ms * k_n / prof_steps, "launches_per_step": k_n / prof_steps}
     lib.zk_timing_reset()
+    from zealot_amd import dense
+    lw0 = w.layers[0]
+    proj = {}
+    for nm, t, od in (("qkv", lw0.qkv, None), ("o", lw0.o, None), ("gate_up", lw0.gate_up, None),
+                      ("down", lw0.down, None), ("lm_head", w.lm_head, torch.float32)):
+        try:
+            proj[nm] = dense.linear_choice(N, t.shape[0], t.shape[1], torch.bfloat16, od)
+        except Exception as e:  # no plan made for this shape
+            proj[nm] = str(e)
     wbytes = sum(t.numel() * 2 for lw in w.layers for t in (lw.qkv, lw.o, lw.gate_up, lw.down)) + w.lm_head.numel() * 2
     kvbytes = int(sum(int(c) for c in ctx)) * cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
     res = {"ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), "weight_bytes": wbytes, "kv_bytes": kvbytes,
            "gbps_weights_plus_kv": (wbytes + kvbytes) / (ms * 1e-3) / 1e9, "kernels": per,
+           "projections": proj,
            "shape": {"model": "Llama-3-8B shape (random bf16 weights)", "layers": cfg.num_layers, "seqs": N,
                      "ctx": [int(ctx.min()), int(ctx.max())]}}
     del model, w, cache

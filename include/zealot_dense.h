@@ -21,7 +21,8 @@ extern "C" {
  * `residual` is given, s = x + residual (the reference's add_kernel,
  * activation.cu:14-20, fused in) written to residual_out[i] (which may be
  * `residual` itself).  dim <= 32768 (bf16) / 16384 (f32) for 16-byte rows,
- * <= 4096 otherwise.  out / residual_out are packed [num_rows, dim]. */
+ * <= 4096 otherwise.  out / residual_out are packed [num_rows, dim]; out may
+ * be x when rows is NULL. */
 int zk_rms_norm(const void *x, const void *residual, const void *weight, void *out,
                 void *residual_out, const int64_t *rows, int64_t num_rows, int64_t dim, float eps,
                 zk_dtype dtype, void *stream);
@@ -65,6 +66,25 @@ int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64
  * zk_linear. */
 int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype out_dtype,
                      int tile_rows, int splits, void *stream);
+/* No counterpart in the reference (which launches its GEMM, add_kernel and
+ * rms_norm_kernel one after the other, cuda_runner.rs:483-529): the
+ * projection y = x . w^T (bf16, as zk_linear) followed by
+ * zk_rms_norm(y, residual, norm_weight, out, residual_out, NULL rows), bit for
+ * bit, with y itself not kept.  When zk_linear's tuning finds the
+ * weight-streaming kernel with split k as fast as its choice, to within the
+ * launch this saves, the norm kernel adds the split-k sums as it reads its
+ * rows (two launches instead of three); otherwise the projection writes `out`
+ * and the norm runs in place.  residual_out may be residual; dim n % 8 == 0
+ * and <= 32768 for the fused form. */
+int zk_linear_rms_norm(const void *x, const void *w, int64_t m, int64_t n, int64_t k, const void *residual,
+                       const void *norm_weight, float eps, void *out, void *residual_out, void *stream);
+/* No counterpart in the reference: what zk_linear's plan for (m, n, k,
+ * dtypes) on the current device runs, once a call has made it:
+ * choice = {splits, tile_rows, fused_splits, fused_rows}; splits 0 means
+ * hipBLASLt, else the weight-streaming kernel with that split of k and
+ * tile; fused_* is what zk_linear_rms_norm runs (fused_splits 0: the
+ * projection as zk_linear, then the norm). */
+int zk_linear_choice(int64_t m, int64_t n, int64_t k, zk_dtype in_dtype, zk_dtype out_dtype, int choice[4]);
 /* On (default): the first call of each (m, n, k, dtypes) times hipBLASLt's
  * candidate algorithms on its operands (synchronizing the stream once) and
  * keeps the fastest.  Off: the heuristic's first choice, no synchronization

@@ -6,7 +6,9 @@ Bars: add and embedding bit-exact (f32 sum / bf16 round of the f32 sum; rows
 copied); f32 rms_norm / silu_mul within 2e-6 relative (f32 rounding order);
 bf16 outputs within one bf16 rounding (2^-8 relative) of the f32 value of the
 same bf16 inputs; f32 linear within 1e-5 relative of the float64 product,
-bf16 linear within 1e-2 of the largest |y| (f32 accumulation, bf16 output)."""
+bf16 linear within 1e-2 of the largest |y| (f32 accumulation, bf16 output);
+zk_linear_rms_norm bit-exact against the unfused sequence through the same
+projection configuration."""
 import numpy as np
 import pytest
 import torch
@@ -259,3 +261,41 @@ def test_linear_on_more_streams_than_kept_workspaces():
     for y in outs:
         got = as_f32(to_host(y), oracle.BF16)
         assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("m,n,k,with_res", [(64, 4096, 14336, True), (64, 4096, 4096, True), (7, 4096, 4096, False),
+                                            (33, 1024, 2048, True), (200, 512, 1024, True)])
+def test_linear_rms_norm_is_the_unfused_sequence_bit_for_bit(m, n, k, with_res):
+    """zk_linear_rms_norm against the unfused sequence through the projection
+    configuration it ran (zk_linear_choice): the weight-streaming kernel with
+    split k whose sums the norm kernel adds, or zk_linear's own choice, then
+    zk_rms_norm; new residual and normed rows agree bit for bit."""
+    from zealot_amd import dense
+    rng = np.random.default_rng(m + n + k)
+    x = to_dev(normal(rng, (m, k), oracle.BF16))
+    w = to_dev(oracle.bf16_bits_from_f32((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)).reshape(n, k))
+    g = to_dev(normal(rng, (n,), oracle.BF16))
+    r0 = to_dev(normal(rng, (m, n), oracle.BF16)) if with_res else None
+    announce(f"linear_rms_norm {m}x{n}x{k} residual={with_res}")
+    res = r0.clone() if with_res else None
+    got = dense.linear_rms_norm(x, w, g, 1e-5, residual=res, residual_out=res)
+    out = got[0] if with_res else got
+    ch = dense.linear_choice(m, n, k)
+    if ch["fused_splits"] > 1:
+        y = dense.linear_skinny(x, w, ch["fused_splits"], ch["fused_rows"])
+    else:
+        y = dense.linear(x, w)
+    ref = dense.rms_norm(y, g, 1e-5, residual=r0.clone() if with_res else None)
+    ref_out = ref[0] if with_res else ref
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+    if with_res:
+        assert torch.equal(res.view(torch.int16), ref[1].view(torch.int16))
+    # and the float64 product of the same operands, through the oracle's norm
+    xs, ws = as_f32(to_host(x), oracle.BF16), as_f32(to_host(w), oracle.BF16)
+    yy = xs.astype(np.float64) @ ws.astype(np.float64).T
+    if with_res:
+        yy = yy + as_f32(to_host(r0), oracle.BF16)
+    want = oracle.rms_norm(yy.astype(np.float32), as_f32(to_host(g), oracle.BF16), 1e-5)
+    gotf = as_f32(to_host(out), oracle.BF16)
+    assert np.abs(gotf - want).max() <= 3e-2 * np.abs(want).max()

@@ -87,14 +87,21 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 // One workgroup per output row; each thread keeps its MAXV vectors of the
 // row in registers between the sum of squares and the scaled write.
 // in_row = rows ? rows[blockIdx.x] : blockIdx.x selects the input row;
-// residual (optional) is added first and the sum written to res_out.
-template <typename T, int VEC, int MAXV>
+// residual (optional) is added first and the sum written to res_out.  A
+// workgroup reads its whole row before the reduction and writes after it, so
+// out may be x (without row selection) and res_out may be residual.
+// PART: the input row is not read from x but is the projection output a
+// split-k skinny product leaves as f32 sums [splits][rows][dim] in `partial`:
+// x = T(sum over ranges, in range order), the value its reduce kernel would
+// have stored (VEC > 1 only).
+template <typename T, int VEC, int MAXV, bool PART = false>
 __global__ void __launch_bounds__(kThreads)
-rms_norm_kernel(const T *__restrict__ x, const T *residual, const T *__restrict__ w, T *__restrict__ out,
-                T *res_out, const int64_t *__restrict__ rows, int dim, float eps) {  // res_out may be residual
+rms_norm_kernel(const T *x, const T *residual, const T *__restrict__ w, T *out, T *res_out,
+                const int64_t *__restrict__ rows, int dim, float eps,  // out may be x, res_out residual
+                const float *__restrict__ partial = nullptr, int splits = 0) {
     __shared__ float red[kThreads / 64];
     const int64_t r_in = rows ? rows[blockIdx.x] : (int64_t)blockIdx.x;
-    const T *xr = x + (size_t)r_in * dim;
+    const T *xr = PART ? nullptr : x + (size_t)r_in * dim;
     const T *rr = residual ? residual + (size_t)r_in * dim : nullptr;
     float v[MAXV][VEC], wv[MAXV][VEC];
     float ss = 0.0f;
@@ -107,18 +114,32 @@ rms_norm_kernel(const T *__restrict__ x, const T *residual, const T *__restrict_
             if (VEC > 1) load_vec(w + i, wv[j]);
             else wv[j][0] = load1(w + i);
             if (VEC > 1) {
-                load_vec(xr + i, v[j]);
+                if constexpr (PART) {
+                    static_assert(VEC % 4 == 0, "f32x4 sums");
+                    const size_t plane = (size_t)gridDim.x * dim;
+                    const f32x4 *pp = reinterpret_cast<const f32x4 *>(partial + (size_t)r_in * dim + i);
+                    f32x4 a[VEC / 4];
+#pragma unroll
+                    for (int q = 0; q < VEC / 4; ++q) a[q] = pp[q];
+                    for (int r = 1; r < splits; ++r)
+#pragma unroll
+                        for (int q = 0; q < VEC / 4; ++q) a[q] += pp[r * plane / 4 + q];
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) v[j][e] = stored(a[e / 4][e % 4], (const T *)nullptr);
+                } else {
+                    load_vec(xr + i, v[j]);
+                }
                 if (rr) {
                     float a[VEC];
                     load_vec(rr + i, a);
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) v[j][e] = stored(v[j][e] + a[e], xr);
+                    for (int e = 0; e < VEC; ++e) v[j][e] = stored(v[j][e] + a[e], (const T *)nullptr);
                     store_vec(res_out + (size_t)blockIdx.x * dim + i, v[j]);
                 }
             } else {
                 v[j][0] = load1(xr + i);
                 if (rr) {
-                    v[j][0] = stored(v[j][0] + load1(rr + i), xr);
+                    v[j][0] = stored(v[j][0] + load1(rr + i), (const T *)nullptr);
                     store1(res_out + (size_t)blockIdx.x * dim + i, v[j][0]);
                 }
             }
@@ -250,7 +271,41 @@ int norm_dispatch(int rows_n, const void *x, const void *res, const void *w, voi
     return 0;
 }
 
+template <int MAXV>
+void launch_norm_partials(int rows_n, const float *partial, int splits, const void *res, const void *w, void *out,
+                          void *res_out, int dim, float eps, hipStream_t s) {
+    rms_norm_kernel<uint16_t, 8, MAXV, true><<<rows_n, kThreads, 0, s>>>(
+        nullptr, (const uint16_t *)res, (const uint16_t *)w, (uint16_t *)out, (uint16_t *)res_out, nullptr, dim, eps,
+        partial, splits);
+}
+
 }  // namespace
+
+namespace zk {
+
+bool rms_norm_partials_ok(int64_t rows, int64_t dim) {
+    return rows >= 1 && rows <= 0x7fffffff && dim >= 8 && dim % 8 == 0 && dim <= 32768;
+}
+
+int rms_norm_partials(const float *partial, int splits, const void *residual, const void *weight, void *out,
+                      void *residual_out, int64_t rows, int64_t dim, float eps, hipStream_t s) {
+    if (!rms_norm_partials_ok(rows, dim) || splits < 1 || !partial || !weight || !out ||
+        (residual && !residual_out))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: rms_norm over split-k sums: bad arguments");
+    if (!aligned16(partial) || !aligned16(weight) || !aligned16(out) || (residual && !aligned16(residual)) ||
+        (residual_out && !aligned16(residual_out)))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: rms_norm over split-k sums: not 16-byte aligned");
+    const int chunks = (int)((dim + kThreads * 8 - 1) / (kThreads * 8));
+    const int r = (int)rows, d = (int)dim;
+    if (chunks <= 1) launch_norm_partials<1>(r, partial, splits, residual, weight, out, residual_out, d, eps, s);
+    else if (chunks <= 2) launch_norm_partials<2>(r, partial, splits, residual, weight, out, residual_out, d, eps, s);
+    else if (chunks <= 4) launch_norm_partials<4>(r, partial, splits, residual, weight, out, residual_out, d, eps, s);
+    else if (chunks <= 8) launch_norm_partials<8>(r, partial, splits, residual, weight, out, residual_out, d, eps, s);
+    else launch_norm_partials<16>(r, partial, splits, residual, weight, out, residual_out, d, eps, s);
+    return check("rms_norm over split-k sums");
+}
+
+}  // namespace zk
 
 extern "C" {
 

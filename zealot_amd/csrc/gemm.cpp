@@ -35,6 +35,7 @@
 #include <utility>
 #include <vector>
 
+#include "../../include/zealot_dense.h"
 #include "zk_common.h"
 
 namespace {
@@ -47,6 +48,9 @@ constexpr double kWarmBudgetMs = 400.0;   // warm timing budget per shape
 constexpr size_t kSkinnyPartial = 32ull << 20;  // split-k sums of the skinny kernel
 const int kSkinnySplits[] = {1, 2, 4, 7, 8, 14, 16, 28};
 const int kSkinnyRows[] = {64, 128};
+// What folding a projection's split-k sum into the RMSNorm after it saves:
+// the reduce kernel's launch (about 4 us of a small kernel on the stream).
+constexpr float kFuseMarginMs = 0.004f;
 
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
@@ -55,6 +59,10 @@ struct Plan {
     size_t ws = 0;
     int splits = 0;                // > 0: the skinny kernel with this split of k
     int tile_rows = 0;             // and tiles of this many weight rows
+    // zk_linear_rms_norm: the skinny configuration with splits > 1 whose
+    // sums the norm kernel adds (fused_splits 0: none within kFuseMarginMs of
+    // the fastest)
+    int fused_splits = 0, fused_rows = 0;
 };
 
 // Workspaces of one stream: hipBLASLt's, and the skinny kernel's split-k
@@ -165,12 +173,13 @@ struct Cand {
     int tile_rows;
 };
 
-// Picks the candidate to keep (see the file comment) and the fastest
-// hipBLASLt one (best_blas, -1 if none ran).  The first n_always candidates
-// are always timed.  The output y is overwritten by every timed run and
-// finally by the real call.
+// Picks the candidate to keep (see the file comment), the fastest hipBLASLt
+// one (best_blas, -1 if none ran) and the fastest skinny one with splits > 1
+// if it is within kFuseMarginMs of the kept one (best_split, else -1).  The
+// first n_always candidates are always timed.  The output y is overwritten
+// by every timed run and finally by the real call.
 int pick_fastest(DeviceState &d, const Scratch &sc, Plan &p, const std::vector<Cand> &cands, const Problem &q,
-                 size_t n_always, hipStream_t stream, bool cold, int *best, int *best_blas) {
+                 size_t n_always, hipStream_t stream, bool cold, int *best, int *best_blas, int *best_split) {
     hipEvent_t e0, e1;
     ZK_HIP_CHECK(hipEventCreate(&e0), "zk_linear tuning");
     ZK_HIP_CHECK(hipEventCreate(&e1), "zk_linear tuning");
@@ -209,9 +218,15 @@ int pick_fastest(DeviceState &d, const Scratch &sc, Plan &p, const std::vector<C
     std::sort(warm.begin(), warm.end());
     *best = warm[0].second;
     *best_blas = -1;
+    *best_split = -1;
     for (auto &t : warm)
         if (!cands[t.second].splits) {
             *best_blas = t.second;
+            break;
+        }
+    for (auto &t : warm)
+        if (cands[t.second].splits > 1) {
+            if (t.first <= warm[0].first + kFuseMarginMs) *best_split = t.second;
             break;
         }
     // cold: flush the caches before each run of the finalists
@@ -227,7 +242,8 @@ int pick_fastest(DeviceState &d, const Scratch &sc, Plan &p, const std::vector<C
                 ++skinny_added;
                 if (i >= fin.size()) fin.push_back(warm[i]);
             }
-        float best_ms = 1e30f, blas_ms = 1e30f;
+        float best_ms = 1e30f, blas_ms = 1e30f, split_ms = 1e30f;
+        int split_at = -1;
         for (size_t f = 0; f < fin.size(); ++f) {
             float total = 0.0f;
             bool ok = true;
@@ -246,7 +262,13 @@ int pick_fastest(DeviceState &d, const Scratch &sc, Plan &p, const std::vector<C
                 blas_ms = total;
                 *best_blas = fin[f].second;
             }
+            if (ok && cands[fin[f].second].splits > 1 && total < split_ms) {
+                split_ms = total;
+                split_at = fin[f].second;
+            }
         }
+        // three runs each: the margin counts three times
+        *best_split = split_ms <= best_ms + 3 * kFuseMarginMs ? split_at : -1;
         (void)hipStreamSynchronize(stream);
         (void)hipFree(flush);
     }
@@ -290,7 +312,7 @@ int make_plan(DeviceState &d, Scratch &sc, int64_t m, int64_t n, int64_t k, zk_d
         if (heur[i].state == HIPBLAS_STATUS_SUCCESS && heur[i].workspaceSize <= kWorkspace)
             cands.push_back({heur[i].algo, heur[i].workspaceSize, 0, 0});
     if (cands.empty()) return fail("no hipBLASLt algorithm fits the workspace", HIPBLAS_STATUS_NOT_SUPPORTED);
-    int best = 0, best_blas = 0;
+    int best = 0, best_blas = 0, best_split = -1;
     const bool deep = m <= 256 && n * k >= (int64_t)1 << 22;
     const Problem q{x, w, y, m, n, k, out == ZK_F32};
     const bool aligned = (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0;
@@ -318,15 +340,38 @@ int make_plan(DeviceState &d, Scratch &sc, int64_t m, int64_t n, int64_t k, zk_d
         }
     }
     if (tune && cands.size() > 1)
-        if (int rc = pick_fastest(d, sc, p, cands, q, n_always, stream, deep, &best, &best_blas)) return rc;
+        if (int rc = pick_fastest(d, sc, p, cands, q, n_always, stream, deep, &best, &best_blas, &best_split))
+            return rc;
     if (best_blas < 0) best_blas = 0;  // candidate 0 is the heuristic's first
     p.splits = cands[best].splits;
     p.tile_rows = cands[best].tile_rows;
+    if (best_split >= 0) {
+        p.fused_splits = cands[best_split].splits;
+        p.fused_rows = cands[best_split].tile_rows;
+    }
     p.algo = cands[best_blas].algo;
     p.ws = cands[best_blas].ws;
     *res = &(d.plans[key] = p);
     return ZK_OK;
 }
+
+// Runs the plan's choice for y = x . w^T (the caller holds g_mu).
+int run_plan(DeviceState &d, Scratch *sc, const Plan *p, const void *x, const void *w, void *y, int64_t m, int64_t n,
+             int64_t k, zk_dtype out_dtype, hipStream_t stream) {
+    const float alpha = 1.0f, beta = 0.0f;
+    if (p->splits && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0) {
+        if (int rc = scratch_for(d, stream, p->splits > 1, &sc)) return rc;
+        zk::KernelTimer timer("linear", stream);
+        return run_skinny(*sc, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, p->tile_rows, p->splits, stream);
+    }
+    zk::KernelTimer timer("linear", stream);
+    hipblasStatus_t st = hipblasLtMatmul(d.handle, p->desc, &alpha, w, p->a, x, p->b, &beta, y, p->c, y, p->c,
+                                         &p->algo, sc->blas, p->ws, stream);
+    if (st != HIPBLAS_STATUS_SUCCESS) return fail("hipblasLtMatmul", st);
+    return ZK_OK;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
@@ -350,18 +395,44 @@ int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64
     Plan *p;
     if (int rc = make_plan(*d, *sc, m, n, k, in_dtype, out_dtype, x, w, y, (hipStream_t)stream, g_tune, &p))
         return rc;
-    const float alpha = 1.0f, beta = 0.0f;
-    if (p->splits && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0) {
-        if (int rc = scratch_for(*d, (hipStream_t)stream, p->splits > 1, &sc)) return rc;
-        zk::KernelTimer timer("linear", (hipStream_t)stream);
-        return run_skinny(*sc, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, p->tile_rows, p->splits,
-                          (hipStream_t)stream);
+    return run_plan(*d, sc, p, x, w, y, m, n, k, out_dtype, (hipStream_t)stream);
+}
+
+int zk_linear_rms_norm(const void *x, const void *w, int64_t m, int64_t n, int64_t k, const void *residual,
+                       const void *norm_weight, float eps, void *out, void *residual_out, void *stream) {
+    if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff)
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_rms_norm: bad shape");
+    if (m == 0) return ZK_OK;
+    if (!x || !w || !norm_weight || !out || (residual && !residual_out))
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_rms_norm: NULL pointer");
+    hipStream_t s = (hipStream_t)stream;
+    {
+        std::lock_guard<std::mutex> g(g_mu);
+        DeviceState *d;
+        if (int rc = device_state(&d)) return rc;
+        Scratch *sc;
+        if (int rc = scratch_for(*d, s, false, &sc)) return rc;
+        Plan *p;
+        if (int rc = make_plan(*d, *sc, m, n, k, ZK_BF16, ZK_BF16, x, w, out, s, g_tune, &p)) return rc;
+        const bool fuse = p->fused_splits > 1 && skinny_fits(m, n, k, p->fused_rows, p->fused_splits) &&
+                          zk::rms_norm_partials_ok(m, n) && aligned16(x) && aligned16(w) && aligned16(out) &&
+                          aligned16(norm_weight) && (!residual || (aligned16(residual) && aligned16(residual_out)));
+        if (fuse) {  // the skinny kernel's split-k sums go straight into the norm kernel
+            if (int rc = scratch_for(*d, s, true, &sc)) return rc;
+            {
+                zk::KernelTimer timer("linear", s);
+                if (int rc = zk::skinny_linear(x, w, nullptr, m, n, k, false, p->fused_rows, p->fused_splits,
+                                               sc->partial, kSkinnyPartial, s, /*reduce=*/false))
+                    return rc;
+            }
+            zk::KernelTimer timer("rms_norm", s);
+            return zk::rms_norm_partials((const float *)sc->partial, p->fused_splits, residual, norm_weight, out,
+                                         residual_out, m, n, eps, s);
+        }
+        if (int rc = run_plan(*d, sc, p, x, w, out, m, n, k, ZK_BF16, s)) return rc;
     }
-    zk::KernelTimer timer("linear", (hipStream_t)stream);
-    hipblasStatus_t st = hipblasLtMatmul(d->handle, p->desc, &alpha, w, p->a, x, p->b, &beta, y, p->c, y, p->c,
-                                         &p->algo, sc->blas, p->ws, (hipStream_t)stream);
-    if (st != HIPBLAS_STATUS_SUCCESS) return fail("hipblasLtMatmul", st);
-    return ZK_OK;
+    // the projection's output sits in `out`, which the norm overwrites in place
+    return zk_rms_norm(out, residual, norm_weight, out, residual_out, nullptr, m, n, eps, ZK_BF16, stream);
 }
 
 int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype out_dtype,
@@ -380,6 +451,21 @@ int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n
     if (int rc = scratch_for(*d, (hipStream_t)stream, splits > 1, &sc)) return rc;
     zk::KernelTimer timer("linear", (hipStream_t)stream);
     return run_skinny(*sc, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, tile_rows, splits, (hipStream_t)stream);
+}
+
+int zk_linear_choice(int64_t m, int64_t n, int64_t k, zk_dtype in_dtype, zk_dtype out_dtype, int choice[4]) {
+    if (!choice) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_choice: NULL pointer");
+    std::lock_guard<std::mutex> g(g_mu);
+    DeviceState *d;
+    if (int rc = device_state(&d)) return rc;
+    auto it = d->plans.find(std::make_tuple(m, n, k, (int)in_dtype, (int)out_dtype));
+    if (it == d->plans.end())
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_choice: no plan for this shape yet");
+    choice[0] = it->second.splits;
+    choice[1] = it->second.tile_rows;
+    choice[2] = it->second.fused_splits;
+    choice[3] = it->second.fused_rows;
+    return ZK_OK;
 }
 
 int zk_linear_tuning(int on) {

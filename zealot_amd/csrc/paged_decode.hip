@@ -104,6 +104,7 @@ struct Params {
     int32_t *work;        // total items at [0]; the head of queue j at [kQueueStride * (j + 1)] (MFMA path)
     int num_waves;        // persistent grid: wave w starts with item w
     int queues;           // work queues in use (1 or kQueues)
+    int reset_queues;     // the reduce kernel puts the queue heads back (MFMA path)
     float2 *ml;   // [N][H][MP] (m, l), log2 domain
     float *po;    // [N][H][MP][D]
     // Shared prefixes (MFMA bf16 path; all null when unused): sequence n's
@@ -810,14 +811,17 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     }
 }
 
-// A launch that reuses the previous launch's plan (the next layer of a step)
-// only needs the queue head back where the plan put it.  (Resetting it from
-// the decode kernel's last wave instead measured 20 % slower on the fp8
-// decode: every wave then waits for its own stores before it exits.)
-__global__ void __launch_bounds__(64) queue_reset_kernel(Params p) {
-    const int t = threadIdx.x;
+// Every MFMA launch ends with the queue heads back where the plan put them,
+// so the next launch on the same plan (the next layer of a step) starts
+// without a kernel of its own for that: the reduce kernel resets them (it
+// runs after the decode kernel has drained), or, when there is nothing to
+// reduce, queue_reset_kernel.  (Resetting them from the decode kernel's last
+// wave instead measured 20 % slower on the fp8 decode: every wave then waits
+// for its own stores before it exits.)
+__device__ __forceinline__ void reset_queue_heads(const Params &p, int t) {
     if (t < p.queues) p.work[kQueueStride * (t + 1)] = (p.num_waves - t + p.queues - 1) / p.queues;
 }
+__global__ void __launch_bounds__(64) queue_reset_kernel(Params p) { reset_queue_heads(p, threadIdx.x); }
 
 // ------------------------------------------------------------ generic kernel
 // One wavefront per (partition, kv-head, sequence).  Lane = token for QK
@@ -954,6 +958,7 @@ __global__ void __launch_bounds__(kWave) decode_generic_kernel(Params p) {
 // the partitions eight at a time so 16 loads per lane are in flight.
 __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
+    if (p.reset_queues && h == 0 && n == 0) reset_queue_heads(p, lane);
     const int ns = shared_parts_of(p, n);
     const int nparts = ns + private_parts_of(p, n);
     if (ns == 0 && nparts <= 1) return;  // written by the partition kernel
@@ -1006,6 +1011,7 @@ __global__ void __launch_bounds__(kWave) decode_reduce_vec_kernel(Params p) {
     constexpr int LP = D / 4, P = kWave / LP, U = 16;  // lanes per partition, partitions per load, loads per lane
     static_assert(D % 4 == 0 && kWave % LP == 0, "partition layout");
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
+    if (p.reset_queues && h == 0 && n == 0) reset_queue_heads(p, lane);
     const int ns = shared_parts_of(p, n);
     const int nparts = ns + private_parts_of(p, n);
     if (ns == 0 && nparts <= 1) return;  // written by the partition kernel
@@ -1260,7 +1266,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                          "Internal error: zk_paged_decode: workspace too small or not 256-B aligned (need " +
                              std::to_string(w.total) + " bytes)");
 
-    Params p;
+    Params p{};
     p.q = q;
     p.k_pool = (const char *)k_pool;
     p.v_pool = (const char *)v_pool;
@@ -1307,13 +1313,16 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
         }
         if (int rc = check_launch("zk_paged_decode seq_info")) return rc;
     }
+    const bool reduce = max_parts > 1 || shared;
     if (use_mfma) {
-        {
-            KernelTimer timer("decode_plan", s);
-            if (reuse_plan) queue_reset_kernel<<<1, 64, 0, s>>>(p);
-            else plan_kernel<<<1, 1024, 0, s>>>(p, num_seqs);
+        p.reset_queues = 1;
+        if (!reuse_plan) {  // a reused plan's queue heads were reset by the launch before
+            {
+                KernelTimer timer("decode_plan", s);
+                plan_kernel<<<1, 1024, 0, s>>>(p, num_seqs);
+            }
+            if (int rc = check_launch("zk_paged_decode plan")) return rc;
         }
-        if (int rc = check_launch("zk_paged_decode plan")) return rc;
         KernelTimer timer("decode_partials", s);
         const int grid = p.num_waves;
         if (kv_dtype == ZK_BF16) launch_mfma<ZK_BF16>(p, grid, s, G);
@@ -1326,7 +1335,14 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
         else decode_generic_kernel<ZK_FP8_E4M3><<<grid, kWave, 0, s>>>(p);
     }
     if (int rc = check_launch("zk_paged_decode partials")) return rc;
-    if (max_parts > 1 || shared) {
+    if (use_mfma && !reduce) {
+        {
+            KernelTimer timer("decode_plan", s);
+            queue_reset_kernel<<<1, 64, 0, s>>>(p);
+        }
+        if (int rc = check_launch("zk_paged_decode queue reset")) return rc;
+    }
+    if (reduce) {
         dim3 rgrid(num_heads, num_seqs);
         KernelTimer timer("decode_reduce", s);
         if (head_dim == 128) decode_reduce_vec_kernel<128><<<rgrid, kWave, 0, s>>>(p);

@@ -18,7 +18,9 @@
 //    flight), with one barrier per chunk;
 //  - splits == 1: the waves write y; splits > 1: each range's sums go to a
 //    workspace [splits][m][n] and skinny_reduce_kernel adds them in range
-//    order, so the result does not depend on scheduling.
+//    order, so the result does not depend on scheduling (or the RMSNorm
+//    that follows the product adds them as it reads its rows: reduce ==
+//    false, for zk_linear_rms_norm).
 // MFMA 16x16x32 bf16 operand layout: lane l holds A[l % 16][8 (l / 16) + j]
 // and B[8 (l / 16) + j][l % 16] for j < 8, and receives
 // D[4 (l / 16) + r][l % 16] for r < 4.  A = weight rows, B = x^T, so lane l
@@ -219,10 +221,10 @@ size_t skinny_linear_partial_bytes(int64_t m, int64_t n, int splits) {
 }
 
 int skinny_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, bool f32_out, int tile_rows,
-                  int splits, void *partial, size_t partial_bytes, hipStream_t stream) {
+                  int splits, void *partial, size_t partial_bytes, hipStream_t stream, bool reduce) {
     if (!skinny_linear_ok(m, n, k, tile_rows, splits))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_skinny: unsupported shape");
-    if (!x || !w || !y)
+    if (!x || !w || (!y && (reduce || splits == 1)))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_skinny: NULL pointer");
     if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_skinny: operands not 16-byte aligned");
@@ -235,7 +237,7 @@ int skinny_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, i
         launch_rf<1>(a, f32_out, stream);
     else
         launch_rf<2>(a, f32_out, stream);
-    if (splits > 1) {
+    if (splits > 1 && reduce) {
         const size_t quads = (size_t)m * n / 4;
         const uint32_t blocks = (uint32_t)((quads + kThreads - 1) / kThreads);
         if (f32_out)

@@ -103,7 +103,15 @@ int paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, cons
 bool skinny_linear_ok(int64_t m, int64_t n, int64_t k, int tile_rows, int splits);
 size_t skinny_linear_partial_bytes(int64_t m, int64_t n, int splits);
 int skinny_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, bool f32_out, int tile_rows,
-                  int splits, void *partial, size_t partial_bytes, hipStream_t stream);
+                  int splits, void *partial, size_t partial_bytes, hipStream_t stream, bool reduce = true);
+// RMSNorm (with the residual add, as zk_rms_norm) of the bf16 rows
+// y = bf16(sum over ranges of partial[range][row]) that skinny_linear with
+// splits > 1 and reduce == false leaves in `partial` ([splits][rows][dim]
+// f32): bit for bit the reduce kernel's y followed by zk_rms_norm.  bf16,
+// dim % 8 == 0 and <= 32768, 16-byte aligned.
+bool rms_norm_partials_ok(int64_t rows, int64_t dim);
+int rms_norm_partials(const float *partial, int splits, const void *residual, const void *weight, void *out,
+                      void *residual_out, int64_t rows, int64_t dim, float eps, hipStream_t s);
 size_t paged_decode_workspace(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq, int block_size,
                               bool shared);
 // Whether paged_decode runs shared-prefix items for this shape (otherwise pg

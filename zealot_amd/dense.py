@@ -79,6 +79,42 @@ def linear(x, weight, out=None, out_dtype=None, stream=None):
     return out
 
 
+def linear_rms_norm(x, weight, norm_weight, eps: float = 1e-6, residual=None, out=None, residual_out=None,
+                    stream=None):
+    """rms_norm(linear(x, weight), norm_weight, eps, residual, ...) bit for
+    bit, for bf16 in two launches instead of three when the projection runs on
+    the weight-streaming kernel with split k (its sums feed the norm
+    directly); f32 runs the two calls.  Returns out, or (out, residual_out)
+    with a residual."""
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or weight.dtype != x.dtype:
+        raise ValueError("weight must be [n, k] of x's dtype")
+    if x.dtype != torch.bfloat16:
+        return rms_norm(linear(x, weight), norm_weight, eps, residual=residual, out=out, residual_out=residual_out,
+                        stream=stream)
+    if out is None:
+        out = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    if residual is not None and residual_out is None:
+        residual_out = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().zk_linear_rms_norm(
+        _dev(x, "x"), _dev(weight, "weight"), m, n, k, None if residual is None else _dev(residual, "residual"),
+        _dev(norm_weight, "norm_weight"), float(eps), _dev(out, "out"),
+        None if residual_out is None else _dev(residual_out, "residual_out"), _stream(stream)))
+    return out if residual is None else (out, residual_out)
+
+
+def linear_choice(m, n, k, in_dtype=torch.bfloat16, out_dtype=None) -> dict:
+    """What the projection plan for this shape runs (after a first call made
+    it): splits 0 = hipBLASLt, else the weight-streaming kernel with that split
+    of k and tile_rows; fused_* is what linear_rms_norm runs."""
+    import ctypes
+    code = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+    c = (ctypes.c_int * 4)()
+    _lib.check(_lib.lib().zk_linear_choice(m, n, k, code[in_dtype], code[out_dtype or in_dtype], c))
+    return {"splits": c[0], "tile_rows": c[1], "fused_splits": c[2], "fused_rows": c[3]}
+
+
 def linear_skinny(x, weight, splits=1, tile_rows=128, out=None, out_dtype=None, stream=None):
     """The weight-streaming kernel zk_linear may choose for bf16 and m <= 64,
     called directly: tiles of tile_rows weight rows, k split in `splits`."""

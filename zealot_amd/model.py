@@ -14,8 +14,10 @@ reference).  What differs is the shape of the work:
     weight, gate/up from one against [2 I, hidden]; K and V are appended and
     q attended straight out of the fused output through row strides (no
     transpose kernels, no copies; cf. cuda_runner.rs:373-392);
-  - each residual add is fused into the RMSNorm that follows it, and the
-    final norm runs only over the last row of each sequence;
+  - each residual add is fused into the RMSNorm that follows it, and so,
+    for the o and down projections, is the projection's split-k sum when it
+    runs on the weight-streaming kernel (dense.linear_rms_norm); the final
+    norm runs only over the last row of each sequence;
   - weights are random-initialised here (there is no checkpoint loader in
     this build; the reference loads HF weights, model_loader.rs:241).
 """
@@ -114,23 +116,24 @@ class HipModelRunner:
         qd, kd = H * D, Hkv * D
         resid = dense.embedding(ids, w.embedding)  # the residual stream [T, hidden]
         normed = torch.empty_like(resid)
-        delta = None
+        dense.rms_norm(resid, w.layers[0].attn_norm, cfg.rms_eps, out=normed)
+        last = len(w.layers) - 1
         for layer, lw in enumerate(w.layers):
-            if delta is None:
-                dense.rms_norm(resid, lw.attn_norm, cfg.rms_eps, out=normed)
-            else:  # resid += delta; normed = norm(resid)
-                dense.rms_norm(delta, lw.attn_norm, cfg.rms_eps, residual=resid, out=normed, residual_out=resid)
             qkv = dense.linear(normed, lw.qkv)
             q = qkv[:, :qd].view(T, H, D)
             k = qkv[:, qd:qd + kd].view(T, Hkv, D)
             v = qkv[:, qd + kd:].view(T, Hkv, D)
             self.kv.write(layer, plan, k, v)
             attn = self.kv.attention(layer, plan, q)
-            o = dense.linear(attn.view(T, qd), lw.o)
-            dense.rms_norm(o, lw.ffn_norm, cfg.rms_eps, residual=resid, out=normed, residual_out=resid)
+            # resid += o_proj(attn); normed = norm(resid)
+            dense.linear_rms_norm(attn.view(T, qd), lw.o, lw.ffn_norm, cfg.rms_eps, residual=resid, out=normed,
+                                  residual_out=resid)
             gu = dense.linear(normed, lw.gate_up)
             act = dense.silu_mul(gu[:, :I], gu[:, I:])
-            delta = dense.linear(act, lw.down)
+            if layer < last:  # resid += down_proj(act); normed = the next layer's attention norm of resid
+                dense.linear_rms_norm(act, lw.down, w.layers[layer + 1].attn_norm, cfg.rms_eps, residual=resid,
+                                      out=normed, residual_out=resid)
+        delta = dense.linear(act, w.layers[last].down)
         final, _ = dense.rms_norm(delta, w.final_norm, cfg.rms_eps, residual=resid, rows=last_rows)
         return dense.linear(final, w.lm_head, out_dtype=torch.float32)
 
