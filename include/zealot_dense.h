@@ -78,6 +78,19 @@ int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n
  * and <= 32768 for the fused form. */
 int zk_linear_rms_norm(const void *x, const void *w, int64_t m, int64_t n, int64_t k, const void *residual,
                        const void *norm_weight, float eps, void *out, void *residual_out, void *stream);
+/* No counterpart in the reference (which launches gate and up sgemms and
+ * silu_gate_mul_kernel, cuda_runner.rs:531-571): act[m, inter] = silu(gate) *
+ * up for x[m, k] (bf16) against w[2 inter, k] whose rows hold gate and up
+ * interleaved in blocks of 16 -- rows 32 b .. 32 b + 15 are gate rows
+ * 16 b .. 16 b + 15, the next 16 the up rows of the same columns -- bit for
+ * bit zk_linear(x, w) followed by SiLU * up of the rounded outputs.  When
+ * zk_linear's tuning keeps the weight-streaming kernel with 128-row tiles and
+ * no split for (m, 2 inter, k), that kernel's waves hold the gate and up
+ * outputs of the same columns and write act directly (one launch); otherwise
+ * the projection goes to gu [m, 2 inter] (bf16, always required: the tuning
+ * also writes there) and a second kernel forms act.  inter % 16 == 0. */
+int zk_linear_silu_mul(const void *x, const void *w, void *act, int64_t m, int64_t inter, int64_t k, void *gu,
+                       void *stream);
 /* No counterpart in the reference: what zk_linear's plan for (m, n, k,
  * dtypes) on the current device runs, once a call has made it:
  * choice = {splits, tile_rows, fused_splits, fused_rows}; splits 0 means

@@ -22,7 +22,8 @@ from . import BF16, F32, GROUPED, add, embedding, f32_from_bf16_bits, linear, pa
 
 class LlamaRef:
     """weights: dict of float32 numpy arrays with the fused layouts of
-    zealot_amd.model.LlamaWeights (qkv [(H+2Hkv)D, hid], gate_up [2I, hid])."""
+    zealot_amd.model.LlamaWeights (qkv [(H+2Hkv)D, hid], gate_up [2I, hid] with
+    gate and up rows interleaved in blocks of 16)."""
 
     def __init__(self, cfg, weights):
         self.cfg = cfg
@@ -73,8 +74,10 @@ class LlamaRef:
                 attn = self._attend(rid, layer, q.reshape(n, H, D), before).reshape(n, qd)
                 h = add(linear(attn, lw["o"]), h)
                 normed = rms_norm(h, lw["ffn_norm"], cfg.rms_eps)
-                gate = linear(normed, lw["gate_up"][:I])
-                up = linear(normed, lw["gate_up"][I:])
+                # gate_up rows: gate and up interleaved in blocks of 16
+                gu_w = lw["gate_up"].reshape(I // 16, 2, 16, -1)
+                gate = linear(normed, np.ascontiguousarray(gu_w[:, 0].reshape(I, -1)))
+                up = linear(normed, np.ascontiguousarray(gu_w[:, 1].reshape(I, -1)))
                 h = add(linear(silu_gate_mul(gate, up), lw["down"]), h)
             final = rms_norm(h[-1:], w["final_norm"], cfg.rms_eps)
             logits.append(linear(final, w["lm_head"])[0])

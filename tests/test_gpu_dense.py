@@ -299,3 +299,30 @@ def test_linear_rms_norm_is_the_unfused_sequence_bit_for_bit(m, n, k, with_res):
     want = oracle.rms_norm(yy.astype(np.float32), as_f32(to_host(g), oracle.BF16), 1e-5)
     gotf = as_f32(to_host(out), oracle.BF16)
     assert np.abs(gotf - want).max() <= 3e-2 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("m,inter,k", [(64, 14336, 4096), (7, 1024, 512), (33, 512, 256), (200, 512, 1024)])
+def test_linear_silu_mul_is_the_unfused_sequence_bit_for_bit(m, inter, k):
+    """zk_linear_silu_mul (gate and up rows interleaved in blocks of 16)
+    against zk_linear on the same weight followed by SiLU * up of the rounded
+    gate / up columns: bit for bit whether the projection's own waves formed
+    the product (weight-streaming kernel, 128-row tiles, no split) or a second
+    kernel did; and close to the float64 product."""
+    from zealot_amd import dense
+    rng = np.random.default_rng(m + inter + k)
+    x = to_dev(normal(rng, (m, k), oracle.BF16))
+    gate = oracle.bf16_bits_from_f32((rng.standard_normal((inter, k)) / np.sqrt(k)).astype(np.float32)).reshape(inter, k)
+    up = oracle.bf16_bits_from_f32((rng.standard_normal((inter, k)) / np.sqrt(k)).astype(np.float32)).reshape(inter, k)
+    w = dense.interleave_gate_up(to_dev(gate), to_dev(up))
+    announce(f"linear_silu_mul {m}x{inter}x{k}")
+    act = dense.linear_silu_mul(x, w)
+    y = dense.linear(x, w).view(m, inter // 16, 2, 16)
+    ref = dense.silu_mul(y[:, :, 0].reshape(m, inter), y[:, :, 1].reshape(m, inter))
+    torch.cuda.synchronize()
+    assert torch.equal(act.view(torch.int16), ref.view(torch.int16)), dense.linear_choice(m, 2 * inter, k)
+    xs = as_f32(to_host(x), oracle.BF16).astype(np.float64)
+    g64 = xs @ as_f32(gate, oracle.BF16).astype(np.float64).T
+    u64 = xs @ as_f32(up, oracle.BF16).astype(np.float64).T
+    want = g64 / (1 + np.exp(-g64)) * u64
+    got = as_f32(to_host(act), oracle.BF16)
+    assert np.abs(got - want).max() <= 3e-2 * np.abs(want).max()

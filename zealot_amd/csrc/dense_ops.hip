@@ -163,7 +163,10 @@ rms_norm_kernel(const T *x, const T *residual, const T *__restrict__ w, T *out, 
 }
 
 // ---------------------------------------------------------- SiLU * up, add
-template <typename T, int VEC>
+// BLOCKED: gate and up are the column blocks of one projection output whose
+// gate / up columns alternate in blocks of 16: output column c reads gate
+// column 32 (c / 16) + c % 16 and up column 16 after it (VEC divides 16).
+template <typename T, int VEC, bool BLOCKED = false>
 __global__ void __launch_bounds__(kThreads)
 silu_mul_kernel(const T *__restrict__ gate, const T *__restrict__ up, T *__restrict__ out, int64_t rows, int cols,
                 int64_t gate_stride, int64_t up_stride) {
@@ -173,13 +176,14 @@ silu_mul_kernel(const T *__restrict__ gate, const T *__restrict__ up, T *__restr
          idx += (int64_t)gridDim.x * kThreads) {
         const int64_t r = idx / per_row;
         const int c = (int)(idx - r * per_row) * VEC;
+        const int gc = BLOCKED ? (c / 16) * 32 + c % 16 : c, uc = BLOCKED ? gc + 16 : c;
         float g[VEC], u[VEC], o[VEC];
         if (VEC > 1) {
-            load_vec(gate + r * gate_stride + c, g);
-            load_vec(up + r * up_stride + c, u);
+            load_vec(gate + r * gate_stride + gc, g);
+            load_vec(up + r * up_stride + uc, u);
         } else {
-            g[0] = load1(gate + r * gate_stride + c);
-            u[0] = load1(up + r * up_stride + c);
+            g[0] = load1(gate + r * gate_stride + gc);
+            u[0] = load1(up + r * up_stride + uc);
         }
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o[e] = (g[e] / (1.0f + expf(-g[e]))) * u[e];
@@ -282,6 +286,20 @@ void launch_norm_partials(int rows_n, const float *partial, int splits, const vo
 }  // namespace
 
 namespace zk {
+
+int silu_mul_blocked(const void *gu, void *act, int64_t rows, int64_t inter, hipStream_t s) {
+    if (rows < 0 || inter <= 0 || inter % 16 || !gu || !act)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: blocked silu_mul: bad arguments");
+    if (rows == 0) return ZK_OK;
+    const int grid_v = grid_for(rows * inter / 8), grid_1 = grid_for(rows * inter);
+    if (aligned16(gu) && aligned16(act))
+        silu_mul_kernel<uint16_t, 8, true><<<grid_v, kThreads, 0, s>>>(
+            (const uint16_t *)gu, (const uint16_t *)gu, (uint16_t *)act, rows, (int)inter, 2 * inter, 2 * inter);
+    else
+        silu_mul_kernel<uint16_t, 1, true><<<grid_1, kThreads, 0, s>>>(
+            (const uint16_t *)gu, (const uint16_t *)gu, (uint16_t *)act, rows, (int)inter, 2 * inter, 2 * inter);
+    return check("blocked silu_mul");
+}
 
 bool rms_norm_partials_ok(int64_t rows, int64_t dim) {
     return rows >= 1 && rows <= 0x7fffffff && dim >= 8 && dim % 8 == 0 && dim <= 32768;

@@ -453,6 +453,35 @@ int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n
     return run_skinny(*sc, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, tile_rows, splits, (hipStream_t)stream);
 }
 
+int zk_linear_silu_mul(const void *x, const void *w, void *act, int64_t m, int64_t inter, int64_t k, void *gu,
+                       void *stream) {
+    if (m < 0 || inter <= 0 || inter % 16 || k <= 0 || m > 0x7fffffff || 2 * inter > 0x7fffffff || k > 0x7fffffff)
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT,
+                             "Internal error: zk_linear_silu_mul: bad shape (inter must be a multiple of 16)");
+    if (m == 0) return ZK_OK;
+    if (!x || !w || !act || !gu)
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_silu_mul: NULL pointer");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t n = 2 * inter;
+    {
+        std::lock_guard<std::mutex> g(g_mu);
+        DeviceState *d;
+        if (int rc = device_state(&d)) return rc;
+        Scratch *sc;
+        if (int rc = scratch_for(*d, s, false, &sc)) return rc;
+        Plan *p;
+        if (int rc = make_plan(*d, *sc, m, n, k, ZK_BF16, ZK_BF16, x, w, gu, s, g_tune, &p)) return rc;
+        if (p->splits == 1 && p->tile_rows == 128 && aligned16(x) && aligned16(w) && aligned16(act)) {
+            // each wave holds the gate and up outputs of the same columns: SiLU * up in its epilogue
+            zk::KernelTimer timer("linear", s);
+            return zk::skinny_linear_silu(x, w, act, m, n, k, s);
+        }
+        if (int rc = run_plan(*d, sc, p, x, w, gu, m, n, k, ZK_BF16, s)) return rc;
+    }
+    zk::KernelTimer timer("silu_mul", s);
+    return zk::silu_mul_blocked(gu, act, m, inter, s);
+}
+
 int zk_linear_choice(int64_t m, int64_t n, int64_t k, zk_dtype in_dtype, zk_dtype out_dtype, int choice[4]) {
     if (!choice) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_choice: NULL pointer");
     std::lock_guard<std::mutex> g(g_mu);

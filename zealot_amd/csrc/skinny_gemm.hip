@@ -79,7 +79,13 @@ __device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "mem
 constexpr int ring_depth(int mt, int rf) { return 4 * (64 * rf + 16 * mt) * 256 <= 163840 ? 4 : 3; }
 
 // MT: 16-row tiles of x (ceil(m / 16)); RF: 16-row weight tiles per wave.
-template <int MT, int RF, bool F32>
+// SILU (RF = 2, no split, bf16 out): W holds gate and up rows interleaved in
+// blocks of 16 (rows 32 b .. 32 b + 15 gate rows 16 b .., the next 16 the up
+// rows of the same columns), so a wave's two tiles are the gate and up
+// outputs of 16 columns, lane by lane; the wave writes
+// y[m, n / 2] = silu(gate) * up instead of both (the value silu_mul_kernel
+// computes from the rounded projection).
+template <int MT, int RF, bool F32, bool SILU = false>
 __global__ void __launch_bounds__(kThreads) skinny_linear_kernel(SkinnyArgs a) {
     constexpr int D = ring_depth(MT, RF);
     constexpr int WU = 16 * RF * 16;         // 16-byte units of a wave's weight chunk
@@ -164,6 +170,26 @@ __global__ void __launch_bounds__(kThreads) skinny_linear_kernel(SkinnyArgs a) {
     }
 
     // lane: column t * 16 + r16, rows row0 + 16 f + 4 g .. + 3
+    if constexpr (SILU) {
+        static_assert(RF == 2 && !F32, "gate and up tiles of one wave, bf16 out");
+        const int inter = a.n / 2, c0 = (row0 / 32) * 16 + 4 * g;
+        auto rounded = [](float x) { return __uint_as_float(zk::f32_to_bf16_bits(x) << 16); };
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int col = t * 16 + r16;
+            if (col < a.m) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float gt = rounded(acc[0][t][e]), up = rounded(acc[1][t][e]);
+                    v[e] = (gt / (1.0f + expf(-gt))) * up;
+                }
+                const zk::u32x2 o = {zk::pack_bf16x2(v[0], v[1]), zk::pack_bf16x2(v[2], v[3])};
+                *reinterpret_cast<zk::u32x2 *>((uint16_t *)a.y + (size_t)col * inter + c0) = o;
+            }
+        }
+        return;
+    }
     void *out = a.splits == 1 ? a.y : (void *)(a.partial + (size_t)s * a.m * a.n);
     const bool f32 = F32 || a.splits > 1;
 #pragma unroll
@@ -206,9 +232,34 @@ void launch_rf(const SkinnyArgs &a, bool f32, hipStream_t stream) {
     }
 }
 
+template <int MT>
+void launch_silu(const SkinnyArgs &a, hipStream_t stream) {
+    skinny_linear_kernel<MT, 2, false, true><<<(uint32_t)(a.n / 128), kThreads, 0, stream>>>(a);
+}
+
 }  // namespace
 
 namespace zk {
+
+int skinny_linear_silu(const void *x, const void *w, void *act, int64_t m, int64_t n, int64_t k, hipStream_t stream) {
+    if (!skinny_linear_ok(m, n, k, 128, 1))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_silu_mul: unsupported shape");
+    if (!x || !w || !act)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_silu_mul: NULL pointer");
+    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)act) & 15)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_silu_mul: operands not 16-byte aligned");
+    SkinnyArgs a{(const uint16_t *)x, (const uint16_t *)w, act, nullptr, (int)m, (int)n, (int)k, (int)k, 1};
+    switch ((m + 15) / 16) {
+        case 1: launch_silu<1>(a, stream); break;
+        case 2: launch_silu<2>(a, stream); break;
+        case 3: launch_silu<3>(a, stream); break;
+        default: launch_silu<4>(a, stream); break;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(ZK_ERR_HIP, std::string("Internal error: zk_linear_silu_mul: ") + hipGetErrorString(e));
+    return ZK_OK;
+}
 
 bool skinny_linear_ok(int64_t m, int64_t n, int64_t k, int tile_rows, int splits) {
     return m >= 1 && m <= 64 && (tile_rows == 64 || tile_rows == 128) && n >= tile_rows && n % tile_rows == 0 &&

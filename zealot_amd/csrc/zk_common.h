@@ -104,6 +104,14 @@ bool skinny_linear_ok(int64_t m, int64_t n, int64_t k, int tile_rows, int splits
 size_t skinny_linear_partial_bytes(int64_t m, int64_t n, int splits);
 int skinny_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, bool f32_out, int tile_rows,
                   int splits, void *partial, size_t partial_bytes, hipStream_t stream, bool reduce = true);
+// y = x . w^T with w's rows gate / up interleaved in blocks of 16 (n = 2 I),
+// written as act[m, I] = silu(gate) * up of the bf16-rounded outputs: the
+// skinny kernel with 128-row tiles and no split, m <= 64, bf16.
+int skinny_linear_silu(const void *x, const void *w, void *act, int64_t m, int64_t n, int64_t k, hipStream_t stream);
+// act[r, c] = silu(gu[r, g(c)]) * gu[r, g(c) + 16], g(c) = 32 (c / 16) + c % 16:
+// SiLU * up over a [rows, 2 inter] projection output whose gate / up columns
+// are interleaved in blocks of 16 (bf16, inter % 16 == 0).
+int silu_mul_blocked(const void *gu, void *act, int64_t rows, int64_t inter, hipStream_t s);
 // RMSNorm (with the residual add, as zk_rms_norm) of the bf16 rows
 // y = bf16(sum over ranges of partial[range][row]) that skinny_linear with
 // splits > 1 and reduce == false leaves in `partial` ([splits][rows][dim]

@@ -104,6 +104,48 @@ def linear_rms_norm(x, weight, norm_weight, eps: float = 1e-6, residual=None, ou
     return out if residual is None else (out, residual_out)
 
 
+GATE_UP_BLOCK = 16  # rows of gate (then of up) per block of a fused gate|up weight
+
+
+def interleave_gate_up(gate, up):
+    """The fused [2 I, hidden] gate|up weight for linear_silu_mul: gate and up
+    rows interleaved in blocks of GATE_UP_BLOCK."""
+    i, hid = gate.shape
+    if up.shape != gate.shape or i % GATE_UP_BLOCK:
+        raise ValueError("gate and up must be [I, hidden] with I a multiple of 16")
+    b = GATE_UP_BLOCK
+    return torch.stack([gate.reshape(i // b, b, hid), up.reshape(i // b, b, hid)], 1).reshape(2 * i, hid).contiguous()
+
+
+def split_gate_up(gate_up):
+    """(gate, up) of a weight from interleave_gate_up."""
+    n, hid = gate_up.shape
+    b = GATE_UP_BLOCK
+    v = gate_up.reshape(n // (2 * b), 2, b, hid)
+    return v[:, 0].reshape(n // 2, hid), v[:, 1].reshape(n // 2, hid)
+
+
+def linear_silu_mul(x, gate_up, out=None, gu=None, stream=None):
+    """silu(x . gate^T) * (x . up^T) for a gate|up weight from
+    interleave_gate_up, bit for bit linear() followed by SiLU * up of its
+    rounded outputs; for bf16 one launch when the projection runs on the
+    weight-streaming kernel without split."""
+    m, k = x.shape
+    n = gate_up.shape[0]
+    if gate_up.shape[1] != k or gate_up.dtype != x.dtype or n % (2 * GATE_UP_BLOCK):
+        raise ValueError("gate_up must be [2 I, k] of x's dtype, I a multiple of 16")
+    if x.dtype != torch.bfloat16:  # f32: the projection, then SiLU * up of its column blocks
+        y = linear(x, gate_up).view(m, n // (2 * GATE_UP_BLOCK), 2, GATE_UP_BLOCK)
+        return silu_mul(y[:, :, 0].reshape(m, n // 2), y[:, :, 1].reshape(m, n // 2), out=out, stream=stream)
+    if out is None:
+        out = torch.empty((m, n // 2), dtype=x.dtype, device=x.device)
+    if gu is None:
+        gu = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().zk_linear_silu_mul(_dev(x, "x"), _dev(gate_up, "gate_up"), _dev(out, "out"), m, n // 2, k,
+                                             _dev(gu, "gu"), _stream(stream)))
+    return out
+
+
 def linear_choice(m, n, k, in_dtype=torch.bfloat16, out_dtype=None) -> dict:
     """What the projection plan for this shape runs (after a first call made
     it): splits 0 = hipBLASLt, else the weight-streaming kernel with that split

@@ -11,7 +11,10 @@ reference).  What differs is the shape of the work:
   - one launch per op for all sequences of the batch (the reference loops
     over sequences, cuda_runner.rs:274);
   - q/k/v come from ONE projection against a fused [(H + 2 Hkv) D, hidden]
-    weight, gate/up from one against [2 I, hidden]; K and V are appended and
+    weight, gate/up from one against [2 I, hidden] whose gate and up rows
+    alternate in blocks of 16, so the projection's waves hold the gate and
+    up outputs of the same columns and write SiLU(gate) * up themselves
+    (dense.linear_silu_mul); K and V are appended and
     q attended straight out of the fused output through row strides (no
     transpose kernels, no copies; cf. cuda_runner.rs:373-392);
   - each residual add is fused into the RMSNorm that follows it, and so,
@@ -54,7 +57,7 @@ class LayerWeights:
     qkv: torch.Tensor        # [(H + 2 Hkv) D, hidden]: q rows, then k, then v
     o: torch.Tensor          # [hidden, H D]
     ffn_norm: torch.Tensor   # [hidden]
-    gate_up: torch.Tensor    # [2 I, hidden]: gate rows, then up
+    gate_up: torch.Tensor    # [2 I, hidden]: gate and up rows interleaved in blocks of 16 (dense.interleave_gate_up)
     down: torch.Tensor       # [hidden, I]
 
 
@@ -78,7 +81,8 @@ class LlamaWeights:
 
         H, Hkv, D, hid, I = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden_size, cfg.intermediate_size
         layers = [LayerWeights(norm(hid), lin((H + 2 * Hkv) * D, hid), lin(hid, H * D), norm(hid),
-                               lin(2 * I, hid), lin(hid, I)) for _ in range(cfg.num_layers)]
+                               dense.interleave_gate_up(lin(I, hid), lin(I, hid)), lin(hid, I))
+                  for _ in range(cfg.num_layers)]
         emb = torch.randn((cfg.vocab_size, hid), generator=g, device=device).to(dtype)
         return LlamaWeights(emb, layers, norm(hid), lin(cfg.vocab_size, hid))
 
@@ -109,7 +113,7 @@ class HipModelRunner:
 
     def forward(self, plan: StepPlan, ids: torch.Tensor, last_rows: torch.Tensor) -> torch.Tensor:
         cfg, w = self.cfg, self.w
-        H, Hkv, D, I = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.intermediate_size
+        H, Hkv, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
         T = plan.total_tokens
         if ids.numel() != T:
             raise ValueError("one token id per step row")
@@ -128,8 +132,7 @@ class HipModelRunner:
             # resid += o_proj(attn); normed = norm(resid)
             dense.linear_rms_norm(attn.view(T, qd), lw.o, lw.ffn_norm, cfg.rms_eps, residual=resid, out=normed,
                                   residual_out=resid)
-            gu = dense.linear(normed, lw.gate_up)
-            act = dense.silu_mul(gu[:, :I], gu[:, I:])
+            act = dense.linear_silu_mul(normed, lw.gate_up)
             if layer < last:  # resid += down_proj(act); normed = the next layer's attention norm of resid
                 dense.linear_rms_norm(act, lw.down, w.layers[layer + 1].attn_norm, cfg.rms_eps, residual=resid,
                                       out=normed, residual_out=resid)
