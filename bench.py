@@ -712,8 +712,13 @@ def bench_model(args, torch, lib):
     proj = {}
     for nm, t, od in (("qkv", lw0.qkv, None), ("o", lw0.o, None), ("gate_up", lw0.gate_up, None),
                       ("down", lw0.down, None), ("lm_head", w.lm_head, torch.float32)):
+        tiled = isinstance(t, dense.TiledWeight)
+        if nm == "gate_up" and tiled:  # no plan: always the one-launch SiLU kernel
+            proj[nm] = {"tiled": True, "splits": 1, "tile_rows": 128, "silu_epilogue": True}
+            continue
         try:
-            proj[nm] = dense.linear_choice(N, t.shape[0], t.shape[1], torch.bfloat16, od)
+            proj[nm] = dict(dense.linear_choice(N, t.shape[0], t.shape[1], torch.bfloat16, od, tiled=tiled),
+                            tiled=tiled)
         except Exception as e:  # no plan made for this shape
             proj[nm] = str(e)
     wbytes = sum(t.numel() * 2 for lw in w.layers for t in (lw.qkv, lw.o, lw.gate_up, lw.down)) + w.lm_head.numel() * 2

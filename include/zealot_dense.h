@@ -98,6 +98,41 @@ int zk_linear_silu_mul(const void *x, const void *w, void *act, int64_t m, int64
  * tile; fused_* is what zk_linear_rms_norm runs (fused_splits 0: the
  * projection as zk_linear, then the norm). */
 int zk_linear_choice(int64_t m, int64_t n, int64_t k, zk_dtype in_dtype, zk_dtype out_dtype, int choice[4]);
+
+/* Tiled weights.  No counterpart in the reference, whose weights stay in
+ * nn.Linear layout for cuBLAS (model_loader.rs:241, cuda_runner.rs:331-639):
+ * the layout the weight-streaming kernel reads with contiguous 1 KiB loads,
+ * [k / 128][n / 16][16 rows][16 units of 8 bf16], unit u of row r holding
+ * columns 8 (u ^ r) .. 8 (u ^ r) + 7 of its 128-column chunk.  A model
+ * converts its large decode-time weights once at load; the products below
+ * read them 17-19 % faster than row-major weights on the Llama-3-8B
+ * gate|up and lm_head shapes, bit for bit the same results as the
+ * weight-streaming kernel on the row-major weights (same configuration).
+ * The tiled products run on that kernel only (no hipBLASLt), for any m: up
+ * to 64 rows of x per pass over the weights, so they suit decode-sized m.
+ * All operands 16-byte aligned. */
+/* wt = row-major bf16 w [n, k] tiled; n % 16 == 0, k % 128 == 0, w and wt
+ * must not overlap. */
+int zk_weight_tile(const void *w, void *wt, int64_t n, int64_t k, void *stream);
+/* zk_linear for bf16 x and tiled weights (y bf16 or f32): the fastest
+ * configuration of the weight-streaming kernel (tile rows, split of k) is
+ * timed on first use of (m, n, k, out_dtype) as zk_linear times its
+ * candidates.  Needs n % 64 == 0 and k % 128 == 0. */
+int zk_linear_tiled(const void *x, const void *wt, void *y, int64_t m, int64_t n, int64_t k, zk_dtype out_dtype,
+                    void *stream);
+/* zk_linear_rms_norm (same arguments, bf16) for tiled weights. */
+int zk_linear_rms_norm_tiled(const void *x, const void *wt, int64_t m, int64_t n, int64_t k, const void *residual,
+                             const void *norm_weight, float eps, void *out, void *residual_out, void *stream);
+/* zk_linear_silu_mul for the tiled form of the interleaved gate|up weight
+ * [2 inter, k]: always one launch (the kernel's 128-row tiles hold gate and
+ * up of the same columns), so no projection buffer; inter % 64 == 0. */
+int zk_linear_silu_mul_tiled(const void *x, const void *wt, void *act, int64_t m, int64_t inter, int64_t k,
+                             void *stream);
+/* zk_linear_choice for the plan zk_linear_tiled / zk_linear_rms_norm_tiled
+ * made for (m, n, k, out_dtype): {splits, tile_rows, fused_splits,
+ * fused_rows}. */
+int zk_linear_tiled_choice(int64_t m, int64_t n, int64_t k, zk_dtype out_dtype, int choice[4]);
+
 /* On (default): the first call of each (m, n, k, dtypes) times hipBLASLt's
  * candidate algorithms on its operands (synchronizing the stream once) and
  * keeps the fastest.  Off: the heuristic's first choice, no synchronization

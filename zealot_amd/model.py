@@ -21,6 +21,9 @@ reference).  What differs is the shape of the work:
     for the o and down projections, is the projection's split-k sum when it
     runs on the weight-streaming kernel (dense.linear_rms_norm); the final
     norm runs only over the last row of each sequence;
+  - the large decode-time weights (gate|up, down, lm_head) are kept tiled
+    (dense.TiledWeight): the weight-streaming kernel reads them with
+    contiguous 1 KiB loads;
   - weights are random-initialised here (there is no checkpoint loader in
     this build; the reference loads HF weights, model_loader.rs:241).
 """
@@ -57,8 +60,9 @@ class LayerWeights:
     qkv: torch.Tensor        # [(H + 2 Hkv) D, hidden]: q rows, then k, then v
     o: torch.Tensor          # [hidden, H D]
     ffn_norm: torch.Tensor   # [hidden]
-    gate_up: torch.Tensor    # [2 I, hidden]: gate and up rows interleaved in blocks of 16 (dense.interleave_gate_up)
-    down: torch.Tensor       # [hidden, I]
+    gate_up: object          # [2 I, hidden]: gate and up rows interleaved in blocks of 16 (dense.interleave_gate_up);
+                             # a dense.TiledWeight of it for bf16 models
+    down: object             # [hidden, I] (a dense.TiledWeight for bf16 models)
 
 
 @dataclass
@@ -66,12 +70,15 @@ class LlamaWeights:
     embedding: torch.Tensor  # [vocab, hidden]
     layers: list
     final_norm: torch.Tensor  # [hidden]
-    lm_head: torch.Tensor     # [vocab, hidden]
+    lm_head: object           # [vocab, hidden] (a dense.TiledWeight for bf16 models)
 
     @staticmethod
-    def random(cfg: LlamaConfig, dtype=torch.bfloat16, device="cuda", seed: int = 0) -> "LlamaWeights":
-        """N(0, 1/fan_in) projections and N(1, 0.1) norm weights (seeded)."""
+    def random(cfg: LlamaConfig, dtype=torch.bfloat16, device="cuda", seed: int = 0,
+               tiled: bool = True) -> "LlamaWeights":
+        """N(0, 1/fan_in) projections and N(1, 0.1) norm weights (seeded);
+        with tiled (bf16 only) gate|up, down and lm_head as dense.TiledWeight."""
         g = torch.Generator(device=device).manual_seed(seed)
+        tile = dense.tile_weight if tiled and dtype == torch.bfloat16 else (lambda t: t)
 
         def lin(n, k):
             return (torch.randn((n, k), generator=g, device=device) / math.sqrt(k)).to(dtype)
@@ -81,10 +88,10 @@ class LlamaWeights:
 
         H, Hkv, D, hid, I = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden_size, cfg.intermediate_size
         layers = [LayerWeights(norm(hid), lin((H + 2 * Hkv) * D, hid), lin(hid, H * D), norm(hid),
-                               dense.interleave_gate_up(lin(I, hid), lin(I, hid)), lin(hid, I))
+                               tile(dense.interleave_gate_up(lin(I, hid), lin(I, hid))), tile(lin(hid, I)))
                   for _ in range(cfg.num_layers)]
         emb = torch.randn((cfg.vocab_size, hid), generator=g, device=device).to(dtype)
-        return LlamaWeights(emb, layers, norm(hid), lin(cfg.vocab_size, hid))
+        return LlamaWeights(emb, layers, norm(hid), tile(lin(cfg.vocab_size, hid)))
 
 
 class HipModelRunner:
