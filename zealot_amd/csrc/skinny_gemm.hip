@@ -356,8 +356,9 @@ int skinny_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, i
 }
 
 bool tile_weight_ok(int64_t n, int64_t k) {
+    // one workgroup per 16 x 128 block: the grid's x extent
     return n > 0 && k > 0 && n % 16 == 0 && k % kChunk == 0 && n <= 0x7fffffff && k <= 0x7fffffff &&
-           (n / 16) * (k / kChunk) <= 0xffffffffll;
+           (n / 16) * (k / kChunk) <= 0x7fffffffll;
 }
 
 int tile_weight(const void *w, void *wt, int64_t n, int64_t k, hipStream_t stream) {
