@@ -252,6 +252,22 @@ int zk_cache_append_kv_batch(zk_kv_cache *c, size_t layer, const char *const *id
 int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids,
                          const int32_t *num_tokens, int n, const void *k, const void *v,
                          zk_dtype src_dtype, int64_t src_token_stride);
+/* No counterpart in the reference (whose runner runs three q/k/v sgemms and
+ * then store_kv / append_kv per sequence, cuda_runner.rs:331-406): the fused
+ * projection qkv = x . w_qkv^T (bf16 x [T, hidden], w_qkv [(H + 2 Hkv) D,
+ * hidden] with q rows, then k, then v; T = sum num_tokens) and
+ * zk_cache_write_batch of its K and V columns.  qkv ([T, (H + 2 Hkv) D]
+ * bf16) receives at least the q columns, the input of the layer's attention
+ * (row stride (H + 2 Hkv) D).  When zk_linear's plan for the projection keeps
+ * a weight-streaming configuration with split k (as zk_linear_rms_norm
+ * folds) and the pools are bf16, one kernel adds the split sums, writes the
+ * q columns and stores K and V at their slots (the reduce kernel and the
+ * append in one launch; qkv's K / V columns are then not written);
+ * otherwise the projection writes qkv and the append reads it.  Pools and
+ * q bit for bit the two-call sequence through the same configuration. */
+int zk_cache_write_batch_qkv(zk_kv_cache *c, size_t layer, const char *const *ids,
+                             const int32_t *num_tokens, int n, const void *x, const void *w_qkv,
+                             int64_t hidden, int num_heads, void *qkv);
 /* Block tables from the caller's handles: sequence ids[i]'s table becomes
  * blocks[o_i .. o_i + num_blocks[i]) (packed in batch order), registering the
  * sequence on first use.  This is how a scheduler that shares `bm` with the

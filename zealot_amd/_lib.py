@@ -110,6 +110,7 @@ SIGNATURES = {
     "zk_cache_append_kv_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _P, _I]),
     "zk_cache_bind_blocks": (_I, [_P, _P, ctypes.POINTER(_CP), _I, _P, _P, _P]),
     "zk_cache_write_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _P, _I, _I64]),
+    "zk_cache_write_batch_qkv": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _P, _I64, _I, _P]),
     "zk_cache_enable_swap": (_I, [_P, _SZ]),
     "zk_cache_swap_space": (_I, [_P, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "zk_cache_swap_out": (_I, [_P, ctypes.POINTER(_CP), _I]),

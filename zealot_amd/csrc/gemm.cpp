@@ -632,3 +632,33 @@ int zk_linear_tuning(int on) {
 }
 
 }  // extern "C"
+
+int zk::linear_split_sums(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, hipStream_t stream,
+                          const float **partial, int *splits) {
+    if (!partial || !splits) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: linear_split_sums: NULL");
+    *partial = nullptr;
+    *splits = 0;
+    if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff)
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: linear_split_sums: bad shape");
+    if (m == 0) return ZK_OK;
+    if (!x || !w || !y) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: linear_split_sums: NULL pointer");
+    std::lock_guard<std::mutex> g(g_mu);
+    DeviceState *d;
+    if (int rc = device_state(&d)) return rc;
+    Scratch *sc;
+    if (int rc = scratch_for(*d, stream, false, &sc)) return rc;
+    Plan *p;
+    if (int rc = make_plan(*d, *sc, m, n, k, ZK_BF16, ZK_BF16, x, w, y, stream, g_tune, &p)) return rc;
+    if (p->fused_splits > 1 && skinny_fits(m, n, k, p->fused_rows, p->fused_splits) && aligned16(x) && aligned16(w)) {
+        if (int rc = scratch_for(*d, stream, true, &sc)) return rc;
+        zk::KernelTimer timer("linear", stream);
+        if (int rc = zk::skinny_linear(x, w, nullptr, m, n, k, false, p->fused_rows, p->fused_splits, sc->partial,
+                                       kSkinnyPartial, stream, /*reduce=*/false))
+            return rc;
+        *partial = (const float *)sc->partial;
+        *splits = p->fused_splits;
+        return ZK_OK;
+    }
+    return run_plan(*d, sc, p, x, w, y, m, n, k, ZK_BF16, stream);
+}
+

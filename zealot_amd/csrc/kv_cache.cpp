@@ -33,6 +33,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "../../include/zealot_dense.h"
 #include "zk_common.h"
 
 using zk::set_error;
@@ -478,6 +479,110 @@ void plan_sharing(const std::vector<const SeqState *> &seqs, size_t layer, size_
     }
 }
 
+// What a batched write does before and after its copy kernel: validation,
+// copy-on-write of every shared target block and the slot mapping (uploaded
+// with, for fp8 pools, each token's batch row and the sequences' scales at
+// this layer); afterwards the per-layer lengths and, at the last layer, the
+// sequences' token counts.
+struct WritePrep {
+    std::vector<SeqState *> seqs;
+    size_t T = 0;
+    const int64_t *d_slots = nullptr;
+    const int32_t *d_rows = nullptr;
+    const float *d_ks = nullptr, *d_vs = nullptr;
+};
+
+int prepare_write(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,
+                  bool have_src, WritePrep &w) {
+    if (!c || (n > 0 && (!ids || !num_tokens)))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: NULL argument");
+    if (layer >= c->num_layers)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: layer out of range");
+    if (n <= 0) return ZK_OK;
+    DeviceGuard g(c->device);
+    const size_t bs = c->block_size, H = c->num_kv_heads;
+    const bool fp8 = c->dtype == ZK_FP8_E4M3;
+    std::vector<SeqState *> &seqs = w.seqs;
+    seqs.assign((size_t)n, nullptr);
+    size_t T = 0;
+    for (int i = 0; i < n; ++i) {
+        if (int rc = find_seq(c, ids[i], &seqs[i])) return rc;
+        if (seqs[i]->swapped)
+            return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + ids[i] +
+                                                             " is swapped out");
+        for (int j = 0; j < i; ++j)
+            if (seqs[j] == seqs[i])
+                return set_error(ZK_ERR_INVALID_ARGUMENT,
+                                 std::string("Internal error: KVCache write batch: seq ") + ids[i] + " twice");
+        if (num_tokens[i] < 0)
+            return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: negative token count");
+        const SeqState &s = *seqs[i];
+        if (num_tokens[i] > 0) {
+            const size_t last = (s.cached_tokens + (size_t)num_tokens[i] - 1) / bs;
+            if (last >= s.handles.size())  // kv_cache.rs:234-239
+                return set_error(ZK_ERR_INTERNAL, "Internal error: KVCache append_kv: block_idx " +
+                                                      std::to_string(last) + " OOB (have " +
+                                                      std::to_string(s.handles.size()) + " blocks)");
+        }
+        if (fp8 && s.k_scales.empty())
+            return set_error(ZK_ERR_FAILED_PRECONDITION,
+                             std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
+        T += (size_t)num_tokens[i];
+    }
+    if (T == 0) return ZK_OK;
+    if (!have_src) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: NULL k/v");
+    std::vector<std::pair<SeqState *, size_t>> shared;  // copy-on-write of every shared target
+    for (int i = 0; i < n; ++i) {
+        SeqState &s = *seqs[i];
+        if (num_tokens[i] == 0) continue;
+        for (size_t idx = s.cached_tokens / bs; idx <= (s.cached_tokens + (size_t)num_tokens[i] - 1) / bs; ++idx)
+            if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1) shared.emplace_back(&s, idx);
+    }
+    if (int rc = cow_blocks(c, shared)) return rc;
+    const size_t slots_bytes = T * sizeof(int64_t);
+    const size_t rows_bytes = fp8 ? T * sizeof(int32_t) : 0;
+    const size_t scale_bytes = fp8 ? 2 * (size_t)n * H * sizeof(float) : 0;
+    std::vector<char> host(slots_bytes + rows_bytes + scale_bytes);
+    int64_t *slots = (int64_t *)host.data();
+    int32_t *rows = fp8 ? (int32_t *)(host.data() + slots_bytes) : nullptr;
+    size_t t = 0;
+    for (int i = 0; i < n; ++i) {
+        const SeqState &s = *seqs[i];
+        for (int j = 0; j < num_tokens[i]; ++j, ++t) {
+            const size_t pos = s.cached_tokens + (size_t)j;
+            slots[t] = (int64_t)s.handles[pos / bs].block_id * (int64_t)bs + (int64_t)(pos % bs);
+            if (fp8) rows[t] = i;
+        }
+    }
+    if (fp8) {
+        float *sc = (float *)(host.data() + slots_bytes + rows_bytes);
+        for (int i = 0; i < n; ++i) {
+            std::memcpy(sc + (size_t)i * H, seqs[i]->k_scales.data() + layer * H, H * sizeof(float));
+            std::memcpy(sc + (size_t)n * H + (size_t)i * H, seqs[i]->v_scales.data() + layer * H, H * sizeof(float));
+        }
+    }
+    if (int rc = put(c, c->d_meta, host.data(), host.size(), "KVCache slot mapping")) return rc;
+    char *d = (char *)c->d_meta.dev.p;
+    w.T = T;
+    w.d_slots = (const int64_t *)d;
+    w.d_rows = fp8 ? (const int32_t *)(d + slots_bytes) : nullptr;
+    w.d_ks = fp8 ? (const float *)(d + slots_bytes + rows_bytes) : nullptr;
+    w.d_vs = fp8 ? w.d_ks + (size_t)n * H : nullptr;
+    return ZK_OK;
+}
+
+void finish_write(zk_kv_cache *c, size_t layer, const int32_t *num_tokens, int n, WritePrep &w) {
+    for (int i = 0; i < n; ++i) {
+        SeqState &s = *w.seqs[i];
+        s.layer_len[layer] = std::max(s.layer_len[layer], s.cached_tokens + (size_t)num_tokens[i]);
+    }
+    if (layer + 1 == c->num_layers)
+        for (int i = 0; i < n; ++i) {
+            w.seqs[i]->cached_tokens += (size_t)num_tokens[i];
+            w.seqs[i]->block_offset = w.seqs[i]->cached_tokens % c->block_size;
+        }
+}
+
 }  // namespace
 
 extern "C" {
@@ -650,92 +755,51 @@ int zk_cache_append_kv(zk_kv_cache *c, size_t layer, const char *id, const void 
 
 int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,
                          const void *k, const void *v, zk_dtype src_dtype, int64_t src_token_stride) {
-    if (!c || (n > 0 && (!ids || !num_tokens)))
-        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: NULL argument");
-    if (layer >= c->num_layers)
-        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: layer out of range");
     if (src_dtype != ZK_F32 && src_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: bad src dtype");
-    if (n <= 0) return ZK_OK;
-    DeviceGuard g(c->device);
-    const size_t bs = c->block_size, H = c->num_kv_heads;
-    const bool fp8 = c->dtype == ZK_FP8_E4M3;
-    std::vector<SeqState *> seqs((size_t)n);
-    size_t T = 0;
-    for (int i = 0; i < n; ++i) {
-        if (int rc = find_seq(c, ids[i], &seqs[i])) return rc;
-        if (seqs[i]->swapped)
-            return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + ids[i] +
-                                                             " is swapped out");
-        for (int j = 0; j < i; ++j)
-            if (seqs[j] == seqs[i])
-                return set_error(ZK_ERR_INVALID_ARGUMENT,
-                                 std::string("Internal error: KVCache write batch: seq ") + ids[i] + " twice");
-        if (num_tokens[i] < 0)
-            return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: negative token count");
-        const SeqState &s = *seqs[i];
-        if (num_tokens[i] > 0) {
-            const size_t last = (s.cached_tokens + (size_t)num_tokens[i] - 1) / bs;
-            if (last >= s.handles.size())  // kv_cache.rs:234-239
-                return set_error(ZK_ERR_INTERNAL, "Internal error: KVCache append_kv: block_idx " +
-                                                      std::to_string(last) + " OOB (have " +
-                                                      std::to_string(s.handles.size()) + " blocks)");
-        }
-        if (fp8 && s.k_scales.empty())
-            return set_error(ZK_ERR_FAILED_PRECONDITION,
-                             std::string("Failed precondition: fp8 scales not set for seq ") + ids[i]);
-        T += (size_t)num_tokens[i];
-    }
-    if (T == 0) return ZK_OK;
-    if (!k || !v) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: NULL k/v");
-    std::vector<std::pair<SeqState *, size_t>> shared;  // copy-on-write of every shared target
-    for (int i = 0; i < n; ++i) {
-        SeqState &s = *seqs[i];
-        if (num_tokens[i] == 0) continue;
-        for (size_t idx = s.cached_tokens / bs; idx <= (s.cached_tokens + (size_t)num_tokens[i] - 1) / bs; ++idx)
-            if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1) shared.emplace_back(&s, idx);
-    }
-    if (int rc = cow_blocks(c, shared)) return rc;
-    const size_t slots_bytes = T * sizeof(int64_t);
-    const size_t rows_bytes = fp8 ? T * sizeof(int32_t) : 0;
-    const size_t scale_bytes = fp8 ? 2 * (size_t)n * H * sizeof(float) : 0;
-    std::vector<char> host(slots_bytes + rows_bytes + scale_bytes);
-    int64_t *slots = (int64_t *)host.data();
-    int32_t *rows = fp8 ? (int32_t *)(host.data() + slots_bytes) : nullptr;
-    size_t t = 0;
-    for (int i = 0; i < n; ++i) {
-        const SeqState &s = *seqs[i];
-        for (int j = 0; j < num_tokens[i]; ++j, ++t) {
-            const size_t pos = s.cached_tokens + (size_t)j;
-            slots[t] = (int64_t)s.handles[pos / bs].block_id * (int64_t)bs + (int64_t)(pos % bs);
-            if (fp8) rows[t] = i;
-        }
-    }
-    if (fp8) {
-        float *sc = (float *)(host.data() + slots_bytes + rows_bytes);
-        for (int i = 0; i < n; ++i) {
-            std::memcpy(sc + (size_t)i * H, seqs[i]->k_scales.data() + layer * H, H * sizeof(float));
-            std::memcpy(sc + (size_t)n * H + (size_t)i * H, seqs[i]->v_scales.data() + layer * H, H * sizeof(float));
-        }
-    }
-    if (int rc = put(c, c->d_meta, host.data(), host.size(), "KVCache slot mapping")) return rc;
-    char *d = (char *)c->d_meta.dev.p;
-    const int32_t *d_rows = fp8 ? (const int32_t *)(d + slots_bytes) : nullptr;
-    const float *d_ks = fp8 ? (const float *)(d + slots_bytes + rows_bytes) : nullptr;
-    const float *d_vs = fp8 ? d_ks + (size_t)n * H : nullptr;
+    WritePrep w;
+    if (int rc = prepare_write(c, layer, ids, num_tokens, n, k && v, w)) return rc;
+    if (w.T == 0) return ZK_OK;
     if (int rc = zk::append(c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, k, v, src_dtype,
-                            src_token_stride, (const int64_t *)d, (int64_t)T, (int)H, (int)c->head_dim, (int)bs,
-                            (int64_t)c->num_blocks, d_ks, d_vs, d_rows, c->stream))
+                            src_token_stride, w.d_slots, (int64_t)w.T, (int)c->num_kv_heads, (int)c->head_dim,
+                            (int)c->block_size, (int64_t)c->num_blocks, w.d_ks, w.d_vs, w.d_rows, c->stream))
         return rc;
-    for (int i = 0; i < n; ++i) {
-        SeqState &s = *seqs[i];
-        s.layer_len[layer] = std::max(s.layer_len[layer], s.cached_tokens + (size_t)num_tokens[i]);
+    finish_write(c, layer, num_tokens, n, w);
+    return ZK_OK;
+}
+
+int zk_cache_write_batch_qkv(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,
+                             const void *x, const void *w_qkv, int64_t hidden, int num_heads, void *qkv) {
+    if (!c) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write qkv: NULL cache");
+    const int64_t qcols = (int64_t)num_heads * (int64_t)c->head_dim,
+                  cols = qcols + 2 * (int64_t)c->num_kv_heads * (int64_t)c->head_dim;
+    if (num_heads <= 0 || hidden <= 0)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write qkv: bad shape");
+    WritePrep w;
+    if (int rc = prepare_write(c, layer, ids, num_tokens, n, x && w_qkv && qkv, w)) return rc;
+    if (w.T == 0) return ZK_OK;
+    const int64_t T = (int64_t)w.T;
+    const float *partial = nullptr;
+    int splits = 0;
+    if (c->dtype == ZK_BF16) {  // the projection's split-k sums, if its plan keeps them, go straight to the pools
+        if (int rc = zk::linear_split_sums(x, w_qkv, qkv, T, cols, hidden, c->stream, &partial, &splits)) return rc;
+    } else if (int rc = zk_linear(x, w_qkv, qkv, T, cols, hidden, ZK_BF16, ZK_BF16, c->stream)) {
+        return rc;
     }
-    if (layer + 1 == c->num_layers)
-        for (int i = 0; i < n; ++i) {
-            seqs[i]->cached_tokens += (size_t)num_tokens[i];
-            seqs[i]->block_offset = seqs[i]->cached_tokens % bs;
-        }
+    if (splits > 1) {
+        if (int rc = zk::append_split_sums(c->k_pool(layer), c->v_pool(layer), partial, splits, T, cols, qkv, cols,
+                                           qcols, w.d_slots, (int)c->num_kv_heads, (int)c->head_dim,
+                                           (int)c->block_size, (int64_t)c->num_blocks, c->stream))
+            return rc;
+    } else {
+        const char *y = (const char *)qkv;
+        if (int rc = zk::append(c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, y + 2 * qcols,
+                                y + 2 * (qcols + (int64_t)c->num_kv_heads * c->head_dim), ZK_BF16, cols, w.d_slots, T,
+                                (int)c->num_kv_heads, (int)c->head_dim, (int)c->block_size, (int64_t)c->num_blocks,
+                                w.d_ks, w.d_vs, w.d_rows, c->stream))
+            return rc;
+    }
+    finish_write(c, layer, num_tokens, n, w);
     return ZK_OK;
 }
 

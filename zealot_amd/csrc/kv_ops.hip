@@ -64,6 +64,42 @@ append_copy_kernel(const char *__restrict__ k, const char *__restrict__ v, char 
             data);
 }
 
+// A fused q/k/v projection's split-k sums straight into the pools: y[t, c] =
+// bf16(sum over ranges r, in order, of partial[r][t][c]) (the sum the
+// projection's reduce kernel would store), one thread per 8 columns of a
+// row; q columns [0, qcols) go to q_out (row stride ldq), the K and V
+// columns (Hkv * D each, after them) to the bf16 pools at slot_mapping[t],
+// bit for bit the reduce kernel followed by the append of its K / V columns.
+__global__ void __launch_bounds__(kThreads)
+append_split_sums_kernel(const float *__restrict__ partial, int splits, uint32_t rows, uint32_t cols8,
+                         uint16_t *__restrict__ q_out, uint64_t ldq, uint32_t qcols, char *__restrict__ k_pool,
+                         char *__restrict__ v_pool, const int64_t *__restrict__ slots, uint32_t hkv, uint32_t head_dim,
+                         uint32_t block_size, int64_t num_slots) {
+    const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= rows * cols8) return;
+    const uint32_t t = idx / cols8, c = 8 * (idx % cols8);
+    const size_t plane = (size_t)rows * cols8 * 8;
+    const f32x4 *p = reinterpret_cast<const f32x4 *>(partial + (size_t)t * cols8 * 8 + c);
+    f32x4 a = p[0], b = p[1];
+    for (int r = 1; r < splits; ++r) {
+        a += p[r * plane / 4];
+        b += p[r * plane / 4 + 1];
+    }
+    const uint4 v = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])};
+    if (c < qcols) {
+        st16(q_out + (size_t)t * ldq + c, v);
+        return;
+    }
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= num_slots) return;
+    const uint32_t kc = c - qcols, kd = hkv * head_dim, kvc = kc < kd ? kc : kc - kd;
+    const uint32_t h = kvc / head_dim, d = kvc % head_dim;
+    const int64_t blk = slot / block_size, tib = slot % block_size;
+    st16_nt((kc < kd ? k_pool : v_pool) +
+                ((((size_t)blk * hkv + h) * block_size + (size_t)tib) * head_dim + d) * sizeof(uint16_t),
+            v);
+}
+
 // The same copy when the chunks per row, the kv-heads, the row bytes and the
 // block size are all powers of two (16-token blocks, 2^k heads, 256-byte bf16
 // rows: the usual paged layout): shifts and masks instead of the divisions,
@@ -428,6 +464,28 @@ int zk_append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, c
 }
 
 }  // extern "C"
+
+int zk::append_split_sums(void *k_pool, void *v_pool, const float *partial, int splits, int64_t rows,
+                          int64_t cols, void *q_out, int64_t ldq, int64_t qcols, const int64_t *slot_mapping,
+                          int num_kv_heads, int head_dim, int block_size, int64_t num_blocks, void *stream) {
+    if (rows <= 0) return ZK_OK;
+    const int64_t kd = (int64_t)num_kv_heads * head_dim;
+    if (splits < 1 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 || block_size <= 0 || num_blocks <= 0 ||
+        qcols < 0 || qcols % 8 || cols != qcols + 2 * kd || ldq < qcols || rows * (cols / 8) >= (1ll << 31))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append_split_sums: bad shape");
+    if (!k_pool || !v_pool || !partial || !slot_mapping || (qcols > 0 && !q_out))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append_split_sums: NULL pointer");
+    if ((((uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)partial | (uintptr_t)q_out) & 15u) || (ldq % 8))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_append_split_sums: unaligned operand");
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t cols8 = (uint32_t)(cols / 8), total = (uint32_t)(rows * cols8);
+    KernelTimer timer("append", s);
+    append_split_sums_kernel<<<(total + kThreads - 1) / kThreads, kThreads, 0, s>>>(
+        partial, splits, (uint32_t)rows, cols8, (uint16_t *)q_out, (uint64_t)ldq, (uint32_t)qcols, (char *)k_pool,
+        (char *)v_pool, slot_mapping, (uint32_t)num_kv_heads, (uint32_t)head_dim, (uint32_t)block_size,
+        num_blocks * block_size);
+    return check_launch("zk_append_split_sums");
+}
 
 int zk::append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, const void *v, zk_dtype src_dtype,
                int64_t src_token_stride, const int64_t *slot_mapping, int64_t num_tokens, int num_kv_heads,

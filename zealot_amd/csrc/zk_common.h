@@ -51,6 +51,22 @@ int append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, cons
            int64_t src_token_stride, const int64_t *slot_mapping, int64_t num_tokens, int num_kv_heads, int head_dim,
            int block_size, int64_t num_blocks, const float *k_scales, const float *v_scales, const int32_t *token_row,
            void *stream);
+// A fused q/k/v projection's split-k sums (partial: [splits][rows][cols]
+// f32, cols = qcols + 2 Hkv D) added in range order and rounded to bf16 as
+// the projection's reduce kernel does: the q columns to q_out (bf16, row
+// stride ldq elements), the K and V columns into the bf16 pools at
+// slot_mapping[row] -- one launch for the reduce and the append.
+int append_split_sums(void *k_pool, void *v_pool, const float *partial, int splits, int64_t rows, int64_t cols,
+                      void *q_out, int64_t ldq, int64_t qcols, const int64_t *slot_mapping, int num_kv_heads,
+                      int head_dim, int block_size, int64_t num_blocks, void *stream);
+// y = x . w^T (bf16, zk_linear's plan for the shape) left as split-k sums
+// when the plan keeps a weight-streaming configuration with split k beside
+// its choice (the one zk_linear_rms_norm folds): *partial and *splits > 1
+// then describe them ([splits][m][n] f32 in the stream's workspace, valid
+// until the next projection on the stream) and y is not written; otherwise
+// y holds the product and *splits = 0.
+int linear_split_sums(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, hipStream_t stream,
+                      const float **partial, int *splits);
 // Swap staging (kv_ops.hip): blocks[i] of each of the num_pools pools at
 // slab + p * pool_bytes <-> staging[(i * num_pools + p) * block_bytes ...]
 // (to_staging: pools -> staging, else staging -> pools).

@@ -211,6 +211,27 @@ class KVCache:
         _lib.check(_lib.lib().zk_cache_write_batch(self._h, layer, b.arr, ctypes.addressof(nt), len(b),
                                                    k.data_ptr(), v.data_ptr(), zk_dtype(k), stride))
 
+    def write_batch_qkv(self, layer: int, ids, num_tokens, x, w_qkv, num_heads: int, out=None):
+        """The fused q/k/v projection of x [T, hidden] (bf16) against w_qkv
+        [(H + 2 Hkv) D, hidden] and write_batch of its K and V columns, in
+        one call (zk_cache_write_batch_qkv): returns the projection buffer
+        [T, (H + 2 Hkv) D], whose q columns are always written (its K / V
+        columns only when the projection was not folded into the write)."""
+        b = _batch(ids)
+        nt = _counts(num_tokens, len(b))
+        rows = int(sum(nt))
+        cols = (num_heads + 2 * self.num_kv_heads) * self.head_dim
+        if x.dtype != torch.bfloat16 or w_qkv.dtype != torch.bfloat16:
+            raise TypeError("x and w_qkv must be bfloat16")
+        if x.dim() != 2 or x.shape[0] != rows or tuple(w_qkv.shape) != (cols, x.shape[1]):
+            raise ValueError("x must be [sum(num_tokens), hidden] and w_qkv [(H + 2 Hkv) D, hidden]")
+        if out is None:
+            out = torch.empty((rows, cols), dtype=torch.bfloat16, device=x.device)
+        _lib.check(_lib.lib().zk_cache_write_batch_qkv(self._h, layer, b.arr, ctypes.addressof(nt), len(b),
+                                                       _dev(x, "x"), _dev(w_qkv, "w_qkv"), x.shape[1], num_heads,
+                                                       _dev(out, "out")))
+        return out
+
     # -- decode --------------------------------------------------------------
     def paged_decode(self, layer: int, ids, q, out=None, scale=None, mapping="grouped"):
         """Decode attention for registered sequences `ids` (batch order; a list

@@ -11,7 +11,9 @@ reference).  What differs is the shape of the work:
   - one launch per op for all sequences of the batch (the reference loops
     over sequences, cuda_runner.rs:274);
   - q/k/v come from ONE projection against a fused [(H + 2 Hkv) D, hidden]
-    weight, gate/up from one against [2 I, hidden] whose gate and up rows
+    weight (its split-k sums, when it has them, added by the kernel that
+    writes K and V to the pages: zk_cache_write_batch_qkv), gate/up from one
+    against [2 I, hidden] whose gate and up rows
     alternate in blocks of 16, so the projection's waves hold the gate and
     up outputs of the same columns and write SiLU(gate) * up themselves
     (dense.linear_silu_mul); K and V are appended and
@@ -130,11 +132,12 @@ class HipModelRunner:
         dense.rms_norm(resid, w.layers[0].attn_norm, cfg.rms_eps, out=normed)
         last = len(w.layers) - 1
         for layer, lw in enumerate(w.layers):
-            qkv = dense.linear(normed, lw.qkv)
+            if normed.dtype == torch.bfloat16:  # projection and KV write in one call
+                qkv = self.kv.write_qkv(layer, plan, normed, lw.qkv, H)
+            else:
+                qkv = dense.linear(normed, lw.qkv)
+                self.kv.write(layer, plan, qkv[:, qd:qd + kd].view(T, Hkv, D), qkv[:, qd + kd:].view(T, Hkv, D))
             q = qkv[:, :qd].view(T, H, D)
-            k = qkv[:, qd:qd + kd].view(T, Hkv, D)
-            v = qkv[:, qd + kd:].view(T, Hkv, D)
-            self.kv.write(layer, plan, k, v)
             attn = self.kv.attention(layer, plan, q)
             # resid += o_proj(attn); normed = norm(resid)
             dense.linear_rms_norm(attn.view(T, qd), lw.o, lw.ffn_norm, cfg.rms_eps, residual=resid, out=normed,

@@ -72,6 +72,11 @@ class PagedKVRunner:
     def write(self, layer: int, plan: StepPlan, k, v) -> None:
         self.cache.write_batch(layer, plan.ids, plan.num_tokens, k, v)
 
+    def write_qkv(self, layer: int, plan: StepPlan, x, w_qkv, num_heads: int, out=None):
+        """The step's fused q/k/v projection and KV write for one layer; returns
+        the projection buffer (its q columns feed attention)."""
+        return self.cache.write_batch_qkv(layer, plan.ids, plan.num_tokens, x, w_qkv, num_heads, out=out)
+
     def attention(self, layer: int, plan: StepPlan, q, out=None, scale=None, mapping="grouped"):
         return self.cache.attention_batch(layer, plan.ids, plan.num_tokens, q, out=out, scale=scale,
                                           mapping=mapping)
