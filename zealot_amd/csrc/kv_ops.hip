@@ -326,7 +326,12 @@ struct PoolArgs {
     char *p[kMaxPoolsPerLaunch];
 };
 
-// One workgroup per (pair i, pool p): block dst[i] := block src[i].
+// One workgroup per (pair i, pool p): block dst[i] := block src[i].  Sources
+// are read with the default cache policy: the forks of one parent copy the
+// same source block, and the nontemporal hint made the re-reads of a source
+// that another fork had just fetched slower (C4's copy: 76 -> 44 us with the
+// default policy, every byte still read from HBM once).  The destinations are
+// written once, nontemporal.
 __global__ void __launch_bounds__(kThreads)
 copy_blocks_kernel(PoolArgs pools, const int32_t *__restrict__ src, const int32_t *__restrict__ dst,
                    uint64_t block_bytes, int64_t num_blocks) {
@@ -340,14 +345,14 @@ copy_blocks_kernel(PoolArgs pools, const int32_t *__restrict__ src, const int32_
         uint64_t n16 = block_bytes >> 4;
         uint64_t i0 = threadIdx.x;
         for (; i0 + 3 * kThreads < n16; i0 += 4 * kThreads) {
-            uint4 a = ld16_nt(from + 16 * i0), b = ld16_nt(from + 16 * (i0 + kThreads));
-            uint4 c = ld16_nt(from + 16 * (i0 + 2 * kThreads)), e = ld16_nt(from + 16 * (i0 + 3 * kThreads));
+            uint4 a = ld16(from + 16 * i0), b = ld16(from + 16 * (i0 + kThreads));
+            uint4 c = ld16(from + 16 * (i0 + 2 * kThreads)), e = ld16(from + 16 * (i0 + 3 * kThreads));
             st16_nt(to + 16 * i0, a);
             st16_nt(to + 16 * (i0 + kThreads), b);
             st16_nt(to + 16 * (i0 + 2 * kThreads), c);
             st16_nt(to + 16 * (i0 + 3 * kThreads), e);
         }
-        for (; i0 < n16; i0 += kThreads) st16_nt(to + 16 * i0, ld16_nt(from + 16 * i0));
+        for (; i0 < n16; i0 += kThreads) st16_nt(to + 16 * i0, ld16(from + 16 * i0));
     } else {
         for (uint64_t b = threadIdx.x; b < block_bytes; b += kThreads) to[b] = from[b];
     }
@@ -364,7 +369,7 @@ copy_blocks_piece_kernel(PoolArgs pools, const int32_t *__restrict__ src, const 
     if (s < 0 || d < 0 || s >= num_blocks || d >= num_blocks) return;
     char *base = pools.p[p];
     const size_t off = (size_t)piece * (16 * kThreads) + 16 * (size_t)threadIdx.x;
-    st16_nt(base + (size_t)d * block_bytes + off, ld16_nt(base + (size_t)s * block_bytes + off));
+    st16_nt(base + (size_t)d * block_bytes + off, ld16(base + (size_t)s * block_bytes + off));
 }
 
 // Swap staging: block blocks[i] of every pool (pool p at slab + p *
