@@ -264,7 +264,8 @@ int zk_cache_write_batch(zk_kv_cache *c, size_t layer, const char *const *ids,
  * q columns and stores K and V at their slots (the reduce kernel and the
  * append in one launch; qkv's K / V columns are then not written);
  * otherwise the projection writes qkv and the append reads it.  Pools and
- * q bit for bit the two-call sequence through the same configuration. */
+ * q bit for bit the two-call sequence through the same configuration.  qkv
+ * must not overlap x (rejected). */
 int zk_cache_write_batch_qkv(zk_kv_cache *c, size_t layer, const char *const *ids,
                              const int32_t *num_tokens, int n, const void *x, const void *w_qkv,
                              int64_t hidden, int num_heads, void *qkv);

@@ -51,3 +51,32 @@ def test_tiled_weight_rejects_wrong_buffers():
         dense.TiledWeight(torch.zeros(48 * 128, dtype=torch.float32), 48, 128)
     with pytest.raises(ValueError):
         dense.TiledWeight(torch.zeros(47 * 128, dtype=torch.bfloat16), 48, 128)
+
+
+def test_dense_wrappers_check_operand_sizes_before_any_launch():
+    """The dense wrappers hand plain pointers to kernels that trust the sizes:
+    a caller's out / residual / weight of the wrong size or dtype is rejected
+    on the host (CPU tensors here: the check comes before any device work)."""
+    import pytest
+    import torch
+    from zealot_amd import dense
+    x = torch.zeros((4, 64), dtype=torch.bfloat16)
+    w = torch.zeros(64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        dense.rms_norm(x, w, out=torch.zeros((4, 32), dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        dense.rms_norm(x, torch.zeros(32, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        dense.rms_norm(x, w, out=torch.zeros((4, 64), dtype=torch.float32))
+    with pytest.raises(ValueError):
+        dense.rms_norm(x, w, residual=torch.zeros((3, 64), dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        dense.add(x, torch.zeros((4, 63), dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        dense.linear(x, torch.zeros((16, 64), dtype=torch.bfloat16), out=torch.zeros((4, 8), dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        dense.linear_rms_norm(x, torch.zeros((16, 64), dtype=torch.bfloat16), torch.zeros(8, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        dense.linear_silu_mul(x, torch.zeros((32, 64), dtype=torch.bfloat16), out=torch.zeros((4, 8), dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        dense.silu_mul(x, torch.zeros((4, 64), dtype=torch.float32))

@@ -108,3 +108,9 @@ def test_write_batch_qkv_rejects_bad_shapes():
         cache.write_batch_qkv(0, ["a"], [1], x.float(), w, H)
     with pytest.raises(ZealotError):  # no block for a 17th token
         cache.write_batch_qkv(0, ["a"], [17], torch.zeros((17, 256), dtype=torch.bfloat16, device="cuda"), w, H)
+    with pytest.raises(ValueError):  # out of the wrong shape
+        cache.write_batch_qkv(0, ["a"], [1], x, w, H, out=torch.empty((1, 64), dtype=torch.bfloat16, device="cuda"))
+    buf = torch.zeros(COLS + 256, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ZealotError):  # out overlapping x
+        cache.write_batch_qkv(0, ["a"], [1], buf[:256].view(1, 256), w, H, out=buf[128:128 + COLS].view(1, COLS))
+    assert cache.seq_state("a").cached_tokens == 0  # nothing was written

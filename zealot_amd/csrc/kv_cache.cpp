@@ -775,6 +775,14 @@ int zk_cache_write_batch_qkv(zk_kv_cache *c, size_t layer, const char *const *id
                   cols = qcols + 2 * (int64_t)c->num_kv_heads * (int64_t)c->head_dim;
     if (num_heads <= 0 || hidden <= 0)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write qkv: bad shape");
+    if (x && qkv && n > 0 && num_tokens) {  // the projection reads x while it writes qkv
+        int64_t rows = 0;
+        for (int i = 0; i < n; ++i) rows += num_tokens[i] > 0 ? num_tokens[i] : 0;
+        const uintptr_t xa = (uintptr_t)x, xb = xa + (uintptr_t)(rows * hidden * 2), qa = (uintptr_t)qkv,
+                        qb = qa + (uintptr_t)(rows * cols * 2);
+        if (rows > 0 && xa < qb && qa < xb)
+            return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write qkv: qkv overlaps x");
+    }
     WritePrep w;
     if (int rc = prepare_write(c, layer, ids, num_tokens, n, x && w_qkv && qkv, w)) return rc;
     if (w.T == 0) return ZK_OK;

@@ -18,16 +18,38 @@ def _dt(t: torch.Tensor) -> int:
     return zk_dtype(t)
 
 
+def _sized(t, name: str, numel: int, dtype) -> None:
+    """The kernels take plain pointers and trust the sizes: every operand is
+    checked against the elements and dtype the launch will touch."""
+    if t is None:
+        return
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.numel() != numel:
+        raise ValueError(f"{name} has {t.numel()} elements, the op needs {numel}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
 def rms_norm(x, weight, eps: float = 1e-6, residual=None, out=None, residual_out=None, rows=None, stream=None):
     """out = rms_norm(s) * weight, s = x (+ residual, written to residual_out,
     which may be `residual`), over x's rows or over the rows listed in `rows`
     (device int64); rms_norm.cu:4-55."""
     dim = x.shape[-1]
     n = rows.numel() if rows is not None else x.numel() // dim
+    if rows is None and x.numel() != n * dim:
+        raise ValueError("x must hold whole rows of dim elements")
     if out is None:
         out = torch.empty((n, dim), dtype=x.dtype, device=x.device)
     if residual is not None and residual_out is None:
         residual_out = torch.empty((n, dim), dtype=x.dtype, device=x.device)
+    _sized(weight, "weight", dim, x.dtype)
+    _sized(out, "out", n * dim, x.dtype)
+    if rows is None:
+        _sized(residual, "residual", n * dim, x.dtype)
+    elif residual is not None and (residual.numel() != x.numel() or residual.dtype != x.dtype):
+        raise ValueError("residual must match x (its rows are selected by `rows` too)")
+    _sized(residual_out, "residual_out", n * dim, x.dtype)
     _lib.check(_lib.lib().zk_rms_norm(
         _dev(x, "x"), None if residual is None else _dev(residual, "residual"), _dev(weight, "weight"),
         _dev(out, "out"), None if residual_out is None else _dev(residual_out, "residual_out"),
@@ -39,20 +61,25 @@ def silu_mul(gate, up, out=None, stream=None):
     """silu(gate) * up (activation.cu:4-12); gate / up may be column slices
     of one [rows, 2 * cols] tensor (a fused gate|up projection)."""
     rows, cols = gate.shape
+    if up.dtype != gate.dtype:
+        raise TypeError("gate and up must share a dtype")
     for name, t in (("gate", gate), ("up", up)):
         _dev(t, name, contiguous=False)
         if t.shape != (rows, cols) or t.stride(1) != 1:
             raise ValueError(f"{name} must be [rows, cols] with contiguous rows")
     if out is None:
         out = torch.empty((rows, cols), dtype=gate.dtype, device=gate.device)
+    _sized(out, "out", rows * cols, gate.dtype)
     _lib.check(_lib.lib().zk_silu_mul(gate.data_ptr(), up.data_ptr(), _dev(out, "out"), rows, cols, gate.stride(0),
                                       up.stride(0), _dt(gate), _stream(stream)))
     return out
 
 
 def add(a, b, out=None, stream=None):
+    _sized(b, "b", a.numel(), a.dtype)
     if out is None:
         out = torch.empty_like(a)
+    _sized(out, "out", a.numel(), a.dtype)
     _lib.check(_lib.lib().zk_add(_dev(a, "a"), _dev(b, "b"), _dev(out, "out"), a.numel(), _dt(a), _stream(stream)))
     return out
 
@@ -62,6 +89,7 @@ def embedding(ids, table, out=None, stream=None):
     n = ids.numel()
     if out is None:
         out = torch.empty((n, table.shape[1]), dtype=table.dtype, device=table.device)
+    _sized(out, "out", n * table.shape[1], table.dtype)
     _lib.check(_lib.lib().zk_embedding(_dev(ids, "ids", torch.int64), _dev(table, "table"), _dev(out, "out"), n,
                                        table.shape[0], table.shape[1], _dt(table), _stream(stream)))
     return out
@@ -133,6 +161,7 @@ def linear(x, weight, out=None, out_dtype=None, stream=None):
         _tiled_x(x, weight)
         if out is None:
             out = torch.empty((m, n), dtype=out_dtype or x.dtype, device=x.device)
+        _sized(out, "out", m * n, out.dtype)  # the C ABI checks the dtype pair
         _lib.check(_lib.lib().zk_linear_tiled(_dev(x, "x"), _dev(weight.data, "weight"), _dev(out, "out"), m, n, k,
                                               zk_dtype(out), _stream(stream)))
         return out
@@ -141,6 +170,7 @@ def linear(x, weight, out=None, out_dtype=None, stream=None):
     od = out_dtype or x.dtype
     if out is None:
         out = torch.empty((m, n), dtype=od, device=x.device)
+    _sized(out, "out", m * n, out.dtype)  # the C ABI checks the dtype pair
     _lib.check(_lib.lib().zk_linear(_dev(x, "x"), _dev(weight, "weight"), _dev(out, "out"), m, n, k, _dt(x),
                                     zk_dtype(out), _stream(stream)))
     return out
@@ -167,6 +197,9 @@ def linear_rms_norm(x, weight, norm_weight, eps: float = 1e-6, residual=None, ou
         out = torch.empty((m, n), dtype=x.dtype, device=x.device)
     if residual is not None and residual_out is None:
         residual_out = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    _sized(norm_weight, "norm_weight", n, x.dtype)
+    for name, t in (("out", out), ("residual", residual), ("residual_out", residual_out)):
+        _sized(t, name, m * n, x.dtype)
     fn = _lib.lib().zk_linear_rms_norm_tiled if tiled else _lib.lib().zk_linear_rms_norm
     _lib.check(fn(
         _dev(x, "x"), _dev(weight.data if tiled else weight, "weight"), m, n, k,
@@ -210,6 +243,7 @@ def linear_silu_mul(x, gate_up, out=None, gu=None, stream=None):
         _tiled_x(x, gate_up)
         if out is None:
             out = torch.empty((m, n // 2), dtype=x.dtype, device=x.device)
+        _sized(out, "out", m * (n // 2), x.dtype)
         _lib.check(_lib.lib().zk_linear_silu_mul_tiled(_dev(x, "x"), _dev(gate_up.data, "gate_up"), _dev(out, "out"),
                                                        m, n // 2, k, _stream(stream)))
         return out
@@ -220,6 +254,8 @@ def linear_silu_mul(x, gate_up, out=None, gu=None, stream=None):
         out = torch.empty((m, n // 2), dtype=x.dtype, device=x.device)
     if gu is None:
         gu = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    _sized(out, "out", m * (n // 2), x.dtype)
+    _sized(gu, "gu", m * n, x.dtype)
     _lib.check(_lib.lib().zk_linear_silu_mul(_dev(x, "x"), _dev(gate_up, "gate_up"), _dev(out, "out"), m, n // 2, k,
                                              _dev(gu, "gu"), _stream(stream)))
     return out

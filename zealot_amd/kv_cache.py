@@ -227,6 +227,8 @@ class KVCache:
             raise ValueError("x must be [sum(num_tokens), hidden] and w_qkv [(H + 2 Hkv) D, hidden]")
         if out is None:
             out = torch.empty((rows, cols), dtype=torch.bfloat16, device=x.device)
+        elif out.dtype != torch.bfloat16 or tuple(out.shape) != (rows, cols):
+            raise ValueError("out must be a bfloat16 [sum(num_tokens), (H + 2 Hkv) D] tensor")
         _lib.check(_lib.lib().zk_cache_write_batch_qkv(self._h, layer, b.arr, ctypes.addressof(nt), len(b),
                                                        _dev(x, "x"), _dev(w_qkv, "w_qkv"), x.shape[1], num_heads,
                                                        _dev(out, "out")))
