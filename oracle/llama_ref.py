@@ -25,10 +25,21 @@ class LlamaRef:
     zealot_amd.model.LlamaWeights (qkv [(H+2Hkv)D, hid], gate_up [2I, hid] with
     gate and up rows interleaved in blocks of 16)."""
 
-    def __init__(self, cfg, weights):
+    def __init__(self, cfg, weights, matmul=None):
+        """matmul(x, w) = x . w^T: the oracle's or_matmul by default; a wide
+        model's test may pass numpy's float32 product (the same sums in another
+        order, pinned against or_matmul in tests/test_oracle_dense.py)."""
         self.cfg = cfg
         self.w = weights
+        self.mm = matmul or linear
         self.kv = {}  # request id -> per layer [K (tokens, Hkv, D), V]
+        # gate_up rows: gate and up interleaved in blocks of 16 -> the two projections
+        I = cfg.intermediate_size
+        self.gate_up = []
+        for lw in weights["layers"]:
+            gu = lw["gate_up"].reshape(I // 16, 2, 16, -1)
+            self.gate_up.append((np.ascontiguousarray(gu[:, 0].reshape(I, -1)),
+                                 np.ascontiguousarray(gu[:, 1].reshape(I, -1))))
 
     def drop(self, rid):
         self.kv.pop(rid, None)
@@ -52,8 +63,8 @@ class LlamaRef:
     def step(self, entries):
         """entries: list of (request id, token ids of this step, tokens_before).
         Returns logits [len(entries), vocab] (float32)."""
-        cfg, w = self.cfg, self.w
-        H, Hkv, D, I = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.intermediate_size
+        cfg, w, mm = self.cfg, self.w, self.mm
+        H, Hkv, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
         qd, kd = H * D, Hkv * D
         logits = []
         for rid, ids, before in entries:
@@ -65,22 +76,21 @@ class LlamaRef:
             for layer in range(cfg.num_layers):
                 lw = w["layers"][layer]
                 normed = rms_norm(h, lw["attn_norm"], cfg.rms_eps)
-                q = linear(normed, lw["qkv"][:qd])
-                k = linear(normed, lw["qkv"][qd:qd + kd])
-                v = linear(normed, lw["qkv"][qd + kd:])
+                q = mm(normed, lw["qkv"][:qd])
+                k = mm(normed, lw["qkv"][qd:qd + kd])
+                v = mm(normed, lw["qkv"][qd + kd:])
                 K, V = self.kv[rid][layer]
                 self.kv[rid][layer] = [np.concatenate([K, k.reshape(n, Hkv, D)]),
                                        np.concatenate([V, v.reshape(n, Hkv, D)])]
                 attn = self._attend(rid, layer, q.reshape(n, H, D), before).reshape(n, qd)
-                h = add(linear(attn, lw["o"]), h)
+                h = add(mm(attn, lw["o"]), h)
                 normed = rms_norm(h, lw["ffn_norm"], cfg.rms_eps)
-                # gate_up rows: gate and up interleaved in blocks of 16
-                gu_w = lw["gate_up"].reshape(I // 16, 2, 16, -1)
-                gate = linear(normed, np.ascontiguousarray(gu_w[:, 0].reshape(I, -1)))
-                up = linear(normed, np.ascontiguousarray(gu_w[:, 1].reshape(I, -1)))
-                h = add(linear(silu_gate_mul(gate, up), lw["down"]), h)
+                gate_w, up_w = self.gate_up[layer]
+                gate = mm(normed, gate_w)
+                up = mm(normed, up_w)
+                h = add(mm(silu_gate_mul(gate, up), lw["down"]), h)
             final = rms_norm(h[-1:], w["final_norm"], cfg.rms_eps)
-            logits.append(linear(final, w["lm_head"])[0])
+            logits.append(mm(final, w["lm_head"])[0])
         return np.stack(logits)
 
 

@@ -21,13 +21,19 @@ from tests.gpu_util import announce
 pytestmark = pytest.mark.gpu
 
 
-def _run(dtype, tol, argmax_frac, swap=False):
+def _np_matmul(x, w):
+    """x . w^T in float32 through numpy (BLAS): the oracle's or_matmul in
+    another summation order (tests/test_oracle_dense.py pins the two)."""
+    return np.ascontiguousarray(x, np.float32) @ np.asarray(w, np.float32).T
+
+
+def _run(dtype, tol, argmax_frac, swap=False, cfg=None, short=False):
     import zealot_amd as ze
     from oracle.llama_ref import LlamaRef, weights_to_numpy
     from zealot_amd import KVCache, PagedKVRunner, Priority, Scheduler, SchedulerConfig
     from zealot_amd.model import HipModelRunner, LlamaConfig, LlamaWeights
-    cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_layers=2, num_heads=8,
-                      num_kv_heads=2, head_dim=64)
+    cfg = cfg or LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_layers=2, num_heads=8,
+                             num_kv_heads=2, head_dim=64)
     # with swap: 8 blocks for four requests, so the scheduler preempts by
     # swap (and once by recompute) while the reference keeps every sequence
     NB, BS = (8, 16) if swap else (64, 16)
@@ -40,12 +46,16 @@ def _run(dtype, tol, argmax_frac, swap=False):
         cache.enable_swap(64)
     w = LlamaWeights.random(cfg, dtype=dtype, seed=11)
     runner = HipModelRunner(cfg, w, PagedKVRunner(cache, bm))
-    ref = LlamaRef(cfg, weights_to_numpy(w))
+    ref = LlamaRef(cfg, weights_to_numpy(w), matmul=_np_matmul if cfg.hidden_size > 1024 else None)
     rng = np.random.default_rng(12)
     if swap:
         prompts = {"a": 45, "b": 7, "c": 70, "d": 20}
         max_new = {"a": 20, "b": 30, "c": 12, "d": 25}
         prio = {"a": Priority.Lowest, "b": Priority.High, "c": Priority.Medium, "d": Priority.Highest}
+    elif short:
+        prompts = {"a": 45, "b": 7, "c": 40}
+        max_new = {"a": 3, "b": 4, "c": 2}
+        prio = {r: Priority.Medium for r in prompts}
     else:
         prompts = {"a": 45, "b": 7, "c": 70}
         max_new = {"a": 6, "b": 9, "c": 4}
@@ -104,3 +114,13 @@ def test_model_step_with_swap_preemption_matches_reference():
     reference, which never preempts."""
     _run(torch.float32, 2e-4, 1.0, swap=True)
 
+
+def test_model_step_llama3_width_bf16_close_to_reference():
+    """Two layers at the Llama-3-8B widths the bench times (hidden 4096, 32
+    query / 8 KV heads of 128, intermediate 14336; the vocabulary cut to 1024):
+    the tiled gate|up, down and lm_head products, the fused QKV write and the
+    128-dim decode and prefill at their real shapes, against the oracle."""
+    from zealot_amd.model import LlamaConfig
+    cfg = LlamaConfig(vocab_size=1024, hidden_size=4096, intermediate_size=14336, num_layers=2, num_heads=32,
+                      num_kv_heads=8, head_dim=128)
+    _run(torch.bfloat16, 6e-2, 0.9, cfg=cfg, short=True)

@@ -60,6 +60,9 @@ def test_linear_is_x_times_w_transposed(m, k, n):
     got = oracle.linear(x, w)
     assert got.shape == (m, n)
     assert np.allclose(got, x.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-5, atol=1e-5)
+    # numpy's float32 product (the wide model test's matmul for LlamaRef): the
+    # same sums in another order
+    assert np.allclose(x @ w.T, got, rtol=1e-5, atol=1e-5)
     # a one-hot row picks a column of W^T
     e = np.zeros((1, k), np.float32)
     e[0, k - 1] = 1
