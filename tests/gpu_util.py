@@ -82,3 +82,39 @@ def max_abs_err(a, b) -> float:
 
 def announce(msg: str) -> None:
     print(f"[gpu-case] {msg}", flush=True)
+
+
+def torch_decode_ref(q, kpool, vpool, bt, lens, block_size, k_scales=None, v_scales=None, fp8=False):
+    """Plain PyTorch fp32 paged decode on the GPU, every sequence: out[n, h] =
+    softmax(q[n, h] . K^T / sqrt(D)) V over the sequence's first lens[n]
+    tokens of its pages, kv-head h // (H / Hkv) (grouped).  fp8 pools are
+    uint8 e4m3 codes dequantised with the per-(sequence, kv-head) scales.
+    For whole-batch checks of full-size runs; tests pin it against the oracle
+    on the sequences they sample."""
+    N, H, D = q.shape
+    Hkv = kpool.shape[1]
+    G = H // Hkv
+    out = torch.empty((N, H, D), dtype=torch.float32, device=q.device)
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        for n in range(N):
+            L = int(lens[n])
+            npg = (L + block_size - 1) // block_size
+            idx = torch.from_numpy(np.ascontiguousarray(bt[n, :npg]).astype(np.int64)).to(q.device)
+
+            def pages(pool, scales):
+                p = pool.index_select(0, idx)  # [npg, Hkv, BS, D]
+                p = p.view(torch.float8_e4m3fn).float() if fp8 else p.float()
+                p = p.permute(1, 0, 2, 3).reshape(Hkv, npg * block_size, D)[:, :L]
+                if scales is not None:
+                    p = p * scales[n].view(Hkv, 1, 1)
+                return p
+
+            K, V = pages(kpool, k_scales), pages(vpool, v_scales)
+            qn = q[n].float().view(Hkv, G, D)
+            s = torch.matmul(qn, K.transpose(1, 2).contiguous()) / math.sqrt(D)  # [Hkv, G, L]
+            out[n] = torch.matmul(torch.softmax(s, dim=-1), V).reshape(H, D)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    return out

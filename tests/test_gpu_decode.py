@@ -168,9 +168,11 @@ def test_fp8_kv_decode(src, lens):
 
 def test_c2_full_size_sampled_against_oracle():
     """C2 at full size (256 seqs, ctx U[512, 8192], bf16) on the GPU; 8 sampled
-    sequences are checked against the oracle on their own pages."""
+    sequences are checked against the oracle on their own pages, and all 256
+    against a plain PyTorch fp32 decode on the GPU, itself checked against
+    the oracle on the sampled ones."""
     from zealot_amd import ops
-    from tests.gpu_util import paged_tables
+    from tests.gpu_util import paged_tables, torch_decode_ref
     rng = np.random.default_rng(27)
     N, H, Hkv, D, BS = 256, 32, 8, 128, 16
     lens = rng.integers(512, 8193, N)
@@ -185,6 +187,8 @@ def test_c2_full_size_sampled_against_oracle():
     torch.cuda.synchronize()
     got = as_f32(to_host(out), oracle.BF16)
     assert np.all(np.isfinite(got))
+    tref = torch_decode_ref(q, kpool, vpool, bt, lens, BS).cpu().numpy()
+    assert max_abs_err(got, tref) <= 2e-2  # every sequence
     pick = rng.choice(N, 8, replace=False)
     for n in pick:
         L = int(lens[n])
@@ -195,6 +199,7 @@ def test_c2_full_size_sampled_against_oracle():
         bt1 = np.arange(len(pages), dtype=np.int32)[None, :]
         ref = _oracle(to_host(q[n:n + 1]), kp, vp, bt1, [L], oracle.BF16, oracle.BF16, "grouped")
         assert max_abs_err(got[n:n + 1], ref) <= 2e-2, int(n)
+        assert max_abs_err(tref[n:n + 1], ref) <= 1e-4, int(n)  # the torch decode is the oracle's
 
 
 @pytest.mark.parametrize("H,Hkv,D,dt", [(4, 4, 32, oracle.F32), (32, 8, 128, oracle.BF16)])

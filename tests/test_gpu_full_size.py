@@ -5,8 +5,10 @@ C5: 512 sequences, context U[1024, 16384], Llama-3-8B heads, K/V drawn in
 bf16, quantised to fp8-e4m3 on append with per-(sequence, kv-head) amax
 scales; the batched decode of all 512 is checked on 8 sampled sequences
 against the fp32 oracle on the unquantised bf16 inputs (5e-2) and against the
-oracle on the dequantised fp8 pages (2e-2); their pages are bit-exact with
-the oracle's quantiser.
+oracle on the dequantised fp8 pages (2e-2), their pages bit-exact with the
+oracle's quantiser, and on all 512 against a plain PyTorch fp32 decode of
+the dequantised pages (2e-2; that decode matches the oracle on the sampled
+ones to 1e-4).
 
 C4: 16 prefixes of 2048 + r tokens (r in [1, 15]: the tail block is partial)
 over 32 bf16 layers, 8 forks each, through the stateful KVCache: fork
@@ -22,7 +24,7 @@ import pytest
 import torch
 
 import oracle
-from tests.gpu_util import announce, as_f32, max_abs_err, paged_tables, to_dev, to_host
+from tests.gpu_util import announce, as_f32, max_abs_err, paged_tables, to_dev, to_host, torch_decode_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -68,6 +70,9 @@ def test_c5_fp8_full_size_sampled_against_oracle():
     torch.cuda.synchronize()
     got = as_f32(to_host(out), oracle.BF16)
     assert np.all(np.isfinite(got))
+    # all 512 against a plain PyTorch fp32 decode of the dequantised pages
+    tref = torch_decode_ref(q, kp, vp, bt, lens, BS, k_scales=ks, v_scales=vs, fp8=True).cpu().numpy()
+    assert max_abs_err(got, tref) <= 2e-2
     qh = to_host(q)
     ks_h, vs_h = to_host(ks), to_host(vs)
     scale = np.float32(1 / math.sqrt(D))
@@ -100,6 +105,7 @@ def test_c5_fp8_full_size_sampled_against_oracle():
         ref8 = oracle.paged_decode(q1, k8, v8, oracle.FP8, bt1, [Ln], Hkv, D, BS, scale, oracle.GROUPED,
                                    ks_ref, vs_ref, threads=8)
         assert max_abs_err(got[n:n + 1], ref8) <= 2e-2, n
+        assert max_abs_err(tref[n:n + 1], ref8) <= 1e-4, n  # the torch decode is the oracle's
 
 
 def test_c4_prefix_cow_full_size():
