@@ -14,7 +14,9 @@ C4: 16 prefixes of 2048 + r tokens (r in [1, 15]: the tail block is partial)
 over 32 bf16 layers, 8 forks each, through the stateful KVCache: fork
 refcounts, the copy-on-write of all 128 tails in all 64 pools (bit-exact),
 the 16 prefix subgroups of the shared decode, sampled (fork, layer, step)
-decodes against the oracle (2e-2) with their pages bit-exact, and every block
+decodes against the oracle (2e-2) with their pages bit-exact, the last step's
+decode of all 128 forks at the first and last layer against a plain PyTorch
+fp32 decode of their pages (2e-2), and every block
 back in the BlockManager at the end with old handles stale
 (src/block_manager.rs:125-164, src/kv_cache.rs:281-356)."""
 import math
@@ -150,7 +152,7 @@ def test_c4_prefix_cow_full_size():
            for _ in range(STEPS)]
     sample = [(int(rng.integers(0, n)), layer, step) for step, layer in
               ((0, 0), (0, 31), (1, 7), (2, 20), (3, 0), (3, 31))]
-    outs = {}
+    outs, whole = {}, {}
     out = torch.empty((n, H, D), dtype=torch.bfloat16, device="cuda")
     pos = [int(plen[p]) for p in parent]
     for step in range(STEPS):
@@ -166,6 +168,8 @@ def test_c4_prefix_cow_full_size():
             for i, sl, ss in sample:
                 if (sl, ss) == (layer, step):
                     outs[(i, sl, ss)] = out[i].clone()
+            if step == STEPS - 1 and layer in (0, L - 1):  # every fork, checked below
+                whole[layer] = out.clone()
         if step == 0:
             sg, pages = cache.decode_sharing()
             assert sg == P and pages == P * 128, (sg, pages)  # every subgroup shares its 128 full prefix pages
@@ -190,6 +194,24 @@ def test_c4_prefix_cow_full_size():
         ref = oracle.paged_decode(as_f32(to_host(qin[step][layer][i:i + 1]), oracle.BF16), kpg, vpg, oracle.BF16,
                                   bt1[None, :], [ctx], Hkv, D, BS, scale, threads=8)
         assert max_abs_err(as_f32(to_host(o)[None], oracle.BF16), ref) <= 2e-2, (i, layer, step)
+        if step == STEPS - 1 and layer in whole:  # pins the torch decode used for the whole batch
+            tref = torch_decode_ref(qin[step][layer][i:i + 1], cache.k_pool(layer), cache.v_pool(layer),
+                                    np.asarray(ids[:npg], np.int64)[None, :], [ctx], BS).cpu().numpy()
+            assert max_abs_err(tref, ref) <= 1e-4, (i, layer)
+    # the last step's decode of every fork at the first and last layer against
+    # a plain PyTorch fp32 decode over the forks' final pages (shared prefix
+    # pages, copied tails and the appended tokens)
+    ctxs = [int(plen[p]) + STEPS for p in parent]
+    npg_max = max((c + BS - 1) // BS for c in ctxs)
+    bt_all = np.full((n, npg_max), -1, np.int64)
+    for i, cid in enumerate(children):
+        ids = cache.seq_state(cid).block_ids
+        k = (ctxs[i] + BS - 1) // BS
+        bt_all[i, :k] = ids[:k]
+    for layer, o in whole.items():
+        tref = torch_decode_ref(qin[STEPS - 1][layer], cache.k_pool(layer), cache.v_pool(layer), bt_all, ctxs,
+                                BS).cpu().numpy()
+        assert max_abs_err(as_f32(to_host(o), oracle.BF16), tref) <= 2e-2, layer
     # release: the forks' references go, then the parents' last one bumps the generations
     for cid in children:
         cache.release_seq(cid)
