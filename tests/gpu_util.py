@@ -118,3 +118,34 @@ def torch_decode_ref(q, kpool, vpool, bt, lens, block_size, k_scales=None, v_sca
     finally:
         torch.backends.cuda.matmul.allow_tf32 = prev
     return out
+
+
+def torch_prefill_ref(q, kpool, vpool, block_ids, start, block_size):
+    """Plain PyTorch fp32 causal chunked prefill of one chunk on the GPU:
+    q [C, H, D] are the chunk's rows at positions start .. start + C - 1 of a
+    sequence whose pages are block_ids; row t attends keys 0 .. start + t
+    (grouped kv-heads).  Returns [C, H, D] float32."""
+    C, H, D = q.shape
+    Hkv = kpool.shape[1]
+    G = H // Hkv
+    ctx = start + C
+    npg = (ctx + block_size - 1) // block_size
+    idx = torch.as_tensor(np.asarray(block_ids[:npg], np.int64), device=q.device)
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        def pages(pool):
+            p = pool.index_select(0, idx).float()
+            return p.permute(1, 0, 2, 3).reshape(Hkv, npg * block_size, D)[:, :ctx]
+
+        K, V = pages(kpool), pages(vpool)
+        qn = q.float().view(C, Hkv, G, D).permute(1, 2, 0, 3).reshape(Hkv, G * C, D)
+        s = torch.matmul(qn, K.transpose(1, 2).contiguous()) / math.sqrt(D)  # [Hkv, G * C, ctx]
+        s = s.view(Hkv, G, C, ctx)
+        rows = torch.arange(C, device=q.device).view(C, 1)
+        keys = torch.arange(ctx, device=q.device).view(1, ctx)
+        s = s.masked_fill((keys > start + rows).view(1, 1, C, ctx), float("-inf"))
+        o = torch.matmul(torch.softmax(s, dim=-1).view(Hkv, G * C, ctx), V)  # [Hkv, G * C, D]
+        return o.view(Hkv, G, C, D).permute(2, 0, 1, 3).reshape(C, H, D)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev

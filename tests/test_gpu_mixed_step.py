@@ -155,3 +155,77 @@ def test_mixed_step_errors_write_nothing():
     with pytest.raises(RuntimeError, match="fewer tokens"):
         cache.attention_batch(1, ["x", "y"], [1, 1], q)
     torch.cuda.synchronize()
+
+
+def test_mixed_step_at_bench_shape_every_row():
+    """The bench's runner step at its full shape (252 decodes with contexts
+    U[512, 8192] and 4 prompt chunks of 512 tokens after U[0, 4096) cached
+    ones, 32/8 heads of 128, bf16): one write_batch + attention_batch, every
+    decode row against a plain PyTorch fp32 decode and every chunk row against
+    a plain PyTorch fp32 causal prefill over the cache's pages (2e-2); both
+    references pinned to the oracle on sampled rows (1e-4)."""
+    import zealot_amd as ze
+    from zealot_amd import KVCache
+    from zealot_amd.kv_cache import SeqBatch
+    from tests.gpu_util import torch_decode_ref, torch_prefill_ref
+    ND, NC, C, H, Hkv, D, BS = 252, 4, 512, 32, 8, 128, 16
+    rng = np.random.default_rng(64)
+    dec_ctx = rng.integers(512, 8193, ND)
+    starts = rng.integers(0, 4096, NC)
+    total = [int(x) for x in dec_ctx] + [int(s) + C for s in starts]
+    pages = [(t + BS - 1) // BS for t in total]
+    nb = sum(pages) + 16
+    announce(f"mixed step at bench shape: {ND} decodes + {NC} chunks of {C}, {nb} blocks")
+    bm = ze.BlockManager(nb, BS)
+    cache = KVCache(nb, BS, 1, Hkv, D, dtype=torch.bfloat16, max_seqs=ND + NC, max_blocks_per_seq=max(pages))
+    ids = [f"d{i}" for i in range(ND)] + [f"c{i}" for i in range(NC)]
+    for sid, p in zip(ids, pages):
+        cache.register_seq(sid, p)
+        for _ in range(p):
+            cache.alloc_block(sid, bm)
+    before = [int(x) - 1 for x in dec_ctx] + [int(s) for s in starts]
+    g = torch.Generator(device="cuda").manual_seed(64)
+    allb = SeqBatch(ids)
+    T0 = sum(before)
+    k0 = torch.randn((T0, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    v0 = torch.randn((T0, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    cache.write_batch(0, allb, before, k0, v0)
+    del k0, v0
+    nt = [1] * ND + [C] * NC
+    T = sum(nt)
+    k = torch.randn((T, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((T, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn((T, H, D), generator=g, device="cuda").to(torch.bfloat16)
+    cache.write_batch(0, allb, nt, k, v)
+    out = cache.attention_batch(0, allb, nt, q)
+    torch.cuda.synchronize()
+    got = as_f32(to_host(out), oracle.BF16)
+    assert np.all(np.isfinite(got))
+    blocks = [cache.seq_state(s).block_ids for s in ids]
+    bt = np.full((ND, max(pages)), -1, np.int64)
+    for i in range(ND):
+        bt[i, :pages[i]] = blocks[i][:pages[i]]
+    dref = torch_decode_ref(q[:ND], cache.k_pool(0), cache.v_pool(0), bt, dec_ctx, BS).cpu().numpy()
+    assert max_abs_err(got[:ND], dref) <= 2e-2
+    scale = np.float32(1 / math.sqrt(D))
+    for i in rng.choice(ND, 3, replace=False):  # the torch decode is the oracle's
+        L = int(dec_ctx[i])
+        idx = torch.tensor(bt[i, :pages[i]], dtype=torch.int64, device="cuda")
+        kp, vp = to_host(cache.k_pool(0).index_select(0, idx)), to_host(cache.v_pool(0).index_select(0, idx))
+        ref = oracle.paged_decode(as_f32(to_host(q[i:i + 1]), oracle.BF16), kp, vp, oracle.BF16,
+                                  np.arange(pages[i], dtype=np.int32)[None, :], [L], Hkv, D, BS, scale, threads=8)
+        assert max_abs_err(dref[i:i + 1], ref) <= 1e-4, int(i)
+    row = ND
+    for c in range(NC):
+        sid, st = ND + c, int(starts[c])
+        pref = torch_prefill_ref(q[row:row + C], cache.k_pool(0), cache.v_pool(0), blocks[sid], st, BS).cpu().numpy()
+        assert max_abs_err(got[row:row + C], pref) <= 2e-2, c
+        if c == 0:  # the torch prefill is the oracle's, on the chunk's first 8 rows
+            npg = (st + 8 + BS - 1) // BS
+            idx = torch.tensor(blocks[sid][:npg], dtype=torch.int64, device="cuda")
+            kp, vp = to_host(cache.k_pool(0).index_select(0, idx)), to_host(cache.v_pool(0).index_select(0, idx))
+            ref = oracle.paged_prefill(as_f32(to_host(q[row:row + 8]), oracle.BF16), kp, vp, oracle.BF16,
+                                       np.arange(npg, dtype=np.int32)[None, :], np.array([0, 8], np.int64), [st],
+                                       Hkv, D, BS, scale, True, oracle.GROUPED)
+            assert max_abs_err(pref[:8], ref) <= 1e-4
+        row += C
