@@ -3,7 +3,9 @@ the oracle's or_paged_prefill on the same seeded inputs: causal (row t of a
 chunk after `start` cached tokens sees positions [0, start + t],
 attention.cu:117-121) and non-causal (CpuAttention::forward), both GQA
 mappings, bf16 and fp8 pools, f32 and bf16 queries, ragged and empty chunks,
-sentinel-cut tables, and the C3 shape at full size (sampled rows).
+sentinel-cut tables, and C3's chunks at full size (every row against a
+PyTorch fp32 causal prefill pinned to the oracle, sampled rows against the
+oracle).
 Tolerance: 2e-2 absolute (bf16 products / bf16 outputs)."""
 import math
 
@@ -101,25 +103,36 @@ def test_prefill_sentinel_cuts_context():
 
 
 def test_prefill_c3_shape_sampled_rows():
-    """C3's chunk shape (512 tokens at unaligned offsets < 4096, 32/8 heads,
-    D = 128, bf16; 16 of its 64 sequences) in one call; 4 sequences x 3 x 16
-    rows are checked against the oracle (a causal sub-chunk of rows t0.. is the
-    chunk that starts at start + t0)."""
+    """C3's chunks at full size (64 sequences, 512 tokens at unaligned offsets
+    < 4096, 32/8 heads, D = 128, bf16) in one call; 4 sequences x 3 x 16 rows
+    are checked against the oracle (a causal sub-chunk of rows t0.. is the
+    chunk that starts at start + t0), and every row of every chunk against a
+    plain PyTorch fp32 causal prefill, itself within 1e-4 of the oracle on
+    those rows."""
+    from tests.gpu_util import torch_prefill_ref
     rng = np.random.default_rng(12)
-    H, Hkv, D, N, C = 32, 8, 128, 16, 512
+    H, Hkv, D, N, C = 32, 8, 128, 64, 512
     starts = rng.integers(0, 4096, N)
     starts[starts % 16 == 0] += 1
     chunks = [C] * N
     q, kp, vp, kvdt, bt, cu, ks, vs = _case(13, H, Hkv, D, list(starts), chunks)
     announce("prefill C3 shape")
     out = _run(q, kp, vp, bt, cu, list(starts), True, "grouped", None, None)
+    got = as_f32(out, oracle.BF16)
+    qd, kd, vd = to_dev(q), to_dev(kp), to_dev(vp)
+    tref = {}
+    for n in range(N):
+        a, b = int(cu[n]), int(cu[n + 1])
+        tref[n] = torch_prefill_ref(qd[a:b], kd, vd, bt[n], int(starts[n]), 16).cpu().numpy()
+        assert max_abs_err(got[a:b], tref[n]) <= 2e-2, n
     scale = np.float32(1 / math.sqrt(D))
-    for n in (0, 5, 10, 15):
+    for n in (0, 21, 42, 63):
         for t0 in (0, 255, 496):
             rows = slice(int(cu[n]) + t0, int(cu[n]) + t0 + 16)
             ref = oracle.paged_prefill(as_f32(q[rows], oracle.BF16), kp, vp, kvdt, bt[n:n + 1],
                                        np.array([0, 16], np.int64), [int(starts[n]) + t0], Hkv, D, 16, scale, True)
-            assert max_abs_err(as_f32(out[rows], oracle.BF16), ref) <= 2e-2, (n, t0)
+            assert max_abs_err(got[rows], ref) <= 2e-2, (n, t0)
+            assert max_abs_err(tref[n][t0:t0 + 16], ref) <= 1e-4, (n, t0)  # the torch prefill is the oracle's
 
 
 def test_prefill_one_row_chunks_equal_decode():
