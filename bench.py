@@ -651,8 +651,11 @@ def bench_model(args, torch, lib):
     D = 128, hidden 4096, intermediate 14336, vocab 128256, bf16, random
     weights) for 64 sequences with contexts U[512, 8192], through
     HipModelRunner: embedding, per layer fused-add RMSNorm, the fused QKV /
-    o / gate-up / down projections on hipBLASLt, SiLU*up, one KV write and
-    one paged decode for the batch, final norm and f32 lm_head logits.  Each
+    o / gate-up / down projections (hipBLASLt or the weight-streaming kernel,
+    whichever the first call timed faster; gate|up, down and lm_head on tiled
+    weights), SiLU*up in the gate|up epilogue, the KV write with the QKV
+    split-k sums folded in and one paged decode for the batch, final norm and
+    f32 lm_head logits.  Each
     step appends one token per sequence (contexts grow by the step count,
     < 1 %)."""
     import ctypes
