@@ -133,6 +133,17 @@ int zk_linear_silu_mul_tiled(const void *x, const void *wt, void *act, int64_t m
  * fused_rows}. */
 int zk_linear_tiled_choice(int64_t m, int64_t n, int64_t k, zk_dtype out_dtype, int choice[4]);
 
+/* No counterpart in the reference.  Pins the split-k configuration that
+ * zk_linear_rms_norm[_tiled] and zk_cache_write_batch_qkv fold for the plan
+ * an earlier call made for (m, n, k, dtypes; tiled: the tiled plan):
+ * fused_splits > 1 ranges of k over tiles of fused_rows weight rows, or
+ * fused_splits 0 for none (the projection, then its consumer).  For callers
+ * that fix a configuration they measured, and for tests that must run the
+ * folded kernels whatever the tuning chose.  ZK_ERR_INVALID_ARGUMENT if no
+ * plan exists yet or the configuration does not fit the shape. */
+int zk_linear_pin_split(int64_t m, int64_t n, int64_t k, zk_dtype in_dtype, zk_dtype out_dtype, int tiled,
+                        int fused_splits, int fused_rows);
+
 /* On (default): the first call of each (m, n, k, dtypes) times hipBLASLt's
  * candidate algorithms on its operands (synchronizing the stream once) and
  * keeps the fastest.  Off: the heuristic's first choice, no synchronization

@@ -149,3 +149,48 @@ def torch_prefill_ref(q, kpool, vpool, block_ids, start, block_size):
         return o.view(Hkv, G, C, D).permute(2, 0, 1, 3).reshape(C, H, D)
     finally:
         torch.backends.cuda.matmul.allow_tf32 = prev
+
+
+def torch_model_decode_ref(cfg, w, tok, ctx_kv):
+    """Plain PyTorch fp32 restatement of one decode step of
+    zealot_amd.model.HipModelRunner.forward (src/cuda_runner.rs:271-660 op
+    order) on the GPU: one step token per sequence (tok [N] int64), each
+    attending its context K/V from ctx_kv(layer, n) -> (K, V), float32
+    [Hkv, tokens, D] on the device, then its own K/V from the step's
+    projection.  Weights are the model's (TiledWeight read back row-major),
+    every activation stays fp32.  Returns the fp32 logits [N, vocab].
+    Whole-batch check of full-size model steps; tests pin it against
+    oracle/llama_ref.py on a small model."""
+    from zealot_amd import dense
+    H, Hkv, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    G = H // Hkv
+    N = tok.numel()
+
+    def f32(t):
+        return (t.rowmajor() if isinstance(t, dense.TiledWeight) else t).float()
+
+    def rms(x, wt):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.rms_eps) * wt.float()
+
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        resid = w.embedding.float()[tok]
+        for layer, lw in enumerate(w.layers):
+            qkv = rms(resid, lw.attn_norm) @ f32(lw.qkv).T
+            q, kn, vn = qkv[:, :H * D], qkv[:, H * D:(H + Hkv) * D], qkv[:, (H + Hkv) * D:]
+            attn = torch.empty((N, H * D), dtype=torch.float32, device=tok.device)
+            for n in range(N):
+                K, V = ctx_kv(layer, n)
+                K = torch.cat([K, kn[n].view(Hkv, 1, D)], 1)
+                V = torch.cat([V, vn[n].view(Hkv, 1, D)], 1)
+                s = torch.matmul(q[n].view(Hkv, G, D), K.transpose(1, 2).contiguous()) / math.sqrt(D)
+                attn[n] = torch.matmul(torch.softmax(s, -1), V).reshape(H * D)
+            resid = resid + attn @ f32(lw.o).T
+            normed = rms(resid, lw.ffn_norm)
+            gate, up = dense.split_gate_up(f32(lw.gate_up))
+            act = torch.nn.functional.silu(normed @ gate.T) * (normed @ up.T)
+            resid = resid + act @ f32(lw.down).T
+        return rms(resid, w.final_norm) @ f32(w.lm_head).T
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev

@@ -3,7 +3,7 @@
  * (benches/block_manager.rs:35-134): a 4096-block pool of 16-token blocks, the
  * timed operations in batches of 256 with their setup untimed.
  *
- *   gcc -O2 -Iinclude zealot_amd/bm_microbench.c -Lzealot_amd -lzealot_kv \
+ *   gcc -O2 -Iinclude tests/native/bm_microbench.c -Lzealot_amd -lzealot_kv \
  *       -Wl,-rpath,$PWD/zealot_amd -o bm_microbench && ./bm_microbench [rounds]
  *
  * Prints one line per case: name and nanoseconds per operation (the median

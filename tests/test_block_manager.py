@@ -267,7 +267,7 @@ def test_forged_handle_for_free_block_is_rejected():
 
 
 def test_bm_microbench_builds_and_runs(tmp_path):
-    """The C-ABI latency bench (zealot_amd/bm_microbench.c) builds with gcc
+    """The C-ABI latency bench (tests/native/bm_microbench.c) builds with gcc
     against the header and the library and reports every case."""
     import os
     import shutil
@@ -279,7 +279,7 @@ def test_bm_microbench_builds_and_runs(tmp_path):
     lib_dir = os.path.join(root, "zealot_amd")
     exe = str(tmp_path / "bm_microbench")
     subprocess.run([gcc, "-O2", "-Wall", "-I", os.path.join(root, "include"),
-                    os.path.join(lib_dir, "bm_microbench.c"), "-L", lib_dir, "-lzealot_kv",
+                    os.path.join(root, "tests", "native", "bm_microbench.c"), "-L", lib_dir, "-lzealot_kv",
                     f"-Wl,-rpath,{lib_dir}", "-o", exe], check=True)
     out = subprocess.run([exe, "50"], check=True, capture_output=True, text=True).stdout.split()
     got = dict(zip(out[0::2], map(float, out[1::2])))

@@ -301,6 +301,49 @@ def test_linear_rms_norm_is_the_unfused_sequence_bit_for_bit(m, n, k, with_res):
     assert np.abs(gotf - want).max() <= 3e-2 * np.abs(want).max()
 
 
+@pytest.mark.parametrize("m,n,k,splits,rows", [(64, 4096, 4096, 4, 64), (33, 1024, 2048, 8, 128), (7, 4096, 14336, 7, 64)])
+def test_linear_rms_norm_pinned_split_is_the_unfused_sequence_bit_for_bit(m, n, k, splits, rows):
+    """The plan pinned to a split of k (zk_linear_pin_split), so the norm
+    kernel that adds the split sums (rms_norm_partials) runs whatever the
+    tuning chose: bit for bit the weight-streaming kernel with that split,
+    then zk_rms_norm, new residual included."""
+    from zealot_amd import dense
+    rng = np.random.default_rng(m * 7 + n + k)
+    x = to_dev(normal(rng, (m, k), oracle.BF16))
+    w = to_dev(oracle.bf16_bits_from_f32((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)).reshape(n, k))
+    g = to_dev(normal(rng, (n,), oracle.BF16))
+    r0 = to_dev(normal(rng, (m, n), oracle.BF16))
+    announce(f"linear_rms_norm pinned split {m}x{n}x{k} splits={splits} rows={rows}")
+    dense.linear_rms_norm(x, w, g, 1e-5, residual=r0.clone())  # makes the plan
+    before = dense.linear_choice(m, n, k)
+    dense.pin_split(m, n, k, splits, rows)
+    try:
+        assert dense.linear_choice(m, n, k)["fused_splits"] == splits
+        res = r0.clone()
+        out, _ = dense.linear_rms_norm(x, w, g, 1e-5, residual=res, residual_out=res)
+        y = dense.linear_skinny(x, w, splits, rows)
+        ref_out, ref_res = dense.rms_norm(y, g, 1e-5, residual=r0.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+        assert torch.equal(res.view(torch.int16), ref_res.view(torch.int16))
+    finally:
+        dense.pin_split(m, n, k, before["fused_splits"], before["fused_rows"])
+
+
+def test_pin_split_rejects_what_does_not_fit():
+    from zealot_amd import dense
+    from zealot_amd._lib import ZealotError
+    x = torch.zeros((8, 1024), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((512, 1024), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ZealotError, match="no plan"):
+        dense.pin_split(8, 512, 3072, 2, 64)
+    dense.linear(x, w)
+    with pytest.raises(ZealotError, match="does not fit"):
+        dense.pin_split(8, 512, 1024, 16, 64)  # k % (128 * 16) != 0
+    with pytest.raises(ZealotError, match="does not fit"):
+        dense.pin_split(8, 512, 1024, 1, 64)   # no split
+
+
 @pytest.mark.parametrize("m,inter,k", [(64, 14336, 4096), (7, 1024, 512), (33, 512, 256), (200, 512, 1024)])
 def test_linear_silu_mul_is_the_unfused_sequence_bit_for_bit(m, inter, k):
     """zk_linear_silu_mul (gate and up rows interleaved in blocks of 16)

@@ -11,14 +11,17 @@ the dequantised pages (2e-2; that decode matches the oracle on the sampled
 ones to 1e-4).
 
 C4: 16 prefixes of 2048 + r tokens (r in [1, 15]: the tail block is partial)
-over 32 bf16 layers, 8 forks each, through the stateful KVCache: fork
-refcounts, the copy-on-write of all 128 tails in all 64 pools (bit-exact),
-the 16 prefix subgroups of the shared decode, sampled (fork, layer, step)
-decodes against the oracle (2e-2) with their pages bit-exact, the last step's
-decode of all 128 forks at the first and last layer against a plain PyTorch
-fp32 decode of their pages (2e-2), and every block
-back in the BlockManager at the end with old handles stale
-(src/block_manager.rs:125-164, src/kv_cache.rs:281-356)."""
+over 32 bf16 layers, 8 forks each, through the stateful KVCache, for all 64
+decode steps of append + paged attention: fork refcounts, the copy-on-write
+of all 128 tails in all 64 pools (bit-exact), the 16 prefix subgroups of the
+shared decode, every block a fork gains on the way (a fresh private block
+with one reference whenever its position crosses a block boundary, about
+four per fork), sampled (fork, layer, step) decodes spread over the 64 steps
+against the oracle (2e-2) with their pages bit-exact, the decode of all 128
+forks at the first and last layer on steps 0, 15, 31, 47 and 63 against a
+plain PyTorch fp32 decode of their pages (2e-2), and every block back in the
+BlockManager at the end with old handles stale (src/block_manager.rs:108-164,
+src/kv_cache.rs:281-356)."""
 import math
 
 import numpy as np
@@ -115,11 +118,13 @@ def test_c4_prefix_cow_full_size():
     from zealot_amd import KVCache
     from zealot_amd.kv_cache import SeqBatch
     P, F, L, H, Hkv, D, BS = 16, 8, 32, 32, 8, 128, 16
-    STEPS = 4
+    STEPS = 64
+    WHOLE = (0, 15, 31, 47, 63)  # steps whose whole batch is checked at the first and last layer
     rng = np.random.default_rng(44)
     plen = 2048 + rng.integers(1, BS, P)
     MB = (int(plen.max()) + STEPS + BS - 1) // BS + 1
-    NB = sum((int(x) + BS - 1) // BS for x in plen) + P * F * 2 + 64
+    grown = (STEPS + BS - 1) // BS + 1  # blocks a fork may gain: its tail copy and the steps' new blocks
+    NB = sum((int(x) + BS - 1) // BS for x in plen) + P * F * grown + 64
     bm = ze.BlockManager(NB, BS)
     cache = KVCache(NB, BS, L, Hkv, D, dtype=torch.bfloat16, max_seqs=P * (F + 1), max_blocks_per_seq=MB)
     announce(f"C4 full size: {P} prefixes x {int(plen.min())}..{int(plen.max())} tokens, {L} layers, "
@@ -150,15 +155,26 @@ def test_c4_prefix_cow_full_size():
            for _ in range(STEPS)]
     qin = [[torch.randn((n, H, D), generator=g, device="cuda").to(torch.bfloat16) for _ in range(L)]
            for _ in range(STEPS)]
+    # sampled decodes spread over the steps, late ones included (step >= 40:
+    # every fork has crossed at least two block boundaries by then)
     sample = [(int(rng.integers(0, n)), layer, step) for step, layer in
-              ((0, 0), (0, 31), (1, 7), (2, 20), (3, 0), (3, 31))]
+              ((0, 0), (0, 31), (3, 7), (12, 20), (17, 0), (29, 31), (40, 5), (46, 31), (55, 0), (63, 17),
+               (63, 31))]
     outs, whole = {}, {}
     out = torch.empty((n, H, D), dtype=torch.bfloat16, device="cuda")
     pos = [int(plen[p]) for p in parent]
+    private = [set() for _ in children]  # blocks each fork gained by alloc_block
     for step in range(STEPS):
         for i, cid in enumerate(children):  # a block for the token if the tail is full
             if pos[i] % BS == 0:
+                before = cache.seq_state(cid).block_ids
                 cache.alloc_block(cid, bm)
+                ids = cache.seq_state(cid).block_ids
+                # kv_cache.rs:107-130 / block_manager.rs:108-122: one fresh block
+                # at the table's end, one reference, the earlier entries unchanged
+                assert ids[:-1] == before and len(ids) == pos[i] // BS + 1, (cid, step)
+                assert bm.refcount(ids[-1]) == 1 and ids[-1] not in private[i], (cid, step)
+                private[i].add(ids[-1])
         for layer in range(L):
             cache.append_kv_batch(layer, batch, kin[step][layer], vin[step][layer])
             if step == 0 and layer == 0:
@@ -168,13 +184,30 @@ def test_c4_prefix_cow_full_size():
             for i, sl, ss in sample:
                 if (sl, ss) == (layer, step):
                     outs[(i, sl, ss)] = out[i].clone()
-            if step == STEPS - 1 and layer in (0, L - 1):  # every fork, checked below
-                whole[layer] = out.clone()
+            if step in WHOLE and layer in (0, L - 1):  # every fork, checked below
+                whole[(step, layer)] = out.clone()
         if step == 0:
             sg, pages = cache.decode_sharing()
             assert sg == P and pages == P * 128, (sg, pages)  # every subgroup shares its 128 full prefix pages
         pos = [x + 1 for x in pos]
+        for i, cid in enumerate(children):
+            st = cache.seq_state(cid)
+            assert st.cached_tokens == pos[i] and st.block_offset == pos[i] % BS, (cid, step)
     torch.cuda.synchronize()
+    # every fork: the shared full prefix blocks, its copied tail, then the
+    # blocks it gained, all private and distinct across forks
+    for i, cid in enumerate(children):
+        ids = cache.seq_state(cid).block_ids
+        t = int(plen[parent[i]]) // BS
+        assert ids[:t] == pblocks[parent[i]][:t]
+        assert len(ids) == (pos[i] + BS - 1) // BS and set(ids[t + 1:]) == private[i], cid
+        assert len(private[i]) == (pos[i] - 1) // BS - t, cid  # (pos - 1) // BS - t boundaries crossed
+        assert all(bm.refcount(b) == 1 for b in ids[t:]), cid
+    gained = [b for s_ in private for b in s_] + [cache.seq_state(c).block_ids[int(plen[parent[i]]) // BS]
+                                                   for i, c in enumerate(children)]
+    assert len(set(gained)) == len(gained)
+    # positions 2048 + r .. 2111 + r (r in [1, 15]) cross 2064, 2080, 2096 and 2112: four blocks per fork
+    assert sum(len(s_) for s_ in private) == 4 * n
     scale = np.float32(1 / math.sqrt(D))
     for (i, layer, step), o in outs.items():
         p = parent[i]
@@ -194,24 +227,23 @@ def test_c4_prefix_cow_full_size():
         ref = oracle.paged_decode(as_f32(to_host(qin[step][layer][i:i + 1]), oracle.BF16), kpg, vpg, oracle.BF16,
                                   bt1[None, :], [ctx], Hkv, D, BS, scale, threads=8)
         assert max_abs_err(as_f32(to_host(o)[None], oracle.BF16), ref) <= 2e-2, (i, layer, step)
-        if step == STEPS - 1 and layer in whole:  # pins the torch decode used for the whole batch
-            tref = torch_decode_ref(qin[step][layer][i:i + 1], cache.k_pool(layer), cache.v_pool(layer),
-                                    np.asarray(ids[:npg], np.int64)[None, :], [ctx], BS).cpu().numpy()
-            assert max_abs_err(tref, ref) <= 1e-4, (i, layer)
-    # the last step's decode of every fork at the first and last layer against
-    # a plain PyTorch fp32 decode over the forks' final pages (shared prefix
-    # pages, copied tails and the appended tokens)
-    ctxs = [int(plen[p]) + STEPS for p in parent]
-    npg_max = max((c + BS - 1) // BS for c in ctxs)
-    bt_all = np.full((n, npg_max), -1, np.int64)
+        # pins the torch decode used for the whole batch
+        tref = torch_decode_ref(qin[step][layer][i:i + 1], cache.k_pool(layer), cache.v_pool(layer),
+                                np.asarray(ids[:npg], np.int64)[None, :], [ctx], BS).cpu().numpy()
+        assert max_abs_err(tref, ref) <= 1e-4, (i, layer, step)
+    # the decode of every fork at the first and last layer on the WHOLE steps
+    # against a plain PyTorch fp32 decode over the forks' final pages (shared
+    # prefix pages, copied tails, the gained blocks and the appended tokens):
+    # later steps only wrote positions past that step's context
+    bt_all = np.full((n, MB), -1, np.int64)
     for i, cid in enumerate(children):
         ids = cache.seq_state(cid).block_ids
-        k = (ctxs[i] + BS - 1) // BS
-        bt_all[i, :k] = ids[:k]
-    for layer, o in whole.items():
-        tref = torch_decode_ref(qin[STEPS - 1][layer], cache.k_pool(layer), cache.v_pool(layer), bt_all, ctxs,
+        bt_all[i, :len(ids)] = ids
+    for (step, layer), o in sorted(whole.items()):
+        ctxs = [int(plen[p]) + step + 1 for p in parent]
+        tref = torch_decode_ref(qin[step][layer], cache.k_pool(layer), cache.v_pool(layer), bt_all, ctxs,
                                 BS).cpu().numpy()
-        assert max_abs_err(as_f32(to_host(o), oracle.BF16), tref) <= 2e-2, layer
+        assert max_abs_err(as_f32(to_host(o), oracle.BF16), tref) <= 2e-2, (step, layer)
     # release: the forks' references go, then the parents' last one bumps the generations
     for cid in children:
         cache.release_seq(cid)

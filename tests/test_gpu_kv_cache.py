@@ -26,6 +26,20 @@ def _ctx(cache, layer, sid, L):
     return k, v
 
 
+def _decode_vs_oracle(cache, layer, ids, lens, rng, H, D, BS):
+    """One decode of every sequence at `layer` through the KVCache, within 1e-5
+    of the fp32 oracle (src/attention/mod.rs:64-98) over the pages as they are."""
+    q = normal(rng, (len(ids), H, D), oracle.F32)
+    out = to_host(cache.paged_decode(layer, ids, to_dev(q)))
+    kp, vp = to_host(cache.k_pool(layer)), to_host(cache.v_pool(layer))
+    bt = -np.ones((len(ids), 16), np.int32)
+    for i, sid in enumerate(ids):
+        b = cache.seq_state(sid).block_ids
+        bt[i, :len(b)] = b
+    ref = oracle.paged_decode(q, kp, vp, oracle.F32, bt, lens, H, D, BS, np.float32(1 / math.sqrt(D)))
+    assert max_abs_err(out, ref) <= 1e-5, (layer, lens)
+
+
 def test_c1_plumbing_through_kvcache():
     import zealot_amd as ze
     from zealot_amd import KVCache
@@ -36,6 +50,7 @@ def test_c1_plumbing_through_kvcache():
     cache = KVCache(NB, BS, L, H, D, dtype=torch.float32, max_seqs=8, max_blocks_per_seq=16)
     written = {sid: {l: ([], []) for l in range(L)} for sid in prompts}
     announce("kvcache C1 plumbing")
+    ids = list(prompts)
     for sid, p in prompts.items():
         cache.register_seq(sid, 16)
         for _ in range((p + 8 + BS - 1) // BS):
@@ -57,23 +72,16 @@ def test_c1_plumbing_through_kvcache():
                 written[sid][layer][1].append(v)
             st = cache.seq_state(sid)
             assert st.cached_tokens == p + step + 1 and st.block_offset == (p + step + 1) % BS
+        # the decode of every layer after each step (model_runner_cpu.rs:241-250
+        # attends the last row over the context so far)
+        for layer in range(L):
+            _decode_vs_oracle(cache, layer, ids, [prompts[s] + step + 1 for s in ids], rng, H, D, BS)
     torch.cuda.synchronize()
-    ids = list(prompts)
     for layer in range(L):
         for sid, p in prompts.items():
             k, v = _ctx(cache, layer, sid, p + 8)
             assert np.array_equal(k, np.concatenate(written[sid][layer][0]))
             assert np.array_equal(v, np.concatenate(written[sid][layer][1]))
-        q = normal(rng, (4, H, D), oracle.F32)
-        out = to_host(cache.paged_decode(layer, ids, to_dev(q)))
-        kp, vp = to_host(cache.k_pool(layer)), to_host(cache.v_pool(layer))
-        bt = -np.ones((4, 16), np.int32)
-        for i, sid in enumerate(ids):
-            b = cache.seq_state(sid).block_ids
-            bt[i, :len(b)] = b
-        ref = oracle.paged_decode(q, kp, vp, oracle.F32, bt, [prompts[s] + 8 for s in ids], H, D, BS,
-                                  np.float32(1 / math.sqrt(D)))
-        assert max_abs_err(out, ref) <= 1e-5
     # errors follow kv_cache.rs
     with pytest.raises(RuntimeError, match="unknown seq nope"):
         cache.seq_state("nope")

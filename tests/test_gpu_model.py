@@ -11,12 +11,14 @@ GEMMs and attention); bf16 -- within 6e-2 of the largest |logit| (bf16
 activations between ops, f32 reference) and the same argmax on at least 90 %
 of the rows.  A third run squeezes four requests into eight blocks so the
 scheduler preempts by swap (zk_cache_swap_out / _in through the runner) and
-by recompute; the logits must not notice."""
+by recompute; the logits must not notice.  At the Llama-3-8B widths, one run
+also pins the PyTorch fp32 restatement of the full-size model test against
+the oracle, and one takes prefill steps of more than 64 rows."""
 import numpy as np
 import pytest
 import torch
 
-from tests.gpu_util import announce
+from tests.gpu_util import announce, torch_model_decode_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -27,7 +29,13 @@ def _np_matmul(x, w):
     return np.ascontiguousarray(x, np.float32) @ np.asarray(w, np.float32).T
 
 
-def _run(dtype, tol, argmax_frac, swap=False, cfg=None, short=False):
+def _run(dtype, tol, argmax_frac, swap=False, cfg=None, short=False, long_prefill=False, pin_torch_ref=False):
+    """long_prefill: prefill steps of more than 64 rows (chunks of 128, up
+    to 256 prefill tokens a step), so the tiled weights' products run on
+    their row-major copies.  pin_torch_ref: on the first all-decode step, the
+    PyTorch fp32 restatement the full-size model test uses
+    (tests.gpu_util.torch_model_decode_ref) is checked against the oracle on
+    the oracle's own context K/V (1e-4 of the largest |logit|)."""
     import zealot_amd as ze
     from oracle.llama_ref import LlamaRef, weights_to_numpy
     from zealot_amd import KVCache, PagedKVRunner, Priority, Scheduler, SchedulerConfig
@@ -37,9 +45,11 @@ def _run(dtype, tol, argmax_frac, swap=False, cfg=None, short=False):
     # with swap: 8 blocks for four requests, so the scheduler preempts by
     # swap (and once by recompute) while the reference keeps every sequence
     NB, BS = (8, 16) if swap else (64, 16)
+    max_prefill, chunk = (256, 128) if long_prefill else (64, 32)
     bm = ze.BlockManager(NB, BS)
-    sched = Scheduler(SchedulerConfig(max_num_seqs=4, block_size=BS, num_gpu_blocks=NB, max_prefill_tokens=64,
-                                      prefill_chunk_size=32, swap_blocks=64 if swap else 0), block_manager=bm)
+    sched = Scheduler(SchedulerConfig(max_num_seqs=4, block_size=BS, num_gpu_blocks=NB,
+                                      max_prefill_tokens=max_prefill, prefill_chunk_size=chunk,
+                                      swap_blocks=64 if swap else 0), block_manager=bm)
     cache = KVCache(NB, BS, cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, dtype=dtype, max_seqs=8,
                     max_blocks_per_seq=NB)
     if swap:
@@ -52,6 +62,10 @@ def _run(dtype, tol, argmax_frac, swap=False, cfg=None, short=False):
         prompts = {"a": 45, "b": 7, "c": 70, "d": 20}
         max_new = {"a": 20, "b": 30, "c": 12, "d": 25}
         prio = {"a": Priority.Lowest, "b": Priority.High, "c": Priority.Medium, "d": Priority.Highest}
+    elif long_prefill:
+        prompts = {"a": 300, "b": 7, "c": 150}
+        max_new = {"a": 3, "b": 4, "c": 2}
+        prio = {r: Priority.Medium for r in prompts}
     elif short:
         prompts = {"a": 45, "b": 7, "c": 40}
         max_new = {"a": 3, "b": 4, "c": 2}
@@ -62,7 +76,7 @@ def _run(dtype, tol, argmax_frac, swap=False, cfg=None, short=False):
         prio = {r: Priority.Medium for r in prompts}
     for rid, p in prompts.items():
         sched.add(sched.make_sequence(rid, list(rng.integers(0, cfg.vocab_size, p)), max_new[rid], prio[rid]))
-    worst, agree, rows, steps, swaps = 0.0, 0, 0, 0, 0
+    worst, agree, rows, steps, swaps, widest, pinned = 0.0, 0, 0, 0, 0, 0, False
     while not sched.is_idle():
         steps += 1
         assert steps < 100
@@ -72,8 +86,25 @@ def _run(dtype, tol, argmax_frac, swap=False, cfg=None, short=False):
         swaps += len(out.swapped_out)
         announce(f"model {dtype} step {steps}: {[(e.request_id, e.num_tokens, e.tokens_before) for e in out.batch]}")
         entries = [(e.request_id, e.step_input(), e.tokens_before) for e in out.batch]
+        widest = max(widest, sum(len(x[1]) for x in entries))
+        pin_now = pin_torch_ref and not pinned and all(not e.is_prefill() for e in out.batch)
+        if pin_now:  # the oracle's context K/V before this step
+            ctx = {rid: [[torch.from_numpy(a.copy()) for a in kv] for kv in ref.kv[rid]] for rid, _, _ in entries}
         logits = runner.step(out).cpu().numpy()
         expect = ref.step(entries)
+        if pin_now:
+            rids = [rid for rid, _, _ in entries]
+            tok = torch.tensor([x[1][0] for x in entries], dtype=torch.int64, device="cuda")
+
+            def ctx_kv(layer, n):
+                K, V = ctx[rids[n]][layer]
+                return (K.cuda().permute(1, 0, 2).contiguous(), V.cuda().permute(1, 0, 2).contiguous())
+
+            tref = torch_model_decode_ref(cfg, w, tok, ctx_kv).cpu().numpy()
+            perr = float(np.abs(tref - expect).max() / np.abs(expect).max())
+            announce(f"torch model restatement vs oracle: {perr:.2e} of max |logit|")
+            assert perr <= 1e-4, perr
+            pinned = True
         scale = np.abs(expect).max()
         worst = max(worst, float(np.abs(logits - expect).max() / scale))
         agree += int((logits.argmax(1) == expect.argmax(1)).sum())
@@ -96,6 +127,9 @@ def _run(dtype, tol, argmax_frac, swap=False, cfg=None, short=False):
     assert worst <= tol, worst
     assert agree >= argmax_frac * rows, (agree, rows)
     assert bm.free_blocks == NB
+    assert pinned or not pin_torch_ref
+    if long_prefill:
+        assert widest > 64, widest  # a step the tiled weights served from their row-major copies
     if swap:
         assert swaps >= 1 and cache.swap_space()[1] == 64
 
@@ -123,7 +157,18 @@ def test_model_step_llama3_width_bf16_close_to_reference():
     from zealot_amd.model import LlamaConfig
     cfg = LlamaConfig(vocab_size=1024, hidden_size=4096, intermediate_size=14336, num_layers=2, num_heads=32,
                       num_kv_heads=8, head_dim=128)
-    _run(torch.bfloat16, 6e-2, 0.9, cfg=cfg, short=True)
+    _run(torch.bfloat16, 6e-2, 0.9, cfg=cfg, short=True, pin_torch_ref=True)
+
+
+def test_model_step_llama3_width_long_prefill_close_to_reference():
+    """The same widths with prefill steps of up to 256 rows: the tiled
+    gate|up, down (and lm_head) weights serve those steps from their
+    row-major copies on the GEMM plan, decode steps from the tiled layout;
+    both against the oracle."""
+    from zealot_amd.model import LlamaConfig
+    cfg = LlamaConfig(vocab_size=1024, hidden_size=4096, intermediate_size=14336, num_layers=2, num_heads=32,
+                      num_kv_heads=8, head_dim=128)
+    _run(torch.bfloat16, 6e-2, 0.9, cfg=cfg, long_prefill=True)
 
 
 def test_model_decode_step_at_bench_shape():
@@ -134,7 +179,8 @@ def test_model_decode_step_at_bench_shape():
     GPU: the op order of HipModelRunner.forward, fp32 throughout (the HIP
     path rounds activations to bf16 between ops), context K/V read from the
     cache's pages and the step token's own K/V from the reference's own
-    projection.  Bars: logits within 5e-2 of the largest |logit| (2.6e-2
+    projection (tests.gpu_util.torch_model_decode_ref, pinned against the
+    oracle by the two-layer Llama-width test).  Bars: logits within 5e-2 of the largest |logit| (2.6e-2
     measured) and the same argmax on at least 75 % of the sequences (92 %
     measured)."""
     import ctypes
@@ -177,40 +223,18 @@ def test_model_decode_step_at_bench_shape():
     logits = model.forward(plan, tok, last)
     torch.cuda.synchronize()
 
-    def f32(t):
-        return (t.rowmajor() if isinstance(t, dense.TiledWeight) else t).float()
-
-    def rms(x, wt):
-        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.rms_eps) * wt.float()
-
     blocks = [cache.seq_state(s).block_ids for s in ids]
-    prev = torch.backends.cuda.matmul.allow_tf32
-    torch.backends.cuda.matmul.allow_tf32 = False
-    try:
-        resid = w.embedding.float()[tok]
-        for layer, lw in enumerate(w.layers):
-            qkv = rms(resid, lw.attn_norm) @ f32(lw.qkv).T
-            q, kn, vn = qkv[:, :H * D], qkv[:, H * D:(H + Hkv) * D], qkv[:, (H + Hkv) * D:]
-            attn = torch.empty((N, H * D), dtype=torch.float32, device="cuda")
-            kp, vp = cache.k_pool(layer), cache.v_pool(layer)
-            for n in range(N):
-                b = before[n]
-                npg = (b + BS - 1) // BS
-                idx = torch.tensor(blocks[n][:npg], dtype=torch.int64, device="cuda")
-                K = kp.index_select(0, idx).float().permute(1, 0, 2, 3).reshape(Hkv, npg * BS, D)[:, :b]
-                V = vp.index_select(0, idx).float().permute(1, 0, 2, 3).reshape(Hkv, npg * BS, D)[:, :b]
-                K = torch.cat([K, kn[n].view(Hkv, 1, D)], 1)
-                V = torch.cat([V, vn[n].view(Hkv, 1, D)], 1)
-                s = torch.matmul(q[n].view(Hkv, G, D), K.transpose(1, 2).contiguous()) / math.sqrt(D)
-                attn[n] = torch.matmul(torch.softmax(s, -1), V).reshape(H * D)
-            resid = resid + attn @ f32(lw.o).T
-            normed = rms(resid, lw.ffn_norm)
-            gate, up = dense.split_gate_up(f32(lw.gate_up))
-            act = torch.nn.functional.silu(normed @ gate.T) * (normed @ up.T)
-            resid = resid + act @ f32(lw.down).T
-        ref = rms(resid, w.final_norm) @ f32(w.lm_head).T
-    finally:
-        torch.backends.cuda.matmul.allow_tf32 = prev
+
+    def ctx_kv(layer, n):  # the context K/V the HIP step read: the cache's pages
+        b = before[n]
+        npg = (b + BS - 1) // BS
+        idx = torch.tensor(blocks[n][:npg], dtype=torch.int64, device="cuda")
+        kp, vp = cache.k_pool(layer), cache.v_pool(layer)
+        K = kp.index_select(0, idx).float().permute(1, 0, 2, 3).reshape(Hkv, npg * BS, D)[:, :b]
+        V = vp.index_select(0, idx).float().permute(1, 0, 2, 3).reshape(Hkv, npg * BS, D)[:, :b]
+        return K, V
+
+    ref = torch_model_decode_ref(cfg, w, tok, ctx_kv)
     got, want = logits.float(), ref
     err = float((got - want).abs().max() / want.abs().max())
     agree = float((got.argmax(1) == want.argmax(1)).float().mean())

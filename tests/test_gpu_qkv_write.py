@@ -8,7 +8,9 @@ columns and every pool byte must agree bit for bit.  Covered: a decode step
 of 48 sequences with forks whose first write copies a shared tail block
 (T <= 64: the folded form when the plan keeps a split), a prefill step of
 T > 64 (the projection, then the append), bf16 and fp8 pools (fp8 always
-takes the two-step form, quantising in the append)."""
+takes the two-step form, quantising in the append), and the bf16 decode
+step with its plan pinned to a split of k (zk_linear_pin_split), so the
+folded kernel is covered whatever the tuning keeps."""
 import numpy as np
 import pytest
 import torch
@@ -58,9 +60,13 @@ def _same(a, b):
     return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
 
 
-@pytest.mark.parametrize("kv", ["bf16", "fp8"])
-def test_write_batch_qkv_is_projection_then_write_bit_for_bit(kv):
-    rng = np.random.default_rng({"bf16": 71, "fp8": 72}[kv])
+@pytest.mark.parametrize("kv,pin", [("bf16", 0), ("fp8", 0), ("bf16", 4)])
+def test_write_batch_qkv_is_projection_then_write_bit_for_bit(kv, pin):
+    """pin > 1: the decode step's plan is pinned to that split of k over
+    64-row tiles, so the folded reduce + KV write kernel runs whatever the
+    tuning chose."""
+    from zealot_amd import dense
+    rng = np.random.default_rng({"bf16": 71, "fp8": 72}[kv] + pin)
     layers = 2
     base = {f"s{i}": int(rng.integers(1, 40)) for i in range(44)}
     base["par"] = 2 * BS + 5  # forked below: its children's first write copies the partial tail block
@@ -73,6 +79,9 @@ def test_write_batch_qkv_is_projection_then_write_bit_for_bit(kv):
                .reshape(COLS, HID))
     steps = [([s for s in base if s != "par"] + kids, None),                 # decode: 48 rows
              (["s0", "s1", "s2"], [40, 40, 40])]                             # prefill: 120 rows
+    if pin:
+        dense.linear(to_dev(normal(rng, (48, HID), oracle.BF16)), w)  # makes the decode step's plan
+        dense.pin_split(48, COLS, HID, pin, 64)
     for ids, nt in steps:
         nt = nt or [1] * len(ids)
         T = sum(nt)
@@ -83,6 +92,8 @@ def test_write_batch_qkv_is_projection_then_write_bit_for_bit(kv):
             y, ch = _reference(x, w, kv)
             cb.write_batch(layer, ids, nt, y[:, H * D:(H + HKV) * D].view(T, HKV, D), y[:, (H + HKV) * D:].view(T, HKV, D))
             torch.cuda.synchronize()
+            if pin and T <= 64:
+                assert ch["fused_splits"] == pin, ch  # the folded kernel ran
             assert _same(qkv[:, :H * D], y[:, :H * D]), ch
             for pa, pb in ((ca.k_pool(layer), cb.k_pool(layer)), (ca.v_pool(layer), cb.v_pool(layer))):
                 assert _same(pa, pb), (ch, layer, T)

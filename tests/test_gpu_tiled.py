@@ -128,6 +128,35 @@ def test_linear_rms_norm_tiled_is_the_unfused_sequence_bit_for_bit(m, n, k, with
         assert torch.equal(res.view(torch.int16), ref[1].view(torch.int16))
 
 
+@pytest.mark.parametrize("m,n,k,splits,rows", [(64, 4096, 14336, 7, 128), (100, 512, 1024, 4, 64)])
+def test_linear_rms_norm_tiled_pinned_split_is_the_unfused_sequence_bit_for_bit(m, n, k, splits, rows):
+    """The tiled plan pinned to a split of k (zk_linear_pin_split): the norm
+    kernel adds the split sums of the tiled projection, bit for bit the
+    row-major kernel with that split, then zk_rms_norm."""
+    from zealot_amd import dense
+    rng = np.random.default_rng(m * 5 + n + k)
+    x = to_dev(normal(rng, (m, k), oracle.BF16))
+    w = to_dev(_weight(rng, n, k))
+    g = to_dev(normal(rng, (n,), oracle.BF16))
+    r0 = to_dev(normal(rng, (m, n), oracle.BF16))
+    announce(f"linear_rms_norm_tiled pinned split {m}x{n}x{k} splits={splits} rows={rows}")
+    wt = dense.tile_weight(w)
+    dense.linear_rms_norm(x, wt, g, 1e-5, residual=r0.clone())  # makes the plan
+    before = dense.linear_choice(m, n, k, tiled=True)
+    dense.pin_split(m, n, k, splits, rows, tiled=True)
+    try:
+        assert dense.linear_choice(m, n, k, tiled=True)["fused_splits"] == splits
+        res = r0.clone()
+        out, _ = dense.linear_rms_norm(x, wt, g, 1e-5, residual=res, residual_out=res)
+        y = _rowmajor_blocks(x, w, splits, rows, torch.bfloat16)
+        ref_out, ref_res = dense.rms_norm(y, g, 1e-5, residual=r0.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+        assert torch.equal(res.view(torch.int16), ref_res.view(torch.int16))
+    finally:
+        dense.pin_split(m, n, k, before["fused_splits"], before["fused_rows"], tiled=True)
+
+
 @pytest.mark.parametrize("m,inter,k", [(64, 14336, 4096), (7, 1024, 512), (200, 512, 1024)])
 def test_linear_silu_mul_tiled_is_the_unfused_sequence_bit_for_bit(m, inter, k):
     """One launch over the tiled interleaved gate|up weight against the

@@ -117,3 +117,101 @@ def test_noalloc_rejects_oversized_call_and_launches_nothing():
     assert "bytes of scratch, the maximum is 67108864" in L.zk_last_error().decode()
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+
+
+_MEM_PROBE = r"""
+import ctypes, json, math, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+from zealot_amd import _lib
+
+L = _lib.lib()
+dev = "cuda"
+N, H, Hkv, D, BS, NB, MB = 8, 32, 8, 128, 16, 64, 8
+kp = torch.zeros((NB, Hkv, BS, D), dtype=torch.bfloat16, device=dev)
+vp = torch.zeros_like(kp)
+k = torch.randn((N * MB * BS, Hkv, D), device=dev).to(torch.bfloat16)
+v = torch.randn_like(k)
+slots = torch.arange(N * MB * BS, dtype=torch.int64, device=dev)
+q = torch.randn((N, H, D), device=dev).to(torch.bfloat16)
+out = torch.empty_like(q)
+bt = torch.arange(N * MB, dtype=torch.int32, device=dev).view(N, MB)
+lens = torch.full((N,), MB * BS, dtype=torch.int32, device=dev)
+need = L.zk_paged_decode_workspace_size(N, H, D, MB, BS)
+ws = torch.empty(need, dtype=torch.uint8, device=dev)
+s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+torch.cuda.synchronize()
+
+def free():
+    torch.cuda.synchronize()
+    return torch.cuda.mem_get_info()[0]
+
+f = [free()]
+assert L.zk_append(kp.data_ptr(), vp.data_ptr(), _lib.BF16, k.data_ptr(), v.data_ptr(), _lib.BF16,
+                   slots.data_ptr(), k.shape[0], Hkv, D, BS, NB, None, None, None, s) == 0
+f.append(free())
+args = (q.data_ptr(), _lib.BF16, kp.data_ptr(), vp.data_ptr(), _lib.BF16, out.data_ptr(), bt.data_ptr(),
+        lens.data_ptr(), N, H, Hkv, D, BS, MB, NB, 1.0 / math.sqrt(D), _lib.GQA_GROUPED, None, None)
+assert L.zk_paged_decode(*args, ws.data_ptr(), need, s) == 0
+f.append(free())
+assert L.zk_paged_decode_noalloc(*args, s) == 0
+f.append(free())
+assert L.zk_paged_decode_noalloc(*args, s) == 0
+f.append(free())
+print(json.dumps(f))
+"""
+
+
+def test_noalloc_scratch_reserved_by_its_first_call():
+    """The 64 MiB scratch is reserved on a GPU by the first
+    zk_paged_decode_noalloc call there, not by the library's other kernels:
+    device memory free (hipMemGetInfo) in a fresh process before and after the
+    first zk_append, the first zk_paged_decode and two no-alloc calls."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    announce("noalloc scratch reservation probe (fresh process)")
+    r = subprocess.run([sys.executable, "-c", _MEM_PROBE, root], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    f = json.loads(r.stdout.strip().splitlines()[-1])
+    mib = [(a - b) / 2**20 for a, b in zip(f, f[1:])]
+    print(f"[gpu-case] MiB reserved by: first append {mib[0]:.1f}, first decode {mib[1]:.1f}, "
+          f"first no-alloc decode {mib[2]:.1f}, second {mib[3]:.1f}", flush=True)
+    assert mib[0] < 32 and mib[1] < 32, mib    # code objects only, no scratch
+    assert mib[2] >= SCRATCH / 2**20, mib      # the scratch arrives with the first no-alloc call
+    assert abs(mib[3]) < 1, mib                # and is not reserved again
+
+
+def test_noalloc_under_graph_capture():
+    """One eager call (looks the scratch up), then zk_paged_decode_noalloc
+    captured in a HIP graph through torch.cuda.graph and replayed on new q
+    values, eager work and synchronisation between the replays: every replay
+    bit for bit equal to the workspace entry point on the same q."""
+    H, Hkv, D = 32, 8, 128
+    rng = np.random.default_rng(77)
+    lens = [int(x) for x in rng.integers(1, 5000, 40)] + [8192, 1]
+    host, (q, kp, vp, bt, ln) = _case(70, H, Hkv, D, lens, oracle.BF16)
+    announce(f"noalloc decode under graph capture N={len(lens)}")
+    L = _lib.lib()
+    n = len(lens)
+    out = torch.empty_like(q)
+    _call(True, q, kp, vp, bt, ln)  # eager first call on this device
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = L.zk_paged_decode_noalloc(q.data_ptr(), _lib.BF16, kp.data_ptr(), vp.data_ptr(), _lib.BF16,
+                                       out.data_ptr(), bt.data_ptr(), ln.data_ptr(), n, H, Hkv, D, 16, bt.shape[1],
+                                       kp.shape[0], 1.0 / math.sqrt(D), _lib.GQA_GROUPED, None, None, s)
+    assert rc == 0, L.zk_last_error().decode()
+    g = torch.Generator(device="cuda").manual_seed(78)
+    for rep in range(4):
+        q.copy_(torch.randn(q.shape, generator=g, device="cuda").to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _call(False, q, kp, vp, bt, ln)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), rep
+        _call(True, q, kp, vp, bt, ln)  # eager work on the same scratch between replays

@@ -147,6 +147,7 @@ SIGNATURES = {
     "zk_linear_tiled_choice": (_I, [_I64, _I64, _I64, _I, _P]),
     "zk_linear_skinny": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P]),
     "zk_linear_tuning": (_I, [_I]),
+    "zk_linear_pin_split": (_I, [_I64, _I64, _I64, _I, _I, _I, _I, _I]),
     "zk_sched_create": (_I, [ctypes.POINTER(SchedConfigC), _P, ctypes.POINTER(_P)]),
     "zk_sched_destroy": (None, [_P]),
     "zk_sched_block_manager": (_P, [_P]),

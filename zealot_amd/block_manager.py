@@ -52,6 +52,8 @@ class BlockManager:
     def __init__(self, num_gpu_blocks: int, block_size: int):
         L = _lib.lib()
         self._h = None
+        # bound now: at interpreter exit the module globals may already be gone
+        self._destroy = L.zk_bm_destroy
         if num_gpu_blocks < 0 or block_size < 0:
             raise OverflowError("can't convert negative int to unsigned")
         h = ctypes.c_void_p()
@@ -59,8 +61,9 @@ class BlockManager:
         self._h = h
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            _lib.lib().zk_bm_destroy(self._h)
+        destroy = getattr(self, "_destroy", None)
+        if getattr(self, "_h", None) and destroy is not None:
+            destroy(self._h)
             self._h = None
 
     @property

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(HERE, "libzealot_kv.so")
 SOURCES = ["status.cpp", "timing.cpp", "block_manager.cpp", "kv_ops.hip", "paged_decode.hip", "paged_prefill.hip", "kv_cache.cpp", "scheduler.cpp",
-           "dense_ops.hip", "gemm.cpp", "skinny_gemm.hip"]
+           "dense_ops.hip", "gemm.cpp", "skinny_gemm.hip", "noalloc_scratch.hip"]
 ARCH = "gfx950"
 HIPFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall",

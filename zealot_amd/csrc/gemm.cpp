@@ -625,6 +625,23 @@ int zk_linear_choice(int64_t m, int64_t n, int64_t k, zk_dtype in_dtype, zk_dtyp
     return ZK_OK;
 }
 
+int zk_linear_pin_split(int64_t m, int64_t n, int64_t k, zk_dtype in_dtype, zk_dtype out_dtype, int tiled,
+                        int fused_splits, int fused_rows) {
+    std::lock_guard<std::mutex> g(g_mu);
+    DeviceState *d;
+    if (int rc = device_state(&d)) return rc;
+    auto it = d->plans.find(std::make_tuple(m, n, k, (int)in_dtype, (int)out_dtype, tiled != 0));
+    if (it == d->plans.end())
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_linear_pin_split: no plan for this shape yet");
+    if (fused_splits != 0 &&
+        (in_dtype != ZK_BF16 || fused_splits < 2 || !skinny_fits(m, n, k, fused_rows, fused_splits, tiled != 0)))
+        return zk::set_error(ZK_ERR_INVALID_ARGUMENT,
+                             "Internal error: zk_linear_pin_split: configuration does not fit the shape");
+    it->second.fused_splits = fused_splits;
+    it->second.fused_rows = fused_splits ? fused_rows : 0;
+    return ZK_OK;
+}
+
 int zk_linear_tuning(int on) {
     std::lock_guard<std::mutex> g(g_mu);
     g_tune = on != 0;
@@ -634,10 +651,9 @@ int zk_linear_tuning(int on) {
 }  // extern "C"
 
 int zk::linear_split_sums(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, hipStream_t stream,
-                          const float **partial, int *splits) {
-    if (!partial || !splits) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: linear_split_sums: NULL");
-    *partial = nullptr;
-    *splits = 0;
+                          const SplitSumsConsumer &consume, bool *fused) {
+    if (!fused) return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: linear_split_sums: NULL");
+    *fused = false;
     if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff)
         return zk::set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: linear_split_sums: bad shape");
     if (m == 0) return ZK_OK;
@@ -649,14 +665,19 @@ int zk::linear_split_sums(const void *x, const void *w, void *y, int64_t m, int6
     if (int rc = scratch_for(*d, stream, false, &sc)) return rc;
     Plan *p;
     if (int rc = make_plan(*d, *sc, m, n, k, ZK_BF16, ZK_BF16, x, w, y, stream, g_tune, &p)) return rc;
-    if (p->fused_splits > 1 && skinny_fits(m, n, k, p->fused_rows, p->fused_splits) && aligned16(x) && aligned16(w)) {
+    if (p->fused_splits > 1 && skinny_fits(m, n, k, p->fused_rows, p->fused_splits) && aligned16(x) && aligned16(w) &&
+        aligned16(y) && n % 8 == 0) {
         if (int rc = scratch_for(*d, stream, true, &sc)) return rc;
-        zk::KernelTimer timer("linear", stream);
-        if (int rc = zk::skinny_linear(x, w, nullptr, m, n, k, false, p->fused_rows, p->fused_splits, sc->partial,
-                                       kSkinnyPartial, stream, /*reduce=*/false))
-            return rc;
-        *partial = (const float *)sc->partial;
-        *splits = p->fused_splits;
+        {
+            zk::KernelTimer timer("linear", stream);
+            if (int rc = zk::skinny_linear(x, w, nullptr, m, n, k, false, p->fused_rows, p->fused_splits, sc->partial,
+                                           kSkinnyPartial, stream, /*reduce=*/false))
+                return rc;
+        }
+        // the consumer's launch is enqueued before the lock goes: no other
+        // call can evict this stream's workspace in between
+        if (int rc = consume((const float *)sc->partial, p->fused_splits)) return rc;
+        *fused = true;
         return ZK_OK;
     }
     return run_plan(*d, sc, p, x, w, y, m, n, k, ZK_BF16, stream);

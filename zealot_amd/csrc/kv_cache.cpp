@@ -787,19 +787,32 @@ int zk_cache_write_batch_qkv(zk_kv_cache *c, size_t layer, const char *const *id
     if (int rc = prepare_write(c, layer, ids, num_tokens, n, x && w_qkv && qkv, w)) return rc;
     if (w.T == 0) return ZK_OK;
     const int64_t T = (int64_t)w.T;
-    const float *partial = nullptr;
-    int splits = 0;
+    bool fused = false;
     if (c->dtype == ZK_BF16) {  // the projection's split-k sums, if its plan keeps them, go straight to the pools
-        if (int rc = zk::linear_split_sums(x, w_qkv, qkv, T, cols, hidden, c->stream, &partial, &splits)) return rc;
+        struct ToPools : zk::SplitSumsConsumer {
+            zk_kv_cache *c;
+            size_t layer;
+            int64_t T, cols, qcols;
+            void *qkv;
+            const int64_t *slots;
+            int operator()(const float *partial, int splits) const override {
+                return zk::append_split_sums(c->k_pool(layer), c->v_pool(layer), partial, splits, T, cols, qkv, cols,
+                                             qcols, slots, (int)c->num_kv_heads, (int)c->head_dim, (int)c->block_size,
+                                             (int64_t)c->num_blocks, c->stream);
+            }
+        } to_pools;
+        to_pools.c = c;
+        to_pools.layer = layer;
+        to_pools.T = T;
+        to_pools.cols = cols;
+        to_pools.qcols = qcols;
+        to_pools.qkv = qkv;
+        to_pools.slots = w.d_slots;
+        if (int rc = zk::linear_split_sums(x, w_qkv, qkv, T, cols, hidden, c->stream, to_pools, &fused)) return rc;
     } else if (int rc = zk_linear(x, w_qkv, qkv, T, cols, hidden, ZK_BF16, ZK_BF16, c->stream)) {
         return rc;
     }
-    if (splits > 1) {
-        if (int rc = zk::append_split_sums(c->k_pool(layer), c->v_pool(layer), partial, splits, T, cols, qkv, cols,
-                                           qcols, w.d_slots, (int)c->num_kv_heads, (int)c->head_dim,
-                                           (int)c->block_size, (int64_t)c->num_blocks, c->stream))
-            return rc;
-    } else {
+    if (!fused) {
         const char *y = (const char *)qkv;
         if (int rc = zk::append(c->k_pool(layer), c->v_pool(layer), (zk_dtype)c->dtype, y + 2 * qcols,
                                 y + 2 * (qcols + (int64_t)c->num_kv_heads * c->head_dim), ZK_BF16, cols, w.d_slots, T,

@@ -28,11 +28,9 @@
 // scale * log2(e) and exponentiated with exp2 (the FlashAttention trick).
 #include <hip/hip_runtime.h>
 
-#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
-#include <mutex>
 #include <string>
 #include <utility>
 
@@ -1355,42 +1353,9 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
 }
 
 // ------------------------------------------------------------ no-allocation decode
-// zk_paged_decode_noalloc's workspace: a file-scope device array, one copy
-// per GPU, held until the process ends.  Host code never uses the array's
-// name as a device address (on the host it names a stand-in): the device
-// address comes from hipGetSymbolAddress, once per device, with that device
-// current, and is kept per device.
-static __device__ __align__(256) unsigned char scratch[ZK_DECODE_SCRATCH_BYTES];
-
-namespace {
-
-constexpr int kMaxDevices = 64;
-std::atomic<void *> g_scratch_ptr[kMaxDevices];
-std::mutex g_scratch_mu;
-
-// Device address of the current device's scratch array (looked up on the
-// device's first call).
-int scratch_of_current_device(void **out) {
-    int dev = -1;
-    ZK_HIP_CHECK(hipGetDevice(&dev), "zk_paged_decode_noalloc: hipGetDevice");
-    if (dev < 0 || dev >= kMaxDevices)
-        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_decode_noalloc: device ordinal " +
-                                                      std::to_string(dev) + " out of range");
-    void *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
-    if (!p) {
-        std::lock_guard<std::mutex> g(g_scratch_mu);
-        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
-        if (!p) {
-            ZK_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "zk_paged_decode_noalloc: scratch address");
-            if (!p) return set_error(ZK_ERR_HIP, "Internal error: zk_paged_decode_noalloc: NULL scratch address");
-            g_scratch_ptr[dev].store(p, std::memory_order_release);
-        }
-    }
-    *out = p;
-    return ZK_OK;
-}
-
-}  // namespace
+// zk_paged_decode_noalloc's workspace is the device array of
+// noalloc_scratch.hip (zk::noalloc_scratch), reserved on a GPU by the first
+// call there.
 
 extern "C" {
 
@@ -1427,7 +1392,7 @@ int zk_paged_decode_noalloc(const void *q, zk_dtype q_dtype, const void *k_pool,
                                                       std::to_string(need) + " bytes of scratch, the maximum is " +
                                                       std::to_string((size_t)ZK_DECODE_SCRATCH_BYTES));
     void *ws = nullptr;
-    if (int rc = scratch_of_current_device(&ws)) return rc;
+    if (int rc = zk::noalloc_scratch(&ws)) return rc;
     zk::TimingSuspend no_events;  // per-kernel timing would create hipEvents
     return zk::paged_decode(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, seq_lens, num_seqs, num_heads,
                             num_kv_heads, head_dim, block_size, max_blocks_per_seq, num_blocks, scale, mapping,

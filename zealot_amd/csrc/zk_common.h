@@ -61,12 +61,16 @@ int append_split_sums(void *k_pool, void *v_pool, const float *partial, int spli
                       int head_dim, int block_size, int64_t num_blocks, void *stream);
 // y = x . w^T (bf16, zk_linear's plan for the shape) left as split-k sums
 // when the plan keeps a weight-streaming configuration with split k beside
-// its choice (the one zk_linear_rms_norm folds): *partial and *splits > 1
-// then describe them ([splits][m][n] f32 in the stream's workspace, valid
-// until the next projection on the stream) and y is not written; otherwise
-// y holds the product and *splits = 0.
+// its choice (the one zk_linear_rms_norm folds) and x, w, y are 16-byte
+// aligned with n % 8 == 0: consume(partial, splits) then runs, still under
+// the projection's lock (the sums, [splits][m][n] f32, sit in the stream's
+// workspace), y is not written and *fused is set; otherwise y holds the
+// product and *fused is false.
+struct SplitSumsConsumer {
+    virtual int operator()(const float *partial, int splits) const = 0;
+};
 int linear_split_sums(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, hipStream_t stream,
-                      const float **partial, int *splits);
+                      const SplitSumsConsumer &consume, bool *fused);
 // Swap staging (kv_ops.hip): blocks[i] of each of the num_pools pools at
 // slab + p * pool_bytes <-> staging[(i * num_pools + p) * block_bytes ...]
 // (to_staging: pools -> staging, else staging -> pools).
@@ -148,6 +152,10 @@ int rms_norm_partials(const float *partial, int splits, const void *residual, co
                       void *residual_out, int64_t rows, int64_t dim, float eps, hipStream_t s);
 size_t paged_decode_workspace(int num_seqs, int num_heads, int head_dim, int max_blocks_per_seq, int block_size,
                               bool shared);
+// Device address of the current device's ZK_DECODE_SCRATCH_BYTES scratch of
+// zk_paged_decode_noalloc (noalloc_scratch.hip); the first call on a device
+// loads the array there.
+int noalloc_scratch(void **out);
 // Whether paged_decode runs shared-prefix items for this shape (otherwise pg
 // is ignored and every sequence reads its whole table).
 bool paged_decode_shares_prefixes(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads);

@@ -101,14 +101,22 @@ class TiledWeight:
     r holding columns 8 (u ^ r) .. of its 128-column chunk.  linear,
     linear_rms_norm and linear_silu_mul take it in place of the row-major
     tensor; the products read it with contiguous 1 KiB loads (17-19 % faster
-    on the large decode projections).  `data` is the flat device buffer."""
+    on the large decode projections).  `data` is the flat device buffer.
 
-    __slots__ = ("data", "n", "k")
+    The weight-streaming kernel reads the whole weight once per 64 rows of
+    x, so it suits decode-sized products only.  `full`, when kept (the
+    row-major [n, k] weight), serves products of more than TILED_MAX_ROWS
+    rows (prefill and mixed steps) on zk_linear's GEMM plan instead."""
 
-    def __init__(self, data: torch.Tensor, n: int, k: int):
+    __slots__ = ("data", "n", "k", "full")
+
+    def __init__(self, data: torch.Tensor, n: int, k: int, full: torch.Tensor | None = None):
         if data.dtype != torch.bfloat16 or data.numel() != n * k or not data.is_contiguous():
             raise ValueError("a tiled weight is a contiguous bf16 buffer of n * k elements")
-        self.data, self.n, self.k = data, n, k
+        if full is not None and (full.dtype != torch.bfloat16 or tuple(full.shape) != (n, k)
+                                 or not full.is_contiguous()):
+            raise ValueError("the row-major copy is a contiguous bf16 [n, k] tensor")
+        self.data, self.n, self.k, self.full = data, n, k, full
 
     @property
     def shape(self):
@@ -135,15 +143,30 @@ class TiledWeight:
         return torch.gather(t, 3, idx).reshape(n, k).view(torch.bfloat16)  # [b r j c e] = t[b r j (c ^ r) e]
 
 
-def tile_weight(weight: torch.Tensor, stream=None) -> TiledWeight:
+def tile_weight(weight: torch.Tensor, stream=None, keep_full: bool = False) -> TiledWeight:
     """The tiled form of a row-major bf16 weight [n, k] (n % 16 == 0,
-    k % 128 == 0), in a new buffer."""
+    k % 128 == 0), in a new buffer; keep_full keeps `weight` beside it for
+    products of more than TILED_MAX_ROWS rows."""
     n, k = weight.shape
     if weight.dtype != torch.bfloat16:
         raise ValueError("tiled weights are bf16")
     out = torch.empty(n * k, dtype=torch.bfloat16, device=weight.device)
     _lib.check(_lib.lib().zk_weight_tile(_dev(weight, "weight"), _dev(out, "out"), n, k, _stream(stream)))
-    return TiledWeight(out, n, k)
+    return TiledWeight(out, n, k, weight.contiguous() if keep_full else None)
+
+
+# Rows of x up to which a TiledWeight's product runs on the weight-streaming
+# kernel even when its row-major copy is kept: that kernel reads the weight
+# once per 64 rows, a GEMM once.
+TILED_MAX_ROWS = 64
+
+
+def _route(x, weight):
+    """The weight a product of x runs on: a TiledWeight's row-major copy for
+    more than TILED_MAX_ROWS rows, when it keeps one."""
+    if isinstance(weight, TiledWeight) and weight.full is not None and x.shape[0] > TILED_MAX_ROWS:
+        return weight.full
+    return weight
 
 
 def _tiled_x(x, weight):
@@ -154,9 +177,11 @@ def _tiled_x(x, weight):
 def linear(x, weight, out=None, out_dtype=None, stream=None):
     """x [m, k] . weight[n, k]^T on hipBLASLt (the cublasSgemm_v2 sites) or the
     weight-streaming kernel, whichever the first call of the shape timed
-    faster; a TiledWeight runs on the weight-streaming kernel."""
+    faster; a TiledWeight runs on the weight-streaming kernel (on its
+    row-major copy, if kept, for more than TILED_MAX_ROWS rows)."""
     m, k = x.shape
     n = weight.shape[0]
+    weight = _route(x, weight)
     if isinstance(weight, TiledWeight):
         _tiled_x(x, weight)
         if out is None:
@@ -187,6 +212,7 @@ def linear_rms_norm(x, weight, norm_weight, eps: float = 1e-6, residual=None, ou
     n = weight.shape[0]
     if weight.shape[1] != k or weight.dtype != x.dtype:
         raise ValueError("weight must be [n, k] of x's dtype")
+    weight = _route(x, weight)
     tiled = isinstance(weight, TiledWeight)
     if tiled:
         _tiled_x(x, weight)
@@ -239,6 +265,7 @@ def linear_silu_mul(x, gate_up, out=None, gu=None, stream=None):
     n = gate_up.shape[0]
     if gate_up.shape[1] != k or gate_up.dtype != x.dtype or n % (2 * GATE_UP_BLOCK):
         raise ValueError("gate_up must be [2 I, k] of x's dtype, I a multiple of 16")
+    gate_up = _route(x, gate_up)
     if isinstance(gate_up, TiledWeight):  # one launch, no projection buffer
         _tiled_x(x, gate_up)
         if out is None:
@@ -274,6 +301,14 @@ def linear_choice(m, n, k, in_dtype=torch.bfloat16, out_dtype=None, tiled=False)
     else:
         _lib.check(_lib.lib().zk_linear_choice(m, n, k, code[in_dtype], code[out_dtype or in_dtype], c))
     return {"splits": c[0], "tile_rows": c[1], "fused_splits": c[2], "fused_rows": c[3]}
+
+
+def pin_split(m, n, k, fused_splits, fused_rows, in_dtype=torch.bfloat16, out_dtype=None, tiled=False) -> None:
+    """Pin the split-k configuration linear_rms_norm / write_batch_qkv fold
+    for the plan an earlier call made for this shape (fused_splits 0: none)."""
+    code = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+    _lib.check(_lib.lib().zk_linear_pin_split(m, n, k, code[in_dtype], code[out_dtype or in_dtype], int(tiled),
+                                              fused_splits, fused_rows))
 
 
 def linear_skinny(x, weight, splits=1, tile_rows=128, out=None, out_dtype=None, stream=None):

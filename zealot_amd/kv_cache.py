@@ -99,6 +99,8 @@ class KVCache:
         self.head_dim = head_dim
         self.dtype = dtype
         self._stream_obj = stream
+        # bound now: at interpreter exit the module globals may already be gone
+        self._destroy = _lib.lib().zk_cache_destroy
         h = ctypes.c_void_p()
         _lib.check(_lib.lib().zk_cache_create(num_blocks, block_size, num_layers, num_kv_heads,
                                               head_dim, _TORCH_TO_ZK[dtype], max_seqs,
@@ -106,8 +108,9 @@ class KVCache:
         self._h = h
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            _lib.lib().zk_cache_destroy(self._h)
+        destroy = getattr(self, "_destroy", None)
+        if getattr(self, "_h", None) and destroy is not None:
+            destroy(self._h)
             self._h = None
 
     # -- sequence lifecycle (kv_cache.rs:104-166) --------------------------

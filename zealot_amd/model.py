@@ -25,7 +25,9 @@ reference).  What differs is the shape of the work:
     norm runs only over the last row of each sequence;
   - the large decode-time weights (gate|up, down, lm_head) are kept tiled
     (dense.TiledWeight): the weight-streaming kernel reads them with
-    contiguous 1 KiB loads;
+    contiguous 1 KiB loads; their row-major copies serve steps of more than
+    64 rows (prefill, mixed) on the GEMM plan, since the weight-streaming
+    kernel reads a weight once per 64 rows;
   - weights are random-initialised here (there is no checkpoint loader in
     this build; the reference loads HF weights, model_loader.rs:241).
 """
@@ -76,11 +78,15 @@ class LlamaWeights:
 
     @staticmethod
     def random(cfg: LlamaConfig, dtype=torch.bfloat16, device="cuda", seed: int = 0,
-               tiled: bool = True) -> "LlamaWeights":
+               tiled: bool = True, keep_full: bool = True) -> "LlamaWeights":
         """N(0, 1/fan_in) projections and N(1, 0.1) norm weights (seeded);
-        with tiled (bf16 only) gate|up, down and lm_head as dense.TiledWeight."""
+        with tiled (bf16 only) gate|up, down and lm_head as dense.TiledWeight,
+        keeping their row-major copies for steps of more than 64 rows unless
+        keep_full is off (decode-only callers: half the memory of those
+        weights)."""
         g = torch.Generator(device=device).manual_seed(seed)
-        tile = dense.tile_weight if tiled and dtype == torch.bfloat16 else (lambda t: t)
+        tile = ((lambda t: dense.tile_weight(t, keep_full=keep_full)) if tiled and dtype == torch.bfloat16
+                else (lambda t: t))
 
         def lin(n, k):
             return (torch.randn((n, k), generator=g, device=device) / math.sqrt(k)).to(dtype)

@@ -53,12 +53,15 @@ class PendingSequence:
     """A Sequence made by make_sequence and not yet added (scheduler.rs:225-253)."""
 
     def __init__(self, ptr: ctypes.c_void_p, request_id: str):
+        # bound now: at interpreter exit the module globals may already be gone
+        self._destroy = _lib.lib().zk_sequence_destroy
         self._p = ptr
         self.request_id = request_id
 
     def __del__(self):
-        if getattr(self, "_p", None):
-            _lib.lib().zk_sequence_destroy(self._p)
+        destroy = getattr(self, "_destroy", None)
+        if getattr(self, "_p", None) and destroy is not None:
+            destroy(self._p)
             self._p = None
 
 
@@ -116,6 +119,7 @@ class Scheduler:
         self._h = None
         self.cfg = cfg or SchedulerConfig()
         self._bm = block_manager  # keeps a shared manager alive
+        self._destroy = _lib.lib().zk_sched_destroy  # bound now, for __del__ at interpreter exit
         h = ctypes.c_void_p()
         c = self.cfg._c()
         _lib.check(_lib.lib().zk_sched_create(ctypes.byref(c), block_manager.handle if block_manager else None,
@@ -123,8 +127,9 @@ class Scheduler:
         self._h = h
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            _lib.lib().zk_sched_destroy(self._h)
+        destroy = getattr(self, "_destroy", None)
+        if getattr(self, "_h", None) and destroy is not None:
+            destroy(self._h)
             self._h = None
 
     def make_sequence(self, request_id: str, prompt_tokens, max_tokens: int,
