@@ -424,9 +424,8 @@ def bench_c4(args, torch, lib):
             if pos[i] == nblk[i] * BS:
                 cache.alloc_block(cid, bm)
                 nblk[i] += 1
-        for layer in range(L):
-            cache.append_kv_batch(layer, batch, kin[layer % R], vin[layer % R])
-            cache.paged_decode(layer, batch, qin[layer % R], out=out)
+        for layer in range(L):  # append + decode of the layer, one launch (zk_cache_decode_append)
+            cache.decode_append(layer, batch, kin[layer % R], vin[layer % R], qin[layer % R], out=out)
         for i in range(n):
             pos[i] += 1
 

@@ -328,6 +328,17 @@ int zk_cache_block_ids(zk_kv_cache *c, const char *id, int64_t *ids, size_t *n);
 int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, int n,
                           const void *q, zk_dtype q_dtype, void *out, int num_heads, float scale,
                           zk_gqa_mapping mapping);
+/* One decode step of one layer: zk_cache_append_kv_batch of k / v ([n, Hkv,
+ * D], one token per sequence at its next position, copy-on-write of shared
+ * tail blocks included) followed by zk_cache_paged_decode, with the same
+ * results.  For bf16 pools and bf16 k / v on the MFMA decode shapes it is one
+ * decode launch: the work item holding a sequence's last page stores the
+ * token's K / V row into the pools and attends it from registers (the
+ * per-layer append plus paged_forward of cuda_runner.rs:405-461); other
+ * shapes run the two calls.  No single reference counterpart. */
+int zk_cache_decode_append(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *k,
+                           const void *v, zk_dtype src_dtype, const void *q, zk_dtype q_dtype, void *out,
+                           int num_heads, float scale, zk_gqa_mapping mapping);
 /* Batched attention for one layer of a mixed step, after zk_cache_write_batch
  * wrote the step's tokens: the num_tokens[i] query rows of sequence ids[i]
  * (packed in batch order in q / out, [sum num_tokens, H, D]) are its last

@@ -12,7 +12,9 @@ ones to 1e-4).
 
 C4: 16 prefixes of 2048 + r tokens (r in [1, 15]: the tail block is partial)
 over 32 bf16 layers, 8 forks each, through the stateful KVCache, for all 64
-decode steps of append + paged attention: fork refcounts, the copy-on-write
+decode steps of append + paged attention (even steps through the fused
+decode_append launch, odd ones through append_kv_batch + paged_decode):
+fork refcounts, the copy-on-write
 of all 128 tails in all 64 pools (bit-exact), the 16 prefix subgroups of the
 shared decode, every block a fork gains on the way (a fresh private block
 with one reference whenever its position crosses a block boundary, about
@@ -176,11 +178,14 @@ def test_c4_prefix_cow_full_size():
                 assert bm.refcount(ids[-1]) == 1 and ids[-1] not in private[i], (cid, step)
                 private[i].add(ids[-1])
         for layer in range(L):
-            cache.append_kv_batch(layer, batch, kin[step][layer], vin[step][layer])
+            if step % 2 == 0:  # even steps: the fused append + decode launch
+                cache.decode_append(layer, batch, kin[step][layer], vin[step][layer], qin[step][layer], out=out)
+            else:
+                cache.append_kv_batch(layer, batch, kin[step][layer], vin[step][layer])
+                cache.paged_decode(layer, batch, qin[step][layer], out=out)
             if step == 0 and layer == 0:
                 torch.cuda.synchronize()
                 _check_cow(cache, bm, pblocks, plen, parent, children, kin[0][0], vin[0][0], F, L, BS)
-            cache.paged_decode(layer, batch, qin[step][layer], out=out)
             for i, sl, ss in sample:
                 if (sl, ss) == (layer, step):
                     outs[(i, sl, ss)] = out[i].clone()

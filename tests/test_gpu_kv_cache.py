@@ -408,3 +408,75 @@ def test_cow_out_of_blocks_keeps_typed_error():
     cache.release_seq("c")
     cache.release_seq("p")
     assert bm.free_blocks == NB
+
+
+@pytest.mark.parametrize("dtype,H,Hkv,D", [("bf16", 32, 8, 128), ("bf16", 8, 8, 64), ("f32", 4, 4, 32)])
+def test_decode_append_is_append_then_decode(dtype, H, Hkv, D):
+    """zk_cache_decode_append (one launch on bf16 MFMA shapes: the decode
+    stores each sequence's new K / V row and attends it) against
+    append_kv_batch + paged_decode on a twin cache with the same history:
+    outputs and every pool byte equal after each of 40 steps over 2 layers,
+    with forks whose first write copies a shared tail block and sequences
+    crossing block boundaries (src/kv_cache.rs:281-356,
+    src/attention/mod.rs:64-98); the f32 cache takes the two-call path."""
+    import zealot_amd as ze
+    from zealot_amd import KVCache
+    from zealot_amd.kv_cache import SeqBatch
+    cdt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    odt = oracle.BF16 if dtype == "bf16" else oracle.F32
+    L, BS, NB, STEPS = 2, 16, 600, 40
+    rng = np.random.default_rng(46 + D)
+    base = {f"s{i}": int(rng.integers(1, 700)) for i in range(12)}
+    base["par"] = 16 * 20 + 5  # forked: its children's first append copies the partial tail
+    kids = [f"k{i}" for i in range(6)]
+    caches = []
+    init = {s: [normal(rng, (t, Hkv, D), odt) for _ in range(2 * L)] for s, t in base.items()}
+    for _ in range(2):
+        bm = ze.BlockManager(NB, BS)
+        cache = KVCache(NB, BS, L, Hkv, D, dtype=cdt, max_seqs=32, max_blocks_per_seq=64)
+        for sid, t in base.items():
+            cache.register_seq(sid, 64)
+            for _ in range((t + STEPS + BS - 1) // BS):
+                cache.alloc_block(sid, bm)
+            for layer in range(L):
+                cache.store_kv(layer, sid, to_dev(init[sid][2 * layer]), to_dev(init[sid][2 * layer + 1]), 0, t)
+        for k in kids:
+            cache.fork_seq("par", k)
+        caches.append((cache, bm))
+    ids = [s for s in base if s != "par"] + kids
+    batch = SeqBatch(ids)
+    pos = {s: base[s] for s in base}
+    for k in kids:
+        pos[k] = base["par"]
+    announce(f"decode_append {dtype} H{H}/Hkv{Hkv}/D{D}: {len(ids)} seqs x {STEPS} steps")
+    for step in range(STEPS):  # the forks share the parent's later blocks too: each is copied on first write
+        for layer in range(L):
+            k = to_dev(normal(rng, (len(ids), Hkv, D), odt))
+            v = to_dev(normal(rng, (len(ids), Hkv, D), odt))
+            q = to_dev(normal(rng, (len(ids), H, D), odt))
+            (ca, _), (cb, _) = caches
+            got = ca.decode_append(layer, batch, k, v, q)
+            cb.append_kv_batch(layer, batch, k, v)
+            want = cb.paged_decode(layer, batch, q)
+            torch.cuda.synchronize()
+            assert np.array_equal(to_host(got), to_host(want)), (step, layer)
+            for pa, pb in ((ca.k_pool(layer), cb.k_pool(layer)), (ca.v_pool(layer), cb.v_pool(layer))):
+                assert np.array_equal(to_host(pa), to_host(pb)), (step, layer)
+        for sid in ids:
+            pos[sid] += 1
+            assert ca.seq_state(sid).cached_tokens == cb.seq_state(sid).cached_tokens == pos[sid]
+    # and the last step against the oracle on the pages as they are
+    (ca, _), _ = caches
+    last = L - 1
+    kp, vp = to_host(ca.k_pool(last)), to_host(ca.v_pool(last))
+    bt = -np.ones((len(ids), 64), np.int32)
+    for i, sid in enumerate(ids):
+        b = ca.seq_state(sid).block_ids
+        bt[i, :len(b)] = b
+    ref = oracle.paged_decode(as_f32(to_host(q), odt), kp, vp, odt, bt, [pos[s] for s in ids], Hkv, D, BS,
+                              np.float32(1 / math.sqrt(D)), threads=8)
+    assert max_abs_err(as_f32(to_host(got), odt), ref) <= (2e-2 if dtype == "bf16" else 1e-5)
+    par = ca.seq_state("par").block_ids
+    for k in kids:  # the forks copied the partial tail, the full blocks before it stay shared
+        ids_k = ca.seq_state(k).block_ids
+        assert ids_k[:20] == par[:20] and ids_k[20] != par[20]

@@ -125,6 +125,7 @@ SIGNATURES = {
                                 ctypes.POINTER(_SZ)]),
     "zk_cache_block_ids": (_I, [_P, _CP, ctypes.POINTER(_I64), ctypes.POINTER(_SZ)]),
     "zk_cache_paged_decode": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _I, _P, _I, _F, _I]),
+    "zk_cache_decode_append": (_I, [_P, _SZ, ctypes.POINTER(_CP), _I, _P, _P, _I, _P, _I, _P, _I, _F, _I]),
     "zk_cache_attention_batch": (_I, [_P, _SZ, ctypes.POINTER(_CP), _P, _I, _P, _I, _I64, _P, _I, _F, _I]),
     "zk_cache_decode_sharing": (_I, [_P, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int64)]),
     "zk_timing_enable": (_I, [_I]),

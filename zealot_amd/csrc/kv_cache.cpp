@@ -173,6 +173,7 @@ struct zk_kv_cache {
     size_t host_total = 0;
     std::vector<int32_t> host_free;  // sorted descending: back() is the lowest
     DevBuf d_stage, d_swap_ids;
+    int dec_head_set = 0;     // queue-head set of the next decode launch that reuses its plan
     int last_sg = 0;          // prefix subgroups of the last paged_decode
     int64_t last_sg_pages = 0;  // and the pages they shared (summed over subgroups)
 
@@ -493,7 +494,7 @@ struct WritePrep {
 };
 
 int prepare_write(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,
-                  bool have_src, WritePrep &w) {
+                  bool have_src, WritePrep &w, bool upload_slots = true) {
     if (!c || (n > 0 && (!ids || !num_tokens)))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: NULL argument");
     if (layer >= c->num_layers)
@@ -539,6 +540,8 @@ int prepare_write(zk_kv_cache *c, size_t layer, const char *const *ids, const in
             if (zk_bm_refcount(s.bm, s.handles[idx].block_id) > 1) shared.emplace_back(&s, idx);
     }
     if (int rc = cow_blocks(c, shared)) return rc;
+    w.T = T;
+    if (!upload_slots) return ZK_OK;  // the caller's kernel finds the slots itself
     const size_t slots_bytes = T * sizeof(int64_t);
     const size_t rows_bytes = fp8 ? T * sizeof(int32_t) : 0;
     const size_t scale_bytes = fp8 ? 2 * (size_t)n * H * sizeof(float) : 0;
@@ -1126,7 +1129,7 @@ namespace {
 int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState *> &seqs,
                  const std::vector<int32_t> *lens_in, const std::vector<int32_t> *q_rows, const void *q,
                  zk_dtype q_dtype, int64_t q_stride, void *out, int num_heads, float scale, zk_gqa_mapping mapping,
-                 bool share) {
+                 bool share, const zk::AppendRows *append = nullptr) {
     const int n = (int)seqs.size();
     if (n <= 0) return ZK_OK;
     const size_t H = c->num_kv_heads;
@@ -1155,6 +1158,10 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
         zk::paged_decode_shares_prefixes(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads, (int)H))
         plan_sharing(seqs, layer, c->block_size, 32 / (num_heads / (int)H), sp);
     const int nsg = (int)sp.sg_pages.size();
+    if (append && nsg)  // the appended token's page is written by its sequence's own item, never a shared one
+        for (int i = 0; i < n; ++i)
+            if ((size_t)sp.seq_pb[i] * c->block_size >= seqs[i]->layer_len[layer])
+                return set_error(ZK_ERR_INTERNAL, "Internal error: KVCache decode_append: token in a shared page");
     // Lengths at this layer, (fp8) this layer's scales [2][n][H], (shared
     // prefixes) seq_pb [n], sg_members [nsg][32], sg_pages [nsg].
     auto a256 = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -1213,7 +1220,7 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
                               (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
                               mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr, drows,
                               q_stride, /*trusted_tables=*/true,  // built from the sequences' handles
-                              reuse);
+                              reuse, append, &c->dec_head_set);
     if (rc == ZK_OK) c->plan_sig = std::move(sig);
     return rc;
 }
@@ -1311,6 +1318,33 @@ int zk_cache_paged_decode(zk_kv_cache *c, size_t layer, const char *const *ids, 
     std::vector<const SeqState *> seqs;
     if (int rc = find_seqs(c, ids, n, seqs)) return rc;
     return decode_batch(c, layer, seqs, nullptr, nullptr, q, q_dtype, 0, out, num_heads, scale, mapping, true);
+}
+
+int zk_cache_decode_append(zk_kv_cache *c, size_t layer, const char *const *ids, int n, const void *k, const void *v,
+                           zk_dtype src_dtype, const void *q, zk_dtype q_dtype, void *out, int num_heads, float scale,
+                           zk_gqa_mapping mapping) {
+    if (!c || (n > 0 && !ids))
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode_append: NULL argument");
+    if (layer >= c->num_layers)
+        return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode_append: layer out of range");
+    if (n <= 0) return ZK_OK;
+    if (!q || !out) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache decode_append: NULL q / out");
+    DeviceGuard g(c->device);
+    const std::vector<int32_t> ones((size_t)n, 1);
+    const bool fuse = c->dtype == ZK_BF16 && src_dtype == ZK_BF16 && k && v &&
+                      (((uintptr_t)k | (uintptr_t)v) & 15u) == 0 && (c->head_dim * 2) % 16 == 0 &&
+                      zk::paged_decode_fuses_append(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads,
+                                                    (int)c->num_kv_heads);
+    if (!fuse) {  // the two calls
+        if (int rc = zk_cache_write_batch(c, layer, ids, ones.data(), n, k, v, src_dtype, 0)) return rc;
+        return zk_cache_paged_decode(c, layer, ids, n, q, q_dtype, out, num_heads, scale, mapping);
+    }
+    WritePrep w;  // validation and copy-on-write; the decode kernel stores the rows
+    if (int rc = prepare_write(c, layer, ids, ones.data(), n, true, w, /*upload_slots=*/false)) return rc;
+    finish_write(c, layer, ones.data(), n, w);
+    const std::vector<const SeqState *> seqs(w.seqs.begin(), w.seqs.end());
+    const zk::AppendRows rows{k, v, (int64_t)(c->num_kv_heads * c->head_dim * 2)};
+    return decode_batch(c, layer, seqs, nullptr, nullptr, q, q_dtype, 0, out, num_heads, scale, mapping, true, &rows);
 }
 
 int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *ids, const int32_t *num_tokens, int n,

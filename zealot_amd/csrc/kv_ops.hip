@@ -126,6 +126,36 @@ append_copy_pow2_kernel(const char *__restrict__ k, const char *__restrict__ v, 
     st16_nt((kv ? v_pool : k_pool) + (row << row_log2) + (size_t)c * 16, data);
 }
 
+// The same copy with the work laid out by token, for power-of-two shapes
+// whose token moves 64..512 16-byte chunks (K and V rows of every head: 256
+// for 8 heads of 256-byte rows): a workgroup of 512 threads moves
+// 512 / chunks tokens, each wave lies inside one token, so the token's slot
+// is one scalar value (readfirstlane of a uniform load) and the destination
+// splits into a scalar row base plus a per-lane offset fixed by threadIdx.
+// Measured on C3 (64 x 512 tokens, 8 heads x 128 bf16): 49.9 vs 50.5-51.4 us
+// for append_copy_pow2_kernel; one or four tokens per workgroup, or one
+// thread moving a chunk of K and of V, were no faster.
+constexpr int kTokenBlock = 512;
+__global__ void __launch_bounds__(kTokenBlock)
+append_token_kernel(const char *__restrict__ k, const char *__restrict__ v, char *__restrict__ k_pool,
+                    char *__restrict__ v_pool, const int64_t *__restrict__ slots, uint32_t num_tokens,
+                    uint32_t tt_log2, uint32_t cpr_log2, uint32_t hkv_log2, uint32_t row_log2, uint32_t bs_log2,
+                    int64_t num_slots, uint64_t src_token_bytes) {
+    const uint32_t r = threadIdx.x & ((1u << tt_log2) - 1u);
+    const uint32_t t = blockIdx.x * (kTokenBlock >> tt_log2) + (threadIdx.x >> tt_log2);
+    if (t >= num_tokens) return;
+    const uint32_t half = tt_log2 - 1;  // K chunks of a token: Hkv * chunks per row
+    const uint32_t kv = r >> half, h = (r >> cpr_log2) & ((1u << hkv_log2) - 1u), c = r & ((1u << cpr_log2) - 1u);
+    const int64_t sl = slots[t];  // the same for the whole wave
+    const int64_t slot = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(sl >> 32)) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readfirstlane((int)sl));
+    const uint4 data = ld16_nt((kv ? v : k) + (size_t)t * src_token_bytes + ((size_t)(r & ((1u << half) - 1u)) << 4));
+    if (slot < 0 || slot >= num_slots) return;
+    const uint64_t blk = (uint64_t)slot >> bs_log2, tib = (uint64_t)slot & ((1u << bs_log2) - 1u);
+    const uint64_t base = (((blk << hkv_log2) << bs_log2) + tib) << row_log2;
+    st16_nt((kv ? v_pool : k_pool) + base + ((uint64_t)h << (bs_log2 + row_log2)) + (c << 4), data);
+}
+
 // Quantising append into an fp8 pool: one 16-element chunk per index; the
 // source chunk is 32 B (bf16) or 64 B (f32), the destination chunk 16 B.
 template <int SRC>  // ZK_BF16 or ZK_F32
@@ -410,27 +440,56 @@ stream_copy_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, uint6
     if (i < n16) st16_nt(dst + i, ld16_nt(src + i));
 }
 
-// Streaming read (the read-bandwidth yardstick): each workgroup reads one
-// contiguous range (on multi-GB buffers a grid-stride walk, which touches a
-// new region on every step, measured 8 % slower), 4 x 16 B non-temporal loads
-// per lane in flight, folded into one word that is stored only when it
-// equals a value it cannot take for the yardstick's inputs.
-__global__ void __launch_bounds__(kThreads)
-stream_read_kernel(const u32x4 *__restrict__ src, uint64_t n16, uint32_t *__restrict__ sink) {
-    const uint64_t per = (n16 + gridDim.x - 1) / gridDim.x;
-    const uint64_t span = (per + 4 * kThreads - 1) / (4 * kThreads) * (4 * kThreads);
-    uint64_t i = (uint64_t)blockIdx.x * span + threadIdx.x;
-    const uint64_t end = min(n16, (uint64_t)(blockIdx.x + 1) * span);
-    const uint64_t stride = (uint64_t)kThreads * 4;
-    u32x4 acc = {0, 0, 0, 0};
-    for (; i + 3 * kThreads < end; i += stride) {
-        const u32x4 a = __builtin_nontemporal_load(src + i), b = __builtin_nontemporal_load(src + i + kThreads);
-        const u32x4 c = __builtin_nontemporal_load(src + i + 2 * kThreads);
-        const u32x4 d = __builtin_nontemporal_load(src + i + 3 * kThreads);
-        acc ^= a ^ b ^ c ^ d;
+// Streaming read (the read-bandwidth yardstick): persistent one-wave
+// workgroups, one per CU, sweep the buffer in 8 KiB chunks interleaved over
+// the waves (chunk c belongs to wave c % grid, so the whole grid advances
+// through the buffer together), each wave keeping three chunks in flight by
+// global_load_lds_dwordx4 (nontemporal, no VGPRs; the LDS copies are never
+// read).  Measured on MI355X against one contiguous range per 256-thread
+// workgroup with four 16-B register loads per lane in flight (the previous
+// yardstick): 7.44 vs 7.05 TB/s on 2.5 GiB and 7.45 vs 6.69 TB/s on 4.9 GiB;
+// deeper or shallower rings, 2-4 KiB chunks and 2-4 waves per CU were 1-15 %
+// slower.  The tail (bytes % 8 KiB) goes through 16-byte register loads.
+constexpr int kReadChunk = 8192, kReadStages = 3;
+typedef __attribute__((address_space(3))) void lds_void_t;
+template <int N>
+__device__ __forceinline__ void read_wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__global__ void __launch_bounds__(64)
+stream_read_kernel(const char *__restrict__ src, uint64_t bytes, uint32_t *__restrict__ sink) {
+    constexpr int L = kReadChunk / 1024;  // loads per chunk
+    __shared__ __attribute__((aligned(16))) char ring[kReadStages][kReadChunk];
+    const int lane = threadIdx.x;
+    const uint64_t nch = bytes / kReadChunk, step = gridDim.x;
+    auto issue = [&](uint64_t c, int s) {
+        const char *g = src + c * kReadChunk + lane * 16;
+#pragma unroll
+        for (int j = 0; j < L; ++j)
+            __builtin_amdgcn_global_load_lds(g + 1024 * j, (lds_void_t *)(ring[s] + 1024 * j), 16, 0, /*NT*/ 2);
+    };
+    uint64_t c = blockIdx.x;
+#pragma unroll
+    for (int j = 0; j < kReadStages - 1; ++j)
+        if (c + j * step < nch) issue(c + j * step, j);
+    int s = kReadStages - 1;
+    for (; c < nch; c += step, s = s == kReadStages - 1 ? 0 : s + 1) {
+        if (c + (kReadStages - 1) * step < nch) {
+            issue(c + (kReadStages - 1) * step, s);
+            read_wait_vmcnt<(kReadStages - 1) * L>();  // chunk c has landed
+        } else {
+            read_wait_vmcnt<0>();
+        }
     }
-    for (; i < end; i += kThreads) acc ^= __builtin_nontemporal_load(src + i);
-    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u) sink[0] = 1u;
+    // tail bytes after the whole chunks, folded into a word that is stored
+    // only when it equals a value it cannot take for the yardstick's inputs
+    uint32_t acc = 0;
+    for (uint64_t i = nch * kReadChunk / 16 + (uint64_t)blockIdx.x * 64 + lane; i < bytes / 16; i += step * 64) {
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + i);
+        acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+    }
+    if (acc == 0x9e3779b9u) sink[0] = 1u;
 }
 
 // Block-table update: one entry per thread.
@@ -526,7 +585,14 @@ int zk::append(void *k_pool, void *v_pool, zk_dtype cache_dtype, const void *k, 
         auto pow2 = [](uint64_t x) { return x > 0 && (x & (x - 1)) == 0; };
         auto log2u = [](uint64_t x) { return (uint32_t)__builtin_ctzll(x); };
         KernelTimer timer("append", s);
-        if (pow2(cpr) && pow2((uint64_t)num_kv_heads) && pow2(block_size))
+        const uint64_t tt = 2ull * cpr * (uint64_t)num_kv_heads;  // 16-byte chunks per token
+        if (pow2(cpr) && pow2((uint64_t)num_kv_heads) && pow2(block_size) && tt >= 64 && tt <= kTokenBlock) {
+            const uint64_t per = kTokenBlock / tt;
+            append_token_kernel<<<(uint32_t)(((uint64_t)num_tokens + per - 1) / per), kTokenBlock, 0, s>>>(
+                (const char *)k, (const char *)v, (char *)k_pool, (char *)v_pool, slot_mapping, (uint32_t)num_tokens,
+                log2u(tt), log2u(cpr), log2u((uint64_t)num_kv_heads), log2u(row_bytes), log2u((uint64_t)block_size),
+                num_slots, src_token_bytes);
+        } else if (pow2(cpr) && pow2((uint64_t)num_kv_heads) && pow2(block_size))
             append_copy_pow2_kernel<<<grid, kThreads, 0, s>>>(
                 (const char *)k, (const char *)v, (char *)k_pool, (char *)v_pool, slot_mapping, total, log2u(cpr),
                 log2u((uint64_t)num_kv_heads), log2u(row_bytes), log2u((uint64_t)block_size), num_slots,
@@ -672,13 +738,12 @@ int zk_stream_read(const void *src, size_t bytes, uint32_t *sink, void *stream) 
     if (!src || !sink || (bytes & 15u) || ((uintptr_t)src & 15u))
         return set_error(ZK_ERR_INVALID_ARGUMENT,
                          "Internal error: zk_stream_read: needs a 16-B aligned pointer and size, and a sink");
-    const uint64_t n16 = bytes / 16;
-    const uint64_t want = (n16 + kThreads * 4 - 1) / (kThreads * 4);
-    // 16 workgroups per CU: 2 % above 4 per CU on 1 GiB reads, the best of the
-    // read shapes measured (one chunk per thread, 4 chunks per thread one-shot)
-    const uint32_t grid = (uint32_t)(want < 4096 ? (want ? want : 1) : 4096);
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
     KernelTimer timer("stream_read", (hipStream_t)stream);
-    stream_read_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>((const u32x4 *)src, n16, sink);
+    stream_read_kernel<<<(uint32_t)cus, 64, 0, (hipStream_t)stream>>>((const char *)src, (uint64_t)bytes, sink);
     return check_launch("zk_stream_read");
 }
 

@@ -80,7 +80,12 @@ constexpr int kSgStride = 32;  // member slots per prefix subgroup (query rows o
 // lines instead of one, whose atomics the L2 serialises.
 constexpr int kQueues = 8;
 constexpr int kQueueStride = 32;  // int32 slots between heads
-constexpr size_t kWorkBytes = sizeof(int32_t) * kQueueStride * (kQueues + 1);
+// Two sets of queue heads: a launch takes its items through set
+// Params::head_set and puts the other set back to its start values, which
+// the launch after it (same workspace, same stream) then uses; the plan
+// kernel sets both.  So launches that reuse a plan (the layers of one step)
+// need no kernel of their own to reset the heads.
+constexpr size_t kWorkBytes = sizeof(int32_t) * kQueueStride * (2 * kQueues + 1);
 
 struct Params {
     const void *q;        // [rows, H, D]; sequence n's row is q_rows[n] (n when q_rows is null)
@@ -99,10 +104,18 @@ struct Params {
                           //   {n, part, first page, pages} of a sequence's own pages or
                           //   {-1 - g, part, member 0, pages} of subgroup g's shared pages,
                           //   then the block ids of the item's first kDescPages pages
-    int32_t *work;        // total items at [0]; the head of queue j at [kQueueStride * (j + 1)] (MFMA path)
+    int32_t *work;        // total items at [0]; the head of queue j of set s at
+                          // [kQueueStride * (1 + j + s * kQueues)] (MFMA path)
     int num_waves;        // persistent grid: wave w starts with item w
     int queues;           // work queues in use (1 or kQueues)
-    int reset_queues;     // the reduce kernel puts the queue heads back (MFMA path)
+    int head_set;         // the set of queue heads this launch claims from (0 or 1)
+    // Fused append (MFMA bf16 path; null when unused): the step's K / V row
+    // of sequence n, kv-head h, at new_k / new_v + n * new_row_bytes + h * D * 2,
+    // is the token at position len - 1; the item holding the sequence's last
+    // page stores it into the pools and attends it from registers.
+    const char *new_k;
+    const char *new_v;
+    int64_t new_row_bytes;
     float2 *ml;   // [N][H][MP] (m, l), log2 domain
     float *po;    // [N][H][MP][D]
     // Shared prefixes (MFMA bf16 path; all null when unused): sequence n's
@@ -314,8 +327,9 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
     if (t == 0) {
         p.work[0] = total_pairs * p.num_kv_heads;  // total items
     }
-    if (t < p.queues) {  // queue heads: wave w takes item w statically, w < num_waves
-        p.work[kQueueStride * (t + 1)] = (p.num_waves - t + p.queues - 1) / p.queues;
+    if (t < p.queues) {  // queue heads, both sets: wave w takes item w statically, w < num_waves
+        p.work[kQueueStride * (1 + t)] = (p.num_waves - t + p.queues - 1) / p.queues;
+        p.work[kQueueStride * (1 + t + kQueues)] = (p.num_waves - t + p.queues - 1) / p.queues;
     }
 }
 
@@ -436,7 +450,11 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
     // while waves that finish their short items find the queue empty: with
     // mixed item lengths that left a tail of late short items.)
     const int nq = p.queues, xq = blockIdx.x % nq;
-    auto head = [&](int q) { return p.work + kQueueStride * (q + 1); };
+    auto head = [&](int q) { return p.work + kQueueStride * (1 + q + p.head_set * kQueues); };
+    // the other set of heads back to its start for the next launch on this
+    // workspace (no wave of this launch touches it)
+    if (blockIdx.x == 0 && lane < nq)
+        p.work[kQueueStride * (1 + lane + (1 - p.head_set) * kQueues)] = (p.num_waves - lane + nq - 1) / nq;
     auto claim_next = [&]() {
         if (lane == 0) next = atomicAdd(head(xq), 1);
     };
@@ -528,7 +546,7 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
                 }
             nx = __builtin_amdgcn_readfirstlane(got);
         }
-        const int k = min(nx / Hkv, desc_cap - 1);
+        const int k = __builtin_amdgcn_readfirstlane(min(nx / Hkv, desc_cap - 1));
         asm volatile("s_load_dwordx8 %0, %1, 0x0" : "=s"(nraw) : "s"(p.items + 2 * (size_t)k) : "memory");
         have_next = true;
     };
@@ -538,14 +556,22 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         b = make_int4(nraw[4], nraw[5], nraw[6], nraw[7]);
     };
 
+    // q / out row of sequence n
+    auto q_row = [&](int n) -> size_t { return p.q_rows ? (size_t)((cint_t)p.q_rows)[n] : (size_t)n; };
+
     // Attention of T tiles of query rows (qf) over pages [page0, page0 + np)
     // of table `trow` for kv-head kvh; tokens at positions >= len are masked.
     // trow points at the table entry of page page0; blk0 holds the block ids
     // of the first kDescPages pages.
     // Leaves O^T (o), the rows' reference max (m) and sum (l, all 4 lane
-    // groups) for the caller to write.
+    // groups) for the caller to write.  fuse_tib >= 0 (fused append): the
+    // last page's row fuse_tib is the step's token, nrow in this wave's
+    // registers (lane c < CPR: chunk c of K, CPR <= lane < 2 CPR: of V); it is
+    // written into the page's LDS copy once that has landed, and to the pools
+    // at byte offset row_dst of the K / V pool.
     auto attend = [&]<int T>(const bf16x8 (&qf)[T][KK], const int32_t *trow, int4 blk0, int page0, int np, int len,
-                             int kvh, float sl2, f32x4 (&o)[DT][T], float (&m)[T], float (&l)[T]) {
+                             int kvh, float sl2, f32x4 (&o)[DT][T], float (&m)[T], float (&l)[T], int fuse_tib,
+                             u32x4 nrow, size_t row_dst) {
         const char *kbase = p.k_pool + ((size_t)kvh * PAGE);
         const char *vbase = p.v_pool + ((size_t)kvh * PAGE);
         const size_t block_bytes = (size_t)PAGE * Hkv;
@@ -566,6 +592,18 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         }
         auto page = [&](int pi, int s) {
             wait_page(pi, np);
+            if constexpr (KV == ZK_BF16) {
+                if (fuse_tib >= 0 && pi == np - 1) {  // the step's token over the page's stale row
+                    if (lane < CPR)
+                        *reinterpret_cast<u32x4 *>(lds[s][0] + (fuse_tib * CPR + (lane ^ (fuse_tib % CPR))) * 16) =
+                            nrow;
+                    else if (lane < 2 * CPR)
+                        *reinterpret_cast<u32x4 *>(lds[s][1] + fuse_tib * RB + (lane - CPR) * 16) = nrow;
+                    if (lane < 2 * CPR)
+                        __builtin_nontemporal_store(
+                            nrow, reinterpret_cast<u32x4 *>((char *)(lane < CPR ? p.k_pool : p.v_pool) + row_dst));
+                }
+            }
             uint32_t kw[KBYTES / 4];
 #pragma unroll
             for (int f = 0; f < KCH; ++f) {
@@ -682,6 +720,8 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
         for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) asm volatile("" ::"v"(qf[t][kk]));
+        // and so is the fused row
+        asm volatile("" ::"v"(nrow[0]), "v"(nrow[1]), "v"(nrow[2]), "v"(nrow[3]));
         if (np <= kStages) claim_next();
         // one page per iteration (a single loop-carried accumulator set)
         for (int pi = 0, st = 0; pi < np; ++pi, st = (st + 1 == kStages ? 0 : st + 1)) page(pi, st);
@@ -703,8 +743,12 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             __builtin_memcpy(dst + DT * (4 * grp + i), v, sizeof(v));
         }
     };
-    // q / out row of sequence n
-    auto q_row = [&](int n) -> size_t { return p.q_rows ? (size_t)((cint_t)p.q_rows)[n] : (size_t)n; };
+    // a partial slot and its (m, l), for decode_reduce_kernel
+    auto store_partial = [&](size_t slot, const f32x4 (&o)[DT][2], int t, float scale, float m_, float l_) {
+        store_row_f32(p.po + slot * D, o, t, scale);
+        if (grp == 0) p.ml[slot] = make_float2(m_, l_);
+    };
+    const u32x4 no_row = {0u, 0u, 0u, 0u};
 
     int item = blockIdx.x;  // first item static, the rest from the queue
     int4 d0 = make_int4(0, 0, 0, 0), d1 = make_int4(0, 0, 0, 0);
@@ -740,14 +784,13 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
             f32x4 o[DT][2];
             float m[2], l[2];
             attend.template operator()<2>(qf, p.bt + (size_t)n0 * p.max_blocks + page0, d1, page0, np, 0x7fffffff,
-                                          kvh, p.scale_log2, o, m, l);
+                                          kvh, p.scale_log2, o, m, l, -1, no_row, 0);
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int r = 16 * t + col;
                 if (nm[t] >= 0) {
                     const size_t slot = ((size_t)nm[t] * H + qhead_of(p, kvh, r % G, G)) * p.max_parts + part;
-                    store_row_f32(p.po + slot * D, o, t, 1.0f);
-                    if (grp == 0) p.ml[slot] = make_float2(m[t], l[t]);
+                    store_partial(slot, o, t, 1.0f, m[t], l[t]);
                 }
             }
         } else {
@@ -770,10 +813,25 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
                 sl2 *= ((cfloat_t)p.k_scales)[(size_t)n * Hkv + kvh];
                 vscale = ((cfloat_t)p.v_scales)[(size_t)n * Hkv + kvh];
             }
+            // fused append: the item holding the sequence's last page
+            int fuse_tib = -1;
+            u32x4 nrow = no_row;
+            size_t row_dst = 0;
+            if constexpr (KV == ZK_BF16) {
+                if (p.new_k && len > 0 && np > 0 && page0 + np == (len + BS - 1) / BS) {
+                    fuse_tib = (len - 1) % BS;
+                    const int blk = ((cint_t)p.bt)[(size_t)n * p.max_blocks + (len - 1) / BS];
+                    const int c = lane % CPR;
+                    row_dst = ((size_t)blk * Hkv + kvh) * PAGE + (size_t)fuse_tib * RB + (size_t)c * 16;
+                    if (lane < 2 * CPR)
+                        nrow = *reinterpret_cast<const u32x4 *>((lane < CPR ? p.new_k : p.new_v) +
+                                                                (size_t)n * p.new_row_bytes + (size_t)kvh * RB + c * 16);
+                }
+            }
             f32x4 o[DT][1];
             float m[1], l[1];
             attend.template operator()<1>(qf, p.bt + (size_t)n * p.max_blocks + page0, d1, page0, np, len, kvh, sl2,
-                                          o, m, l);
+                                          o, m, l, fuse_tib, nrow, row_dst);
             if (col < G) {
                 if (ns == 0 && nparts <= 1) {  // the whole context: write the output row
                     const float inv = l[0] > 0.0f ? vscale / l[0] : 0.0f;
@@ -798,28 +856,18 @@ __global__ void __launch_bounds__(kWave) decode_mfma_kernel(Params p) {
                     f32x4 o2[DT][2];
 #pragma unroll
                     for (int dt = 0; dt < DT; ++dt) o2[dt][0] = o[dt][0];
-                    store_row_f32(p.po + slot * D, o2, 0, vscale);
-                    if (grp == 0) p.ml[slot] = make_float2(m[0], l[0]);
+                    store_partial(slot, o2, 0, vscale, m[0], l[0]);
                 }
             }
         }
         if (!have_next) fetch_next();  // an item without pages
         item = nx;
         desc_ready(d0, d1);
+        // consumed: a constant until the next fetch, so the descriptor's
+        // scalar registers are not kept across the next item's prologue
+        nraw = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
 }
-
-// Every MFMA launch ends with the queue heads back where the plan put them,
-// so the next launch on the same plan (the next layer of a step) starts
-// without a kernel of its own for that: the reduce kernel resets them (it
-// runs after the decode kernel has drained), or, when there is nothing to
-// reduce, queue_reset_kernel.  (Resetting them from the decode kernel's last
-// wave instead measured 20 % slower on the fp8 decode: every wave then waits
-// for its own stores before it exits.)
-__device__ __forceinline__ void reset_queue_heads(const Params &p, int t) {
-    if (t < p.queues) p.work[kQueueStride * (t + 1)] = (p.num_waves - t + p.queues - 1) / p.queues;
-}
-__global__ void __launch_bounds__(64) queue_reset_kernel(Params p) { reset_queue_heads(p, threadIdx.x); }
 
 // ------------------------------------------------------------ generic kernel
 // One wavefront per (partition, kv-head, sequence).  Lane = token for QK
@@ -956,7 +1004,6 @@ __global__ void __launch_bounds__(kWave) decode_generic_kernel(Params p) {
 // the partitions eight at a time so 16 loads per lane are in flight.
 __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    if (p.reset_queues && h == 0 && n == 0) reset_queue_heads(p, lane);
     const int ns = shared_parts_of(p, n);
     const int nparts = ns + private_parts_of(p, n);
     if (ns == 0 && nparts <= 1) return;  // written by the partition kernel
@@ -1009,7 +1056,6 @@ __global__ void __launch_bounds__(kWave) decode_reduce_vec_kernel(Params p) {
     constexpr int LP = D / 4, P = kWave / LP, U = 16;  // lanes per partition, partitions per load, loads per lane
     static_assert(D % 4 == 0 && kWave % LP == 0, "partition layout");
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    if (p.reset_queues && h == 0 && n == 0) reset_queue_heads(p, lane);
     const int ns = shared_parts_of(p, n);
     const int nparts = ns + private_parts_of(p, n);
     if (ns == 0 && nparts <= 1) return;  // written by the partition kernel
@@ -1182,6 +1228,10 @@ bool zk::paged_decode_shares_prefixes(int kv_dtype, int head_dim, int block_size
            mfma_supported(kv_dtype, head_dim, block_size, num_heads / num_kv_heads);
 }
 
+bool zk::paged_decode_fuses_append(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads) {
+    return zk::paged_decode_shares_prefixes(kv_dtype, head_dim, block_size, num_heads, num_kv_heads);
+}
+
 namespace {
 
 // Host-side argument checks of zk_paged_decode (no device work).
@@ -1239,7 +1289,8 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                      int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                      float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                      void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
-                     const int32_t *q_rows, int64_t q_stride, bool trusted_tables, bool reuse_plan) {
+                     const int32_t *q_rows, int64_t q_stride, bool trusted_tables, bool reuse_plan,
+                     const AppendRows *append, int *head_set) {
     if (int rc = check_decode_args(q_dtype, kv_dtype, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
                                    max_blocks_per_seq, num_blocks, mapping))
         return rc;
@@ -1257,6 +1308,12 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     const DecodeShape ds =
         decode_shape(kv_dtype, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, pg);
     const bool use_mfma = ds.use_mfma, shared = ds.shared;
+    if (append && (!use_mfma || kv_dtype != ZK_BF16 || !trusted_tables || !append->k || !append->v ||
+                   append->row_bytes < (int64_t)num_kv_heads * head_dim * 2 || (append->row_bytes & 15) ||
+                   (((uintptr_t)append->k | (uintptr_t)append->v) & 15u)))
+        return set_error(ZK_ERR_INVALID_ARGUMENT,
+                         "Internal error: paged decode: fused append needs the bf16 MFMA path, trusted tables and "
+                         "16-byte aligned rows");
     const int part_pages = ds.part_pages, shared_pages = ds.shared_pages, max_parts = ds.max_parts;
     const WsLayout &w = ds.w;
     if (workspace_bytes < w.total || ((uintptr_t)workspace & 255u))
@@ -1301,6 +1358,11 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.scale_log2 = scale * kLog2e;
     p.grouped = mapping == ZK_GQA_GROUPED ? 1 : 0;
     p.q_f32 = q_dtype == ZK_F32 ? 1 : 0;
+    if (append) {
+        p.new_k = (const char *)append->k;
+        p.new_v = (const char *)append->v;
+        p.new_row_bytes = append->row_bytes;
+    }
 
     hipStream_t s = (hipStream_t)stream;
     reuse_plan = reuse_plan && use_mfma;
@@ -1313,18 +1375,25 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     }
     const bool reduce = max_parts > 1 || shared;
     if (use_mfma) {
-        p.reset_queues = 1;
-        if (!reuse_plan) {  // a reused plan's queue heads were reset by the launch before
+        // a launch reusing the plan claims from the head set the launch
+        // before it put back
+        reuse_plan = reuse_plan && head_set;
+        p.head_set = reuse_plan ? (*head_set & 1) : 0;
+        if (!reuse_plan) {
             {
                 KernelTimer timer("decode_plan", s);
                 plan_kernel<<<1, 1024, 0, s>>>(p, num_seqs);
             }
             if (int rc = check_launch("zk_paged_decode plan")) return rc;
         }
-        KernelTimer timer("decode_partials", s);
-        const int grid = p.num_waves;
-        if (kv_dtype == ZK_BF16) launch_mfma<ZK_BF16>(p, grid, s, G);
-        else launch_mfma<ZK_FP8_E4M3>(p, grid, s, G);
+        {
+            KernelTimer timer("decode_partials", s);
+            const int grid = p.num_waves;
+            if (kv_dtype == ZK_BF16) launch_mfma<ZK_BF16>(p, grid, s, G);
+            else launch_mfma<ZK_FP8_E4M3>(p, grid, s, G);
+        }
+        if (int rc = check_launch("zk_paged_decode partials")) return rc;
+        if (head_set) *head_set = p.head_set ^ 1;
     } else {
         KernelTimer timer("decode_partials", s);
         dim3 grid(max_parts, num_kv_heads, num_seqs);
@@ -1333,13 +1402,6 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
         else decode_generic_kernel<ZK_FP8_E4M3><<<grid, kWave, 0, s>>>(p);
     }
     if (int rc = check_launch("zk_paged_decode partials")) return rc;
-    if (use_mfma && !reduce) {
-        {
-            KernelTimer timer("decode_plan", s);
-            queue_reset_kernel<<<1, 64, 0, s>>>(p);
-        }
-        if (int rc = check_launch("zk_paged_decode queue reset")) return rc;
-    }
     if (reduce) {
         dim3 rgrid(num_heads, num_seqs);
         KernelTimer timer("decode_reduce", s);

@@ -99,12 +99,26 @@ struct PrefixGroups {
 // invalid entry is skipped.  reuse_plan: the previous call on this workspace
 // and stream had the same lengths, tables, prefix groups and shapes (another
 // layer of the same step), so its work items stand and planning is skipped.
+// append (fused append; bf16 MFMA shapes with trusted tables only): row n
+// of append->k / ->v (bf16 [Hkv, D], row_bytes apart) is sequence n's token
+// at position seq_lens[n] - 1; the decode stores it into the pools and
+// attends it (that page must not be a shared-prefix page).  head_set: the
+// caller's record of which queue-head set the next launch on this workspace
+// uses when it reuses the plan (0 after a planning launch's successor
+// flips it); null: every launch plans.
+struct AppendRows {
+    const void *k, *v;
+    int64_t row_bytes;
+};
 int paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
                  void *out, const int32_t *block_tables, const int32_t *seq_lens, int num_seqs, int num_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                  float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                  void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
-                 const int32_t *q_rows, int64_t q_stride = 0, bool trusted_tables = false, bool reuse_plan = false);
+                 const int32_t *q_rows, int64_t q_stride = 0, bool trusted_tables = false, bool reuse_plan = false,
+                 const AppendRows *append = nullptr, int *head_set = nullptr);
+// Whether paged_decode can take a fused append for this shape.
+bool paged_decode_fuses_append(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads);
 // zk_paged_prefill with the chunk rows of sequence n given as a device
 // offset and length (q_off[n], q_len[n]) instead of cu_seqlens_q; total_q is
 // an upper bound of the rows; q rows are q_stride elements apart (0 = H * D).

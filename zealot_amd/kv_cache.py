@@ -255,6 +255,26 @@ class KVCache:
                                                     zk_dtype(q), _dev(out, "out"), h, float(scale), m))
         return out
 
+    def decode_append(self, layer: int, ids, k, v, q, out=None, scale=None, mapping="grouped"):
+        """append_kv_batch(layer, ids, k, v) then paged_decode(layer, ids, q),
+        with the same results; one decode launch on bf16 MFMA shapes (the
+        decode stores each sequence's new K / V row and attends it)."""
+        _dev(q, "q")
+        b = _batch(ids)
+        n, h, d = q.shape
+        if n != len(b) or d != self.head_dim:
+            raise ValueError("q must be [len(ids), H, head_dim]")
+        dt = self._kv(k, v, n)
+        if out is None:
+            out = torch.empty_like(q)
+        if scale is None:
+            scale = 1.0 / math.sqrt(d)
+        m = {"grouped": _lib.GQA_GROUPED, "modulo": _lib.GQA_MODULO}[mapping]
+        _lib.check(_lib.lib().zk_cache_decode_append(self._h, layer, b.arr, n, k.data_ptr(), v.data_ptr(), dt,
+                                                     q.data_ptr(), zk_dtype(q), _dev(out, "out"), h, float(scale),
+                                                     m))
+        return out
+
     def attention_batch(self, layer: int, ids, num_tokens, q, out=None, scale=None, mapping="grouped"):
         """Mixed step attention after write_batch: the num_tokens[i] rows of
         sequence ids[i] (packed in batch order in q [sum(num_tokens), H, D])
