@@ -1050,10 +1050,14 @@ __global__ void __launch_bounds__(kWave) decode_reduce_kernel(Params p) {
 // partition's partial output as one float4 each, so one load instruction
 // covers 64 / LP partitions and all of a sequence's partitions are in flight
 // at once (the loop above waits for each group of eight).  Lane i reads
-// partition i's (m, l) once for the maximum, the sum and its weight.
+// partition i's (m, l) once for the maximum, the sum and its weight; the
+// first 64 * U0 / LP partials are loaded beside the (m, l), so after the
+// lengths a row of up to that many partitions needs one more memory round
+// trip, not two.
 template <int D>
 __global__ void __launch_bounds__(kWave) decode_reduce_vec_kernel(Params p) {
     constexpr int LP = D / 4, P = kWave / LP, U = 16;  // lanes per partition, partitions per load, loads per lane
+    constexpr int U0 = 4;  // loads per lane issued with the (m, l): few, so that four waves fit a SIMD
     static_assert(D % 4 == 0 && kWave % LP == 0, "partition layout");
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
     const int ns = shared_parts_of(p, n);
@@ -1061,6 +1065,16 @@ __global__ void __launch_bounds__(kWave) decode_reduce_vec_kernel(Params p) {
     if (ns == 0 && nparts <= 1) return;  // written by the partition kernel
     const size_t base = ((size_t)n * p.num_heads + h) * p.max_parts;
     const float2 none = make_float2(-INFINITY, 0.0f);
+    const int sub = lane / LP, j = lane % LP;  // partition slot within a load, float4 index
+    // the first P * U0 partials go out with the (m, l) loads: one round trip
+    // instead of two (they do not depend on the maximum)
+    const int cnt0 = min(kWave, nparts);
+    f32x4 x0[U0];
+#pragma unroll
+    for (int u = 0; u < U0; ++u) {
+        const int i = P * u + sub;
+        x0[u] = i < cnt0 ? *reinterpret_cast<const f32x4 *>(p.po + (base + i) * D + 4 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     const float2 ml0 = lane < nparts ? p.ml[base + lane] : none;
     float M = ml0.x;
     for (int i = lane + kWave; i < nparts; i += kWave) M = fmaxf(M, p.ml[base + i].x);
@@ -1073,7 +1087,6 @@ __global__ void __launch_bounds__(kWave) decode_reduce_vec_kernel(Params p) {
     }
     for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    const int sub = lane / LP, j = lane % LP;  // partition slot within a load, float4 index
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int c0 = 0; c0 < nparts; c0 += kWave) {  // weights of partitions c0 .. c0 + 63 in lanes
         const float w = weight(c0 == 0 ? ml0 : (c0 + lane < nparts ? p.ml[base + c0 + lane] : none));
@@ -1085,8 +1098,9 @@ __global__ void __launch_bounds__(kWave) decode_reduce_vec_kernel(Params p) {
             for (int u = 0; u < U; ++u) {
                 const int i = i0 + P * u + sub;
                 wi[u] = __shfl(w, min(i, kWave - 1));
-                x[u] = i < cnt ? *reinterpret_cast<const f32x4 *>(p.po + (base + c0 + i) * D + 4 * j)
-                               : f32x4{0.f, 0.f, 0.f, 0.f};
+                if (c0 == 0 && i0 == 0 && u < U0) x[u] = x0[u];
+                else x[u] = i < cnt ? *reinterpret_cast<const f32x4 *>(p.po + (base + c0 + i) * D + 4 * j)
+                                    : f32x4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
             for (int u = 0; u < U; ++u)
