@@ -226,3 +226,29 @@ def test_hip_attention_paged_forward(H, Hkv, D, dt):
     with pytest.raises(RuntimeError, match="multiple of num_kv_heads"):
         att.paged_forward(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), btd.data_ptr(), ld.data_ptr(),
                           o.data_ptr(), len(lens), H + 1, Hkv, D, 16, bt.shape[1], nb, q_dtype=zdt, kv_dtype=zdt)
+
+
+def test_fp8_decode_dequantises_every_e4m3_code_exactly():
+    """All 256 e4m3 codes through the fp8 decode's in-register dequantisation:
+    a one-token context with zero K (every score 0, weight 1) and unit scales
+    returns the V row itself, so each output element is the code's exact value
+    in bf16 (every e4m3 value is a bf16 value; the two NaN codes give NaN).  The decoded values are pinned by the OCP e4m3 definition
+    through oracle.f32_from_e4m3_bits (tests/test_oracle.py)."""
+    from zealot_amd import ops
+    H, Hkv, D, BS = 1, 1, 128, 16
+    codes = np.arange(256, dtype=np.uint8)
+    n = 256 // D
+    kp = torch.zeros((n, Hkv, BS, D), dtype=torch.uint8, device="cuda")
+    vp = torch.zeros_like(kp)
+    vp[:, 0, 0, :] = torch.from_numpy(codes.reshape(n, D)).cuda()
+    bt = np.arange(n, dtype=np.int32).reshape(n, 1)
+    ones = torch.ones((n, Hkv), dtype=torch.float32, device="cuda")
+    q = torch.zeros((n, H, D), dtype=torch.bfloat16, device="cuda")
+    announce("fp8 decode: every e4m3 code")
+    out = ops.paged_decode(q, kp, vp, to_dev(bt), to_dev(np.ones(n, np.int32)), k_scales=ones, v_scales=ones)
+    torch.cuda.synchronize()
+    got = as_f32(to_host(out), oracle.BF16).reshape(-1)
+    want = oracle.f32_from_e4m3_bits(codes).reshape(-1)
+    nan = np.isnan(want)
+    assert nan.sum() == 2 and np.all(np.isnan(got[nan]))
+    assert np.array_equal(got[~nan], want[~nan])  # exact values (-0 comes back as +0 from the accumulators)

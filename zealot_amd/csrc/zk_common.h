@@ -226,15 +226,14 @@ __device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float *o) {
     f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
     o[0] = lo[0]; o[1] = lo[1]; o[2] = hi[0]; o[3] = hi[1];
 }
-// Four e4m3 bytes -> four bf16 packed in two dwords (exact: every e4m3 value
-// is a bf16 value, so the high half of the f32 is the bf16).
+// Four e4m3 bytes -> four bf16 packed in two dwords, by gfx950's scaled
+// converter with scale 1 (v_cvt_scalef32_pk_bf16_fp8, two values per
+// instruction): exact, every e4m3 value is a bf16 value.
 __device__ __forceinline__ u32x2 e4m3x4_to_bf16x4(uint32_t w) {
-    f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-    f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-    u32x2 r;
-    r[0] = __builtin_amdgcn_perm(__float_as_uint(lo[1]), __float_as_uint(lo[0]), 0x07060302u);
-    r[1] = __builtin_amdgcn_perm(__float_as_uint(hi[1]), __float_as_uint(hi[0]), 0x07060302u);
-    return r;
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    const bf16x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+    return u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
 }
 
 }  // namespace zk
