@@ -181,8 +181,11 @@ int zk_paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const v
  * allocate device memory (code under HIP graph capture, serving loops and
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
  * workspace is the library's own device scratch of ZK_DECODE_SCRATCH_BYTES
- * (64 MiB), one copy per GPU, held from the first call on a device until the
- * process ends; the call allocates nothing and creates no events.  A call
+ * (64 MiB), one copy per GPU: it sits in a code object of its own, which the
+ * HIP runtime loads on a GPU at the first call there (not when the library's
+ * other kernels load), and is held until the process ends.  That first call
+ * looks the scratch's address up, so make it outside graph capture; later
+ * calls may be captured.  The call allocates nothing and creates no events.  A call
  * that needs more scratch than that (see zk_paged_decode_workspace_size; the
  * exact need depends on the batch) fails with ZK_ERR_INVALID_ARGUMENT and
  * launches nothing.  Every call on one GPU shares that GPU's scratch: calls
