@@ -212,7 +212,10 @@ int zk_cache_create(size_t num_blocks, size_t block_size, size_t num_layers, siz
 void zk_cache_destroy(zk_kv_cache *c);
 /* register_seq (kv_cache.rs:107-124): table of max_blocks entries set to -1. */
 int zk_cache_register_seq(zk_kv_cache *c, const char *id, size_t max_blocks);
-/* alloc_block (kv_cache.rs:127-161): allocate through `bm`, append to the table. */
+/* alloc_block (kv_cache.rs:127-161): allocate through `bm`, append to the table.
+ * The device table row is written by the next call that needs it (a KV
+ * write, the table pointer, fork, register, release), so a step's
+ * allocations reach the device in one upload. */
 int zk_cache_alloc_block(zk_kv_cache *c, const char *id, zk_block_manager *bm, size_t *block_id);
 /* release_seq (kv_cache.rs:164-166).  Also frees the sequence's handles
  * through the BlockManager they came from (the reference leaks them). */
@@ -312,7 +315,8 @@ int zk_cache_seq_swapped(zk_kv_cache *c, const char *id, int *swapped);
  * (k_scales/v_scales: host arrays of num_layers * Hkv floats). */
 int zk_cache_set_fp8_scales(zk_kv_cache *c, const char *id, const float *k_scales,
                             const float *v_scales);
-/* Raw pointers (kv_cache.rs:188-204). */
+/* Raw pointers (kv_cache.rs:188-204).  The table pointer call first applies
+ * queued table writes on the cache stream. */
 int zk_cache_block_table_ptr(zk_kv_cache *c, const char *id, const int32_t **out);
 void *zk_cache_k_pool_ptr(zk_kv_cache *c, size_t layer);
 void *zk_cache_v_pool_ptr(zk_kv_cache *c, size_t layer);

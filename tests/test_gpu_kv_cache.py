@@ -480,3 +480,53 @@ def test_decode_append_is_append_then_decode(dtype, H, Hkv, D):
     for k in kids:  # the forks copied the partial tail, the full blocks before it stay shared
         ids_k = ca.seq_state(k).block_ids
         assert ids_k[:20] == par[:20] and ids_k[20] != par[20]
+
+
+def test_device_table_rows_follow_queued_allocations():
+    """`alloc_block` queues its table write; the device rows
+    (`block_table_ptr`, kv_cache.rs:188-190) still read as the handles say:
+    after the pointer call, after a batched write that flushes the queue, in a
+    fork's copied row, and in a row reset by release / register."""
+    import ctypes
+    import zealot_amd as ze
+    from zealot_amd import KVCache, _lib
+    L, H, D, BS, NB, MB = 2, 2, 32, 16, 64, 8
+    bm = ze.BlockManager(NB, BS)
+    cache = KVCache(NB, BS, L, H, D, dtype=torch.bfloat16, max_seqs=4, max_blocks_per_seq=MB)
+    lib = _lib.lib()
+
+    def row(ptr):  # the device row as it is, without the pointer call's flush
+        dst = torch.empty(MB, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        _lib.check(lib.zk_stream_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(ptr), MB * 4, None))
+        torch.cuda.synchronize()
+        return dst.cpu().tolist()
+
+    def want(sid):
+        b = cache.seq_state(sid).block_ids
+        return b + [-1] * (MB - len(b))
+
+    announce("device table rows after queued allocations")
+    cache.register_seq("a", MB)
+    cache.register_seq("b", MB)
+    for sid in ("a", "b", "a", "a", "b"):
+        cache.alloc_block(sid, bm)
+    assert row(cache.block_table_ptr("a")) == want("a")
+    assert row(cache.block_table_ptr("b")) == want("b")
+    pa = cache.block_table_ptr("a")
+    cache.alloc_block("a", bm)                      # queued
+    x = torch.ones((3, H, D), dtype=torch.bfloat16, device="cuda")
+    cache.store_kv(0, "a", x, x, 0, 3)              # a batched write flushes the queue
+    assert row(pa) == want("a") and want("a")[3] >= 0
+    cache.alloc_block("a", bm)                      # queued, then copied by the fork
+    cache.fork_seq("a", "c")
+    assert row(cache.block_table_ptr("c")) == want("a") == want("c")
+    pb = cache.block_table_ptr("b")
+    cache.alloc_block("b", bm)                      # queued, then the row is reset
+    cache.release_seq("b")
+    cache.register_seq("d", MB)
+    assert row(cache.block_table_ptr("d")) == [-1] * MB
+    assert row(pb) == [-1] * MB or cache.block_table_ptr("d") != pb
+    for sid in ("a", "c", "d"):
+        cache.release_seq(sid)
+    assert bm.free_blocks == NB

@@ -67,7 +67,9 @@ struct DevBuf {
         }
         p = nullptr;
         cap = 0;
-        size_t want = std::max<size_t>(bytes, 4096);
+        // a quarter more than asked: tables and batches grow a little at a
+        // time, and each regrowth waits for the device
+        size_t want = std::max<size_t>(bytes + bytes / 4, 4096);
         ZK_HIP_CHECK(hipMalloc(&p, want), what);
         cap = want;
         return ZK_OK;
@@ -95,7 +97,7 @@ struct Staging {
         if (p) (void)hipHostFree(p);
         p = nullptr;
         cap = 0;
-        size_t want = std::max<size_t>(bytes, 4096);
+        size_t want = std::max<size_t>(bytes + bytes / 4, 64 << 10);  // freeing pinned memory waits for the device
         ZK_HIP_CHECK(hipHostMalloc(&p, want, hipHostMallocDefault), "KVCache pinned staging");
         cap = want;
         return ZK_OK;
@@ -233,7 +235,12 @@ void queue_table_entry(zk_kv_cache *c, const SeqState &s, size_t idx, int32_t va
     ++c->epoch;
 }
 
-// Apply the queued block-table writes in one launch.
+// Apply the queued block-table writes in one launch.  Writes may wait in the
+// queue: the decode and prefill build their tables from the host handles, so
+// only the device table rows (`zk_cache_block_table_ptr`, a fork's row copy,
+// a row reset) need them, and those call this first.  Every write flushes
+// too, so the queue stays short and a step's block allocations go to the
+// device as one upload and one launch.
 int flush_tables(zk_kv_cache *c) {
     if (c->tbl_updates.empty()) return ZK_OK;
     const size_t n = c->tbl_updates.size();
@@ -372,6 +379,7 @@ int write_tokens(zk_kv_cache *c, size_t layer, SeqState &s, const char *id, cons
         return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache ") + what + ": bad src dtype");
     if (n == 0) return ZK_OK;
     if (!k || !v) return set_error(ZK_ERR_INVALID_ARGUMENT, std::string("Internal error: KVCache ") + what + ": NULL k/v");
+    if (int rc = flush_tables(c)) return rc;
     if (s.swapped)
         return set_error(ZK_ERR_FAILED_PRECONDITION, std::string("Failed precondition: seq ") + id + " is swapped out");
     const size_t bs = c->block_size;
@@ -501,6 +509,7 @@ int prepare_write(zk_kv_cache *c, size_t layer, const char *const *ids, const in
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache write batch: layer out of range");
     if (n <= 0) return ZK_OK;
     DeviceGuard g(c->device);
+    if (int rc = flush_tables(c)) return rc;
     const size_t bs = c->block_size, H = c->num_kv_heads;
     const bool fp8 = c->dtype == ZK_FP8_E4M3;
     std::vector<SeqState *> &seqs = w.seqs;
@@ -644,6 +653,7 @@ int zk_cache_register_seq(zk_kv_cache *c, const char *id, size_t max_blocks) {
     s.max_blocks = max_blocks;
     s.layer_len.assign(c->num_layers, 0);
     s.slot = c->free_slots.back();
+    if (int rc = flush_tables(c)) return rc;  // queued writes land before the row is reset
     std::vector<int32_t> row(c->max_blocks_per_seq, -1);
     if (int rc = upload(c, c->table_row(s.slot), row.data(), row.size() * sizeof(int32_t))) return rc;
     c->free_slots.pop_back();
@@ -672,11 +682,7 @@ int zk_cache_alloc_block(zk_kv_cache *c, const char *id, zk_block_manager *bm, s
     DeviceGuard g(c->device);
     zk_block_handle h;
     if (int rc = zk_bm_allocate(bm, &h)) return rc;
-    queue_table_entry(c, *s, s->handles.size(), (int32_t)h.block_id);
-    if (int rc = flush_tables(c)) {
-        (void)zk_bm_free(bm, h);
-        return rc;
-    }
+    queue_table_entry(c, *s, s->handles.size(), (int32_t)h.block_id);  // applied by the next flush_tables
     s->bm = bm;
     s->handles.push_back(h);
     if (block_id) *block_id = (size_t)h.block_id;
@@ -698,8 +704,9 @@ int zk_cache_release_seq(zk_kv_cache *c, const char *id) {
         }
     }
     release_host_slots(c, *s);
+    int rc = flush_tables(c);  // queued writes for this row land before the reset
     std::vector<int32_t> row(c->max_blocks_per_seq, -1);
-    int rc = upload(c, c->table_row(s->slot), row.data(), row.size() * sizeof(int32_t));
+    if (!rc) rc = upload(c, c->table_row(s->slot), row.data(), row.size() * sizeof(int32_t));
     c->free_slots.push_back(s->slot);
     c->seqs.erase(id);
     ++c->epoch;
@@ -727,6 +734,11 @@ int zk_cache_fork_seq(zk_kv_cache *c, const char *parent, const char *child) {
     if (done < p->handles.size()) {
         const zk::ErrorSnapshot saved = zk::save_error();
         for (size_t i = 0; i < done; ++i) (void)zk_bm_free(p->bm, p->handles[i]);
+        return zk::restore_error(saved);
+    }
+    if (int rc = flush_tables(c)) {  // the parent's row is copied below
+        const zk::ErrorSnapshot saved = zk::save_error();
+        for (const auto &h : p->handles) (void)zk_bm_free(p->bm, h);
         return zk::restore_error(saved);
     }
     SeqState s = *p;
@@ -1080,6 +1092,8 @@ int zk_cache_block_table_ptr(zk_kv_cache *c, const char *id, const int32_t **out
     SeqState *s;
     if (int rc = find_seq(c, id, &s)) return rc;
     if (!out) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache: NULL out");
+    DeviceGuard g(c->device);
+    if (int rc = flush_tables(c)) return rc;
     *out = c->table_row(s->slot);
     return ZK_OK;
 }
