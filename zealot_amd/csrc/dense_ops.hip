@@ -105,46 +105,85 @@ rms_norm_kernel(const T *x, const T *residual, const T *__restrict__ w, T *out, 
     const T *rr = residual ? residual + (size_t)r_in * dim : nullptr;
     float v[MAXV][VEC], wv[MAXV][VEC];
     float ss = 0.0f;
+    if constexpr (PART) {
+        static_assert(VEC % 4 == 0, "f32x4 sums");
+        constexpr int N4 = VEC / 4;
+        // ranges loaded up front, within a budget of 32 16-byte loads a thread
+        constexpr int FB = 32 / (MAXV * N4);
+        constexpr int FL = FB < 1 ? 1 : FB > kFoldLoads ? kFoldLoads : FB;
+        const size_t plane4 = (size_t)gridDim.x * dim / 4;
+        f32x4 t[MAXV][FL][N4];
+        float a[MAXV][VEC];
+        // every load of the row before any arithmetic: the first FL ranges'
+        // sums, the residual and the weights in one memory round trip
+        // (no branch around a load: a lane past the row's end re-reads its
+        // start, a range past `splits` range 0, the residual without rr the
+        // weights; unused values, but guarded loads make the compiler wait)
 #pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-        const int i = (j * kThreads + (int)threadIdx.x) * VEC;
-        if (i < dim) {
-            // the weights load with the row (not after the reduction): one
-            // memory round trip per launch instead of two
-            if (VEC > 1) load_vec(w + i, wv[j]);
-            else wv[j][0] = load1(w + i);
-            if (VEC > 1) {
-                if constexpr (PART) {
-                    static_assert(VEC % 4 == 0, "f32x4 sums");
-                    const size_t plane = (size_t)gridDim.x * dim;
-                    const f32x4 *pp = reinterpret_cast<const f32x4 *>(partial + (size_t)r_in * dim + i);
-                    f32x4 a[VEC / 4];
+        for (int j = 0; j < MAXV; ++j) {
+            const int i0 = (j * kThreads + (int)threadIdx.x) * VEC, i = i0 < dim ? i0 : 0;
+            const f32x4 *pp = reinterpret_cast<const f32x4 *>(partial + (size_t)r_in * dim + i);
 #pragma unroll
-                    for (int q = 0; q < VEC / 4; ++q) a[q] = pp[q];
-                    for (int r = 1; r < splits; ++r)
+            for (int r = 0; r < FL; ++r)
 #pragma unroll
-                        for (int q = 0; q < VEC / 4; ++q) a[q] += pp[r * plane / 4 + q];
+                for (int q = 0; q < N4; ++q) t[j][r][q] = pp[fold_offset(r, splits, plane4) + q];
+            load_vec((rr ? rr : w) + i, a[j]);
+            load_vec(w + i, wv[j]);
+        }
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) v[j][e] = stored(a[e / 4][e % 4], (const T *)nullptr);
-                } else {
-                    load_vec(xr + i, v[j]);
-                }
+        for (int j = 0; j < MAXV; ++j) {
+            const int i = (j * kThreads + (int)threadIdx.x) * VEC;
+            if (i < dim) {
+                const f32x4 *pp = reinterpret_cast<const f32x4 *>(partial + (size_t)r_in * dim + i);
+                f32x4 acc[N4];
+#pragma unroll
+                for (int q = 0; q < N4; ++q) acc[q] = t[j][0][q];
+#pragma unroll
+                for (int r = 1; r < FL; ++r)
+#pragma unroll
+                    for (int q = 0; q < N4; ++q) acc[q] = r < splits ? acc[q] + t[j][r][q] : acc[q];
+                for (int r = FL; r < splits; ++r)  // range order, as the reduce kernel adds them
+#pragma unroll
+                    for (int q = 0; q < N4; ++q) acc[q] += pp[(size_t)r * plane4 + q];
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) v[j][e] = stored(acc[e / 4][e % 4], (const T *)nullptr);
                 if (rr) {
-                    float a[VEC];
-                    load_vec(rr + i, a);
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) v[j][e] = stored(v[j][e] + a[e], (const T *)nullptr);
+                    for (int e = 0; e < VEC; ++e) v[j][e] = stored(v[j][e] + a[j][e], (const T *)nullptr);
                     store_vec(res_out + (size_t)blockIdx.x * dim + i, v[j]);
                 }
-            } else {
-                v[j][0] = load1(xr + i);
-                if (rr) {
-                    v[j][0] = stored(v[j][0] + load1(rr + i), (const T *)nullptr);
-                    store1(res_out + (size_t)blockIdx.x * dim + i, v[j][0]);
-                }
-            }
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) ss += v[j][e] * v[j][e];
+                for (int e = 0; e < VEC; ++e) ss += v[j][e] * v[j][e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < MAXV; ++j) {
+            const int i = (j * kThreads + (int)threadIdx.x) * VEC;
+            if (i < dim) {
+                // the weights load with the row (not after the reduction): one
+                // memory round trip per launch instead of two
+                if (VEC > 1) load_vec(w + i, wv[j]);
+                else wv[j][0] = load1(w + i);
+                if (VEC > 1) {
+                    load_vec(xr + i, v[j]);
+                    if (rr) {
+                        float a[VEC];
+                        load_vec(rr + i, a);
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e) v[j][e] = stored(v[j][e] + a[e], (const T *)nullptr);
+                        store_vec(res_out + (size_t)blockIdx.x * dim + i, v[j]);
+                    }
+                } else {
+                    v[j][0] = load1(xr + i);
+                    if (rr) {
+                        v[j][0] = stored(v[j][0] + load1(rr + i), (const T *)nullptr);
+                        store1(res_out + (size_t)blockIdx.x * dim + i, v[j][0]);
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) ss += v[j][e] * v[j][e];
+            }
         }
     }
     const float inv = rsqrtf(block_sum(ss, red) / (float)dim + eps);

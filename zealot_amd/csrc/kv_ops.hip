@@ -80,17 +80,15 @@ append_split_sums_kernel(const float *__restrict__ partial, int splits, uint32_t
     const uint32_t t = idx / cols8, c = 8 * (idx % cols8);
     const size_t plane = (size_t)rows * cols8 * 8;
     const f32x4 *p = reinterpret_cast<const f32x4 *>(partial + (size_t)t * cols8 * 8 + c);
-    f32x4 a = p[0], b = p[1];
-    for (int r = 1; r < splits; ++r) {
-        a += p[r * plane / 4];
-        b += p[r * plane / 4 + 1];
-    }
+    const int64_t slot = c < qcols ? 0 : slots[t];  // loaded beside the sums
+    f32x4 ab[2];
+    sum_ranges(p, plane / 4, splits, ab);
+    const f32x4 a = ab[0], b = ab[1];
     const uint4 v = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])};
     if (c < qcols) {
         st16(q_out + (size_t)t * ldq + c, v);
         return;
     }
-    const int64_t slot = slots[t];
     if (slot < 0 || slot >= num_slots) return;
     const uint32_t kc = c - qcols, kd = hkv * head_dim, kvc = kc < kd ? kc : kc - kd;
     const uint32_t h = kvc / head_dim, d = kvc % head_dim;

@@ -42,6 +42,7 @@ namespace {
 using zk::bf16x8;
 using zk::f32x4;
 using zk::u32x4;
+using zk::sum_ranges;
 
 constexpr int kThreads = 256;  // four waves
 constexpr int kChunk = 128;    // k per chunk: four MFMA k-steps, 256 bytes of a row
@@ -228,9 +229,9 @@ __global__ void __launch_bounds__(kThreads) skinny_reduce_kernel(const float *__
     const size_t q = (size_t)blockIdx.x * kThreads + threadIdx.x;
     if (q >= quads) return;
     const f32x4 *p = reinterpret_cast<const f32x4 *>(partial) + q;
-    f32x4 v = p[0];
-    for (int s = 1; s < splits; ++s) v += p[(size_t)s * quads];
-    store4(y, F32, 4 * q, v);
+    f32x4 v[1];
+    sum_ranges(p, quads, splits, v);
+    store4(y, F32, 4 * q, v[0]);
 }
 
 // grid: (weight tiles x splits, 64-column blocks of y)

@@ -201,6 +201,37 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
+// Sum of N consecutive f32x4 over the k ranges of a split-k product:
+// acc[q] = p[q] + p[plane + q] + ... in range order (the order every reduce
+// of these sums uses, so results do not depend on which kernel adds them).
+// The first kFoldLoads ranges are loaded before any addition, so a fold of up
+// to that many ranges costs one memory round trip, not one per range.  The
+// loads are unconditional (a range past `splits` re-reads range 0, a cache
+// hit whose value is not used): guarded loads make the compiler wait for each
+// group before the next.  The sum selects instead of adding zero, which keeps
+// a -0 sum's sign.
+constexpr int kFoldLoads = 8;
+__device__ __forceinline__ size_t fold_offset(int r, int splits, size_t plane) {
+    return r < splits ? (size_t)r * plane : 0;
+}
+template <int N>
+__device__ __forceinline__ void sum_ranges(const f32x4 *p, size_t plane, int splits, f32x4 (&acc)[N]) {
+    f32x4 t[kFoldLoads][N];
+#pragma unroll
+    for (int r = 0; r < kFoldLoads; ++r)
+#pragma unroll
+        for (int q = 0; q < N; ++q) t[r][q] = p[fold_offset(r, splits, plane) + q];
+#pragma unroll
+    for (int q = 0; q < N; ++q) acc[q] = t[0][q];
+#pragma unroll
+    for (int r = 1; r < kFoldLoads; ++r)
+#pragma unroll
+        for (int q = 0; q < N; ++q) acc[q] = r < splits ? acc[q] + t[r][q] : acc[q];
+    for (int r = kFoldLoads; r < splits; ++r)
+#pragma unroll
+        for (int q = 0; q < N; ++q) acc[q] += p[(size_t)r * plane + q];
+}
+
 // f32 -> OCP e4m3 (e4m3fn), round to nearest even, saturating at +-448, NaN
 // keeps its sign as S.1111.111.  The gfx950 converter rounds in-range values
 // to nearest even; clamping first makes it saturate, and NaN is patched.
