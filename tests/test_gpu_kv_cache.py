@@ -410,7 +410,8 @@ def test_cow_out_of_blocks_keeps_typed_error():
     assert bm.free_blocks == NB
 
 
-@pytest.mark.parametrize("dtype,H,Hkv,D", [("bf16", 32, 8, 128), ("bf16", 8, 8, 64), ("f32", 4, 4, 32)])
+@pytest.mark.parametrize("dtype,H,Hkv,D", [("bf16", 32, 8, 128), ("bf16", 8, 8, 64), ("f32", 4, 4, 32),
+                                           ("fp8", 32, 8, 128)])
 def test_decode_append_is_append_then_decode(dtype, H, Hkv, D):
     """zk_cache_decode_append (one launch on bf16 MFMA shapes: the decode
     stores each sequence's new K / V row and attends it) against
@@ -418,12 +419,13 @@ def test_decode_append_is_append_then_decode(dtype, H, Hkv, D):
     outputs and every pool byte equal after each of 40 steps over 2 layers,
     with forks whose first write copies a shared tail block and sequences
     crossing block boundaries (src/kv_cache.rs:281-356,
-    src/attention/mod.rs:64-98); the f32 cache takes the two-call path."""
+    src/attention/mod.rs:64-98); the f32 and fp8 caches take the two-call
+    path (bf16 rows quantised by the append)."""
     import zealot_amd as ze
     from zealot_amd import KVCache
     from zealot_amd.kv_cache import SeqBatch
-    cdt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype]
-    odt = oracle.BF16 if dtype == "bf16" else oracle.F32
+    cdt = {"bf16": torch.bfloat16, "f32": torch.float32, "fp8": torch.float8_e4m3fn}[dtype]
+    odt = oracle.F32 if dtype == "f32" else oracle.BF16
     L, BS, NB, STEPS = 2, 16, 600, 40
     rng = np.random.default_rng(46 + D)
     base = {f"s{i}": int(rng.integers(1, 700)) for i in range(12)}
@@ -438,6 +440,8 @@ def test_decode_append_is_append_then_decode(dtype, H, Hkv, D):
             cache.register_seq(sid, 64)
             for _ in range((t + STEPS + BS - 1) // BS):
                 cache.alloc_block(sid, bm)
+            if dtype == "fp8":  # N(0,1) rows: |x| < 448 * 0.05 at these sizes
+                cache.set_fp8_scales(sid, np.full(L * Hkv, 0.05, np.float32), np.full(L * Hkv, 0.05, np.float32))
             for layer in range(L):
                 cache.store_kv(layer, sid, to_dev(init[sid][2 * layer]), to_dev(init[sid][2 * layer + 1]), 0, t)
         for k in kids:
@@ -465,8 +469,14 @@ def test_decode_append_is_append_then_decode(dtype, H, Hkv, D):
         for sid in ids:
             pos[sid] += 1
             assert ca.seq_state(sid).cached_tokens == cb.seq_state(sid).cached_tokens == pos[sid]
-    # and the last step against the oracle on the pages as they are
     (ca, _), _ = caches
+    par = ca.seq_state("par").block_ids
+    for k in kids:  # the forks copied the partial tail, the full blocks before it stay shared
+        ids_k = ca.seq_state(k).block_ids
+        assert ids_k[:20] == par[:20] and ids_k[20] != par[20]
+    if dtype == "fp8":  # fp8 decode parity with the oracle: tests/test_gpu_decode.py, test_gpu_full_size.py
+        return
+    # and the last step against the oracle on the pages as they are
     last = L - 1
     kp, vp = to_host(ca.k_pool(last)), to_host(ca.v_pool(last))
     bt = -np.ones((len(ids), 64), np.int32)
@@ -476,10 +486,6 @@ def test_decode_append_is_append_then_decode(dtype, H, Hkv, D):
     ref = oracle.paged_decode(as_f32(to_host(q), odt), kp, vp, odt, bt, [pos[s] for s in ids], Hkv, D, BS,
                               np.float32(1 / math.sqrt(D)), threads=8)
     assert max_abs_err(as_f32(to_host(got), odt), ref) <= (2e-2 if dtype == "bf16" else 1e-5)
-    par = ca.seq_state("par").block_ids
-    for k in kids:  # the forks copied the partial tail, the full blocks before it stay shared
-        ids_k = ca.seq_state(k).block_ids
-        assert ids_k[:20] == par[:20] and ids_k[20] != par[20]
 
 
 def test_device_table_rows_follow_queued_allocations():
