@@ -135,6 +135,7 @@ struct zk_kv_cache {
     int dtype = ZK_F32;
     size_t max_seqs = 0, max_blocks_per_seq = 0;
     int device = 0;
+    int cus = 256;  // compute units of the device
     hipStream_t stream = nullptr;
     char *slab = nullptr;
     size_t pool_bytes = 0;
@@ -620,6 +621,8 @@ int zk_cache_create(size_t num_blocks, size_t block_size, size_t num_layers, siz
     c->max_blocks_per_seq = max_blocks_per_seq;
     c->stream = (hipStream_t)stream;
     if (hipGetDevice(&c->device) != hipSuccess) c->device = 0;
+    if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device) != hipSuccess || c->cus <= 0)
+        c->cus = 256;
     c->pool_bytes = ((num_blocks * c->block_bytes()) + 255) & ~(size_t)255;
     size_t slab_bytes = 2 * num_layers * c->pool_bytes;
     hipError_t e = hipMalloc((void **)&c->slab, slab_bytes);
@@ -1143,7 +1146,7 @@ namespace {
 int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState *> &seqs,
                  const std::vector<int32_t> *lens_in, const std::vector<int32_t> *q_rows, const void *q,
                  zk_dtype q_dtype, int64_t q_stride, void *out, int num_heads, float scale, zk_gqa_mapping mapping,
-                 bool share, const zk::AppendRows *append = nullptr) {
+                 bool share, const zk::AppendRows *append = nullptr, int max_waves = 0) {
     const int n = (int)seqs.size();
     if (n <= 0) return ZK_OK;
     const size_t H = c->num_kv_heads;
@@ -1221,9 +1224,9 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
     // carrying the block ids of its first pages, in the workspace) depends on
     // the shapes, the lengths, the prefix groups and the tables, not on the
     // layer's pools, q or scales: the layers of one step share it.
-    const uintptr_t hdr[] = {(uintptr_t)n,      (uintptr_t)num_heads,     stride,
-                             (uintptr_t)nsg,    (uintptr_t)sp.total_pages, (uintptr_t)c->d_ws.p,
-                             (uintptr_t)c->d_ws.cap, (uintptr_t)c->tbl_version};
+    const uintptr_t hdr[] = {(uintptr_t)n,          (uintptr_t)num_heads,     stride,
+                             (uintptr_t)nsg,        (uintptr_t)sp.total_pages, (uintptr_t)c->d_ws.p,
+                             (uintptr_t)c->d_ws.cap, (uintptr_t)c->tbl_version, (uintptr_t)max_waves};
     std::vector<char> sig((const char *)hdr, (const char *)hdr + sizeof(hdr));
     sig.insert(sig.end(), host.data(), host.data() + len_bytes);
     sig.insert(sig.end(), host.data() + len_bytes + sc_bytes, host.data() + len_bytes + sc_bytes + share_bytes);
@@ -1234,7 +1237,7 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
                               (int)c->head_dim, (int)c->block_size, (int)stride, (int64_t)c->num_blocks, scale,
                               mapping, dks, dvs, c->d_ws.p, c->d_ws.cap, c->stream, nsg ? &pg : nullptr, drows,
                               q_stride, /*trusted_tables=*/true,  // built from the sequences' handles
-                              reuse, append, &c->dec_head_set);
+                              reuse, append, &c->dec_head_set, max_waves);
     if (rc == ZK_OK) c->plan_sig = std::move(sig);
     return rc;
 }
@@ -1262,7 +1265,7 @@ int find_seqs(zk_kv_cache *c, const char *const *ids, int n, std::vector<const S
 int prefill_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState *> &seqs,
                   const std::vector<int32_t> &len, const std::vector<int64_t> &off, int64_t total_rows, const void *q,
                   zk_dtype q_dtype, int64_t q_stride, void *out, int num_heads, float scale, zk_gqa_mapping mapping,
-                  hipStream_t launch) {
+                  hipStream_t launch, int max_groups = 0) {
     const int n = (int)seqs.size();
     if (n <= 0) return ZK_OK;
     const size_t H = c->num_kv_heads;
@@ -1307,7 +1310,7 @@ int prefill_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState
                                   (const int32_t *)(d + tbl_bytes + off_bytes + i32_bytes), n, total_rows, num_heads,
                                   (int)H, (int)c->head_dim, (int)c->block_size, (int)stride,
                                   (int64_t)c->num_blocks, scale, 1, mapping, dks, dvs, c->d_pws.p, c->d_pws.cap,
-                                  launch, q_stride);
+                                  launch, q_stride, max_groups);
 }
 
 int ensure_side_stream(zk_kv_cache *c) {
@@ -1405,17 +1408,24 @@ int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *id
                               pre_pages <= (size_t)zk::kPrefillMaxPages;
     if (mfma_prefill) {
         // chunks first, on the side stream when decodes share the step, so
-        // the two kernels overlap; the cache stream waits for both at the end
+        // the two kernels overlap; the cache stream waits for both at the end.
+        // Neither kernel fits beside the other on one SIMD (their registers
+        // add up to more than a SIMD holds), so each gets half of every CU:
+        // one two-wave prefill workgroup and two decode waves (the HBM-bound
+        // decode streams as fast on two waves a CU as on four)
         hipStream_t ps = c->stream;
+        int pre_groups = 0, dec_waves = 0;
         if (!dec.empty()) {
             if (int rc = ensure_side_stream(c)) return rc;
             ps = c->side;
+            pre_groups = c->cus;
+            dec_waves = 2 * c->cus;
         }
         int rc = prefill_batch(c, layer, pre, pre_len, pre_off, row, q, q_dtype, q_token_stride, out, num_heads,
-                               scale, mapping, ps);
+                               scale, mapping, ps, pre_groups);
         if (!rc)
             rc = decode_batch(c, layer, dec, nullptr, identity ? nullptr : &dec_rows, q, q_dtype, q_token_stride, out,
-                              num_heads, scale, mapping, true);
+                              num_heads, scale, mapping, true, nullptr, dec_waves);
         if (ps != c->stream) {
             hipError_t e = hipEventRecord(c->join_ev, ps);
             if (e == hipSuccess) e = hipStreamWaitEvent(c->stream, c->join_ev, 0);

@@ -1163,9 +1163,8 @@ int items_per_wave_config() {
 
 int persistent_grid();
 
-int mfma_part_pages(int num_seqs, int num_kv_heads, int max_blocks) {
+int mfma_part_pages(int num_seqs, int num_kv_heads, int max_blocks, long waves) {
     if (int e = part_pages_env()) return e;
-    const long waves = persistent_grid();
     const long pairs = (items_per_wave_config() * waves + num_kv_heads - 1) / num_kv_heads;
     const long per_seq = (pairs + num_seqs - 1) / num_seqs;
     long pp = (max_blocks + per_seq - 1) / per_seq;
@@ -1214,14 +1213,14 @@ int check_launch(const char *what) {
 // subgroups' pages, so half the waves stream the shared pages (two query-row
 // tiles each) while the rest run the sequences' own items; measured best on
 // forked-prefix batches.  ZEALOT_DECODE_SHARED_PART_PAGES (16..1024) overrides.
-int shared_part_pages_for(long total_shared_pages, int num_kv_heads) {
+int shared_part_pages_for(long total_shared_pages, int num_kv_heads, long waves) {
     static const int env = [] {
         const char *e = std::getenv("ZEALOT_DECODE_SHARED_PART_PAGES");
         const int v = e ? std::atoi(e) : 0;
         return v <= 0 ? 0 : (v < 16 ? 16 : (v > kMaxItemPages ? kMaxItemPages : v));
     }();
     if (env) return env;
-    const long half = persistent_grid() / 2;
+    const long half = waves / 2;
     long pp = (total_shared_pages * num_kv_heads + half - 1) / half;
     pp = (pp + 15) / 16 * 16;
     return (int)(pp < 16 ? 16 : (pp > kMaxItemPages ? kMaxItemPages : pp));
@@ -1276,19 +1275,23 @@ int check_decode_args(zk_dtype q_dtype, zk_dtype kv_dtype, int num_seqs, int num
 // needs (arguments already checked).
 struct DecodeShape {
     bool use_mfma, shared;
-    int part_pages, shared_pages, max_parts;
+    int part_pages, shared_pages, max_parts, waves;
     WsLayout w;
 };
+// max_waves > 0 caps the MFMA path's persistent grid (partitions are sized
+// for the waves that run them).
 DecodeShape decode_shape(zk_dtype kv_dtype, int num_seqs, int num_heads, int num_kv_heads, int head_dim,
-                         int block_size, int max_blocks_per_seq, const PrefixGroups *pg) {
+                         int block_size, int max_blocks_per_seq, const PrefixGroups *pg, int max_waves = 0) {
     DecodeShape d;
     const int G = num_heads / num_kv_heads;
     d.use_mfma = mfma_supported(kv_dtype, head_dim, block_size, G);
-    d.part_pages = d.use_mfma ? mfma_part_pages(num_seqs, num_kv_heads, max_blocks_per_seq)
+    d.waves = persistent_grid();
+    if (max_waves > 0 && max_waves < d.waves) d.waves = max_waves;
+    d.part_pages = d.use_mfma ? mfma_part_pages(num_seqs, num_kv_heads, max_blocks_per_seq, d.waves)
                               : part_pages_for(ZK_F32, head_dim, block_size);
     d.shared = pg && pg->num_sg > 0 &&
                paged_decode_shares_prefixes(kv_dtype, head_dim, block_size, num_heads, num_kv_heads);
-    d.shared_pages = d.shared ? shared_part_pages_for(pg->total_shared_pages, num_kv_heads) : 0;
+    d.shared_pages = d.shared ? shared_part_pages_for(pg->total_shared_pages, num_kv_heads, d.waves) : 0;
     // slot stride: a sequence's shared and private partitions together
     d.max_parts = d.shared ? max_parts_for(max_blocks_per_seq, min_part_pages(head_dim, block_size)) + 1
                            : max_parts_for(max_blocks_per_seq, d.part_pages);
@@ -1304,7 +1307,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
                      float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                      void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
                      const int32_t *q_rows, int64_t q_stride, bool trusted_tables, bool reuse_plan,
-                     const AppendRows *append, int *head_set) {
+                     const AppendRows *append, int *head_set, int max_waves) {
     if (int rc = check_decode_args(q_dtype, kv_dtype, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
                                    max_blocks_per_seq, num_blocks, mapping))
         return rc;
@@ -1319,8 +1322,8 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     if (pg && pg->num_sg > 0 && (!pg->seq_pb || !pg->sg_members || !pg->sg_pages) &&
         paged_decode_shares_prefixes(kv_dtype, head_dim, block_size, num_heads, num_kv_heads))
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: paged decode: NULL prefix-group array");
-    const DecodeShape ds =
-        decode_shape(kv_dtype, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, pg);
+    const DecodeShape ds = decode_shape(kv_dtype, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
+                                        max_blocks_per_seq, pg, max_waves);
     const bool use_mfma = ds.use_mfma, shared = ds.shared;
     if (append && (!use_mfma || kv_dtype != ZK_BF16 || !trusted_tables || !append->k || !append->v ||
                    append->row_bytes < (int64_t)num_kv_heads * head_dim * 2 || (append->row_bytes & 15) ||
@@ -1351,7 +1354,7 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     p.eff_len = (int32_t *)(ws + w.eff);
     p.items = (int4 *)(ws + w.map);
     p.work = (int32_t *)(ws + w.work);
-    p.num_waves = use_mfma ? persistent_grid() : 0;
+    p.num_waves = use_mfma ? ds.waves : 0;
     p.queues = shared ? kQueues : 1;
     p.ml = (float2 *)(ws + w.ml);
     p.po = (float *)(ws + w.po);

@@ -699,7 +699,7 @@ int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void
                  const int32_t *q_len, const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                  float scale, int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                 void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride);
+                 void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride, int max_groups);
 
 }  // namespace
 
@@ -709,13 +709,13 @@ int zk::paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, 
                            int num_heads, int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq,
                            int64_t num_blocks, float scale, int causal, zk_gqa_mapping mapping,
                            const float *k_scales, const float *v_scales, void *workspace, size_t workspace_bytes,
-                           void *stream, int64_t q_stride) {
+                           void *stream, int64_t q_stride, int max_groups) {
     if (!q_off || !q_len)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: paged prefill: NULL row offsets");
     return prefill_impl(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, nullptr, q_off, q_len, start_pos,
                         num_seqs, total_q, num_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq,
                         num_blocks, scale, causal, mapping, k_scales, v_scales, workspace, workspace_bytes, stream,
-                        q_stride);
+                        q_stride, max_groups);
 }
 
 extern "C" {
@@ -738,7 +738,7 @@ int zk_paged_prefill(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     return prefill_impl(q, q_dtype, k_pool, v_pool, kv_dtype, out, block_tables, cu_seqlens_q, nullptr, nullptr,
                         start_pos, num_seqs, total_q, num_heads, num_kv_heads, head_dim, block_size,
                         max_blocks_per_seq, num_blocks, scale, causal, mapping, k_scales, v_scales, workspace,
-                        workspace_bytes, stream, 0);
+                        workspace_bytes, stream, 0, 0);
 }
 
 }  // extern "C"
@@ -750,7 +750,7 @@ int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void
                  const int32_t *q_len, const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
                  float scale, int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                 void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride) {
+                 void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride, int max_groups) {
     if (q_dtype != ZK_F32 && q_dtype != ZK_BF16)
         return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: zk_paged_prefill: q dtype must be f32 or bf16");
     if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
@@ -805,7 +805,9 @@ int prefill_impl(const void *q, zk_dtype q_dtype, const void *k_pool, const void
     p.block_size = block_size;
     p.max_blocks = max_blocks_per_seq;
     p.tq = kRows / G;
+    // a whole number of workgroups per XCD queue
     p.num_groups = persistent_groups();
+    if (max_groups >= kXcds) p.num_groups = std::min(p.num_groups, max_groups / kXcds * kXcds);
     p.max_items = max_items_for(num_seqs, total_q, num_heads, num_kv_heads);
     p.num_blocks = num_blocks;
     p.scale_log2 = scale * kLog2e;

@@ -105,7 +105,9 @@ struct PrefixGroups {
 // attends it (that page must not be a shared-prefix page).  head_set: the
 // caller's record of which queue-head set the next launch on this workspace
 // uses when it reuses the plan (0 after a planning launch's successor
-// flips it); null: every launch plans.
+// flips it); null: every launch plans.  max_waves > 0 caps the persistent
+// grid of the MFMA path (0: one wave per SIMD); a plan is reused only by
+// launches with the same cap.
 struct AppendRows {
     const void *k, *v;
     int64_t row_bytes;
@@ -116,18 +118,21 @@ int paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const void
                  float scale, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
                  void *workspace, size_t workspace_bytes, void *stream, const PrefixGroups *pg,
                  const int32_t *q_rows, int64_t q_stride = 0, bool trusted_tables = false, bool reuse_plan = false,
-                 const AppendRows *append = nullptr, int *head_set = nullptr);
+                 const AppendRows *append = nullptr, int *head_set = nullptr, int max_waves = 0);
 // Whether paged_decode can take a fused append for this shape.
 bool paged_decode_fuses_append(int kv_dtype, int head_dim, int block_size, int num_heads, int num_kv_heads);
 // zk_paged_prefill with the chunk rows of sequence n given as a device
 // offset and length (q_off[n], q_len[n]) instead of cu_seqlens_q; total_q is
 // an upper bound of the rows; q rows are q_stride elements apart (0 = H * D).
+// max_groups > 0 caps the persistent grid (two-wave workgroups; 0: two per
+// CU, every SIMD), leaving SIMDs to a kernel that runs beside it.
 int paged_prefill_rows(const void *q, zk_dtype q_dtype, const void *k_pool, const void *v_pool, zk_dtype kv_dtype,
                        void *out, const int32_t *block_tables, const int64_t *q_off, const int32_t *q_len,
                        const int32_t *start_pos, int num_seqs, int64_t total_q, int num_heads, int num_kv_heads,
                        int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks, float scale,
                        int causal, zk_gqa_mapping mapping, const float *k_scales, const float *v_scales,
-                       void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride = 0);
+                       void *workspace, size_t workspace_bytes, void *stream, int64_t q_stride = 0,
+                       int max_groups = 0);
 // Weight-streaming product y[m, n] = x[m, k] . w[n, k]^T for bf16 x / w and
 // m <= 64 (any m with tiled weights, in blocks of 64 columns), output f32 or
 // bf16: workgroups own tiles of tile_rows (64 or 128) weight rows and
