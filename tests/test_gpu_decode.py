@@ -252,3 +252,84 @@ def test_fp8_decode_dequantises_every_e4m3_code_exactly():
     nan = np.isnan(want)
     assert nan.sum() == 2 and np.all(np.isnan(got[nan]))
     assert np.array_equal(got[~nan], want[~nan])  # exact values (-0 comes back as +0 from the accumulators)
+
+
+@pytest.mark.parametrize("H,Hkv,D,dt", [(32, 8, 128, torch.bfloat16), (16, 16, 64, torch.bfloat16),
+                                        (4, 4, 32, torch.float32)])
+def test_decode_closed_forms(H, Hkv, D, dt):
+    """Properties the softmax fixes, checked on the kernel itself rather than
+    through the oracle (attention/mod.rs:64-98): a one-token context returns
+    that token's V row exactly; keys all equal give the mean of V; one key far
+    above the others gives its V row; adding the same vector to every key
+    (exact in bf16) leaves the output unchanged.  Lengths cross several
+    split-K partitions on the MFMA path (bf16) and run the generic path (f32)."""
+    from zealot_amd import ops
+    g = torch.Generator(device="cuda").manual_seed(H * 1000 + D)
+    BS, N = 16, 6
+    lens = [1, 1, 300, 2000, 4096 + 7, 700]
+    pages = [(L + BS - 1) // BS for L in lens]
+    NB = sum(pages) + 8
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(5)).to(torch.int32)
+    bt = torch.full((N, max(pages)), -1, dtype=torch.int32)
+    o = 0
+    for i, p in enumerate(pages):
+        bt[i, :p] = perm[o:o + p]
+        o += p
+    btd = bt.cuda()
+    ld = torch.tensor(lens, dtype=torch.int32, device="cuda")
+
+    def quant(x):  # multiples of 1/16 in [-4, 4]: exact in bf16, and so is x + 8
+        return (torch.round(x * 16).clamp(-64, 64) / 16).to(dt)
+
+    q = quant(torch.randn((N, H, D), generator=g, device="cuda") * 0.5)
+    vp = quant(torch.randn((NB, Hkv, BS, D), generator=g, device="cuda"))
+    kp = quant(torch.randn((NB, Hkv, BS, D), generator=g, device="cuda") * 0.5)
+    G = H // Hkv
+    announce(f"decode closed forms H{H}/Hkv{Hkv}/D{D} {dt}")
+
+    def ctx_rows(pool, i):  # sequence i's rows [len, Hkv, D] in token order
+        blocks = bt[i, :pages[i]].long().cuda()
+        return pool[blocks].permute(0, 2, 1, 3).reshape(-1, Hkv, D)[:lens[i]].float()
+
+    out = ops.paged_decode(q, kp, vp, btd, ld)
+    torch.cuda.synchronize()
+    # one-token contexts: exactly that token's V row
+    for i in (0, 1):
+        v0 = ctx_rows(vp, i)[0]
+        for h in range(H):
+            assert torch.equal(out[i, h].float(), v0[h // G]), (i, h)
+    # keys all equal (every row of every page the same vector): the mean of V
+    kc = kp.clone()
+    kc[:] = kp[0, 0, 0]
+    outc = ops.paged_decode(q, kc, vp, btd, ld)
+    torch.cuda.synchronize()
+    tol = 2e-2 if dt == torch.bfloat16 else 1e-5
+    for i in range(N):
+        mean = ctx_rows(vp, i).mean(0)
+        for h in range(H):
+            assert (outc[i, h].float() - mean[h // G]).abs().max() <= tol * max(1.0, mean.abs().max()), (i, h)
+    # one dominant key per (sequence, kv-head): 2^6 x q's direction at one position
+    kd = kp.clone()
+    pos = [0, 0, 123, 1999, 4100, 350]
+    for i in range(N):
+        blk, t = int(bt[i, pos[i] // BS]), pos[i] % BS
+        for kvh in range(Hkv):
+            qs = q[i, kvh * G:(kvh + 1) * G].float().sum(0)  # grouped heads of this kv-head
+            kd[blk, kvh, t] = (torch.sign(qs) * 4).to(dt)
+    sc = 64.0 / math.sqrt(D)
+    outd = ops.paged_decode(q, kd, vp, btd, ld, scale=sc)
+    torch.cuda.synchronize()
+    checked = 0
+    for i in range(2, N):
+        vrow, krows = ctx_rows(vp, i)[pos[i]], ctx_rows(kd, i)
+        for h in range(H):
+            s_ = krows[:, h // G] @ q[i, h].float() * sc
+            others = torch.cat([s_[:pos[i]], s_[pos[i] + 1:]])
+            if s_[pos[i]] - others.max() >= 40.0:  # every other weight below e^-40
+                checked += 1
+                assert (outd[i, h].float() - vrow[h // G]).abs().max() <= 2 * tol * max(1.0, vrow.abs().max()), (i, h)
+    assert checked >= H  # the construction makes most heads dominant
+    # the same vector added to every key: scores shift by q.u per head, softmax unchanged
+    outs = ops.paged_decode(q, (kp.float() + 8.0).to(dt), vp, btd, ld)
+    torch.cuda.synchronize()
+    assert (outs.float() - out.float()).abs().max() <= 2 * tol * max(1.0, out.float().abs().max())

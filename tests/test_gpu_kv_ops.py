@@ -260,3 +260,33 @@ def test_stream_yardsticks(nbytes):
     _lib.check(lib.zk_stream_read(ctypes.c_void_p(zeros.data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()), None))
     torch.cuda.synchronize()
     assert int(sink.abs().sum()) == 0
+
+
+def test_gather_is_invariant_to_moving_blocks():
+    """Moving every block to another physical id (pool rows permuted, tables
+    renumbered the same way) leaves the gathered contexts bit for bit the
+    same: the gather depends on the tables' contents, not on where blocks
+    sit (paged_attention.cu:63-83)."""
+    from zealot_amd import ops
+    rng = np.random.default_rng(71)
+    H, D, BS = 8, 128, 16
+    lens = np.array([1, 16, 17, 300, 999])
+    bt, nb = paged_tables(rng, lens, BS)
+    kp = normal(rng, (nb, H, BS, D), oracle.BF16)
+    vp = normal(rng, (nb, H, BS, D), oracle.BF16)
+    move = rng.permutation(nb)  # block b now lives at move[b]
+    kp2, vp2 = np.empty_like(kp), np.empty_like(vp)
+    kp2[move], vp2[move] = kp, vp
+    bt2 = np.where(bt >= 0, move[np.maximum(bt, 0)], -1).astype(np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    T = int(lens.sum())
+    outs = []
+    announce("gather after moving every block")
+    for k_, v_, t_ in ((kp, vp, bt), (kp2, vp2, bt2)):
+        ko = torch.full((T, H, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+        vo = torch.full_like(ko, float("nan"))
+        ops.gather(to_dev(k_), to_dev(v_), to_dev(t_), to_dev(lens.astype(np.int32)), to_dev(offs), ko, vo)
+        torch.cuda.synchronize()
+        outs.append((to_host(ko), to_host(vo)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    assert not np.any(np.isnan(oracle.f32_from_bf16_bits(outs[0][0].ravel())))
