@@ -536,3 +536,46 @@ def test_device_table_rows_follow_queued_allocations():
     for sid in ("a", "c", "d"):
         cache.release_seq(sid)
     assert bm.free_blocks == NB
+
+
+def test_device_rows_take_the_last_queued_write():
+    """An entry queued twice before a flush (allocations, then a swap-out that
+    clears the row) ends with the later value on the device, every time: the
+    one-launch table update applies only the last write to each entry."""
+    import ctypes
+    import zealot_amd as ze
+    from zealot_amd import KVCache, _lib
+    L, H, D, BS, NB, MB = 2, 2, 32, 16, 256, 64
+    bm = ze.BlockManager(NB, BS)
+    cache = KVCache(NB, BS, L, H, D, dtype=torch.bfloat16, max_seqs=4, max_blocks_per_seq=MB)
+    cache.enable_swap(MB)
+    lib = _lib.lib()
+
+    def row(ptr):
+        dst = torch.empty(MB, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        _lib.check(lib.zk_stream_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(ptr), MB * 4, None))
+        torch.cuda.synchronize()
+        return dst.cpu().tolist()
+
+    announce("device rows: allocation then swap-out queued together")
+    cache.register_seq("s", MB)
+    for rep, (nw, extra) in enumerate(((4, 60), (1, 16), (2, 1), (3, 37))):
+        ptr = cache.block_table_ptr("s")
+        for _ in range(nw):
+            cache.alloc_block("s", bm)
+        x = torch.ones((nw * BS, H, D), dtype=torch.bfloat16, device="cuda")
+        cache.store_kv(0, "s", x, x, 0, nw * BS)   # written blocks (the write flushes the queue)
+        for _ in range(extra):
+            cache.alloc_block("s", bm)          # queued, not flushed
+        cache.swap_out(["s"])                   # queues -1 over every entry, the queued ones too
+        assert cache.is_swapped("s")
+        assert row(ptr) == [-1] * MB, rep
+        cache.swap_in(["s"], bm)                # fresh blocks for the written ones: the row follows them
+        want = cache.seq_state("s").block_ids
+        assert len(want) == nw and row(ptr) == want + [-1] * (MB - nw), rep
+        cache.release_seq("s")
+        cache.register_seq("s", MB)
+        assert row(cache.block_table_ptr("s")) == [-1] * MB, rep
+    cache.release_seq("s")
+    assert bm.free_blocks == NB

@@ -244,13 +244,25 @@ void queue_table_entry(zk_kv_cache *c, const SeqState &s, size_t idx, int32_t va
 // device as one upload and one launch.
 int flush_tables(zk_kv_cache *c) {
     if (c->tbl_updates.empty()) return ZK_OK;
-    const size_t n = c->tbl_updates.size();
+    // The scatter writes its entries in parallel, so an entry queued twice
+    // (an allocation, then a swap-out or a bind before any flush) would land
+    // in either order: keep only the last write to each entry.  The queue is
+    // in program order, and the stable sort keeps that order within an entry.
+    std::vector<int2> &q = c->tbl_updates;
+    std::stable_sort(q.begin(), q.end(), [](const int2 &a, const int2 &b) { return a.x < b.x; });
+    size_t m = 0;
+    for (size_t i = 0; i < q.size(); ++i)
+        if (i + 1 == q.size() || q[i + 1].x != q[i].x) q[m++] = q[i];
+    q.resize(m);
+    const size_t n = q.size();
     int rc = c->d_tblupd.ensure(n * sizeof(int2), "KVCache table update");
     if (!rc) rc = upload(c, c->d_tblupd.p, c->tbl_updates.data(), n * sizeof(int2));
     if (!rc)
         rc = zk::scatter_i32(c->tables, (int64_t)(c->max_seqs * c->max_blocks_per_seq), (const int2 *)c->d_tblupd.p,
                              (int)n, c->stream);
-    c->tbl_updates.clear();
+    // on failure the writes stay queued (they are idempotent): the next flush
+    // applies them, so the device rows never miss an entry the host recorded
+    if (!rc) c->tbl_updates.clear();
     return rc;
 }
 
