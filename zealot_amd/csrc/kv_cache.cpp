@@ -758,9 +758,12 @@ int zk_cache_fork_seq(zk_kv_cache *c, const char *parent, const char *child) {
     }
     SeqState s = *p;
     s.slot = c->free_slots.back();
-    ZK_HIP_CHECK(hipMemcpyAsync(c->table_row(s.slot), c->table_row(p->slot),
-                                c->max_blocks_per_seq * sizeof(int32_t), hipMemcpyDeviceToDevice, c->stream),
-                 "KVCache fork table copy");
+    const hipError_t e = hipMemcpyAsync(c->table_row(s.slot), c->table_row(p->slot),
+                                        c->max_blocks_per_seq * sizeof(int32_t), hipMemcpyDeviceToDevice, c->stream);
+    if (e != hipSuccess) {  // no child: give back the references taken for it
+        for (const auto &h : p->handles) (void)zk_bm_free(p->bm, h);
+        return set_error(ZK_ERR_HIP, std::string("Internal error: KVCache fork table copy: ") + hipGetErrorString(e));
+    }
     c->free_slots.pop_back();
     c->seqs.emplace(child, std::move(s));
     ++c->epoch;
