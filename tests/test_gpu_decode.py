@@ -98,6 +98,47 @@ def test_empty_context_sentinel_and_out_of_range_ids():
     assert max_abs_err(got, ref) <= 2e-2
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_random_batches_against_oracle(seed):
+    """Seeded random batches: head counts and grouping (G in 1, 2, 4, 8), head
+    size, KV dtype, mapping and batch size drawn per case; context lengths mix
+    page and partition edges (0, 1, 15-17, multiples of 16 +- 1) with random
+    ones; some tables carry spare columns, some a sentinel that ends the walk
+    early (src/kernels/paged_attention.cu:63-83: the context is then the
+    pages before it).  Every row against the fp32 oracle."""
+    from tests.gpu_util import normal, paged_tables
+    rng = np.random.default_rng(700 + seed)
+    G = int(rng.choice([1, 2, 4, 8]))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    H = G * Hkv
+    D = int(rng.choice([64, 128]))
+    dt = oracle.F32 if seed % 4 == 3 else oracle.BF16  # fp32 pools take the generic kernel
+    mapping = "grouped" if rng.random() < 0.7 else "modulo"
+    N = int(rng.integers(1, 49))
+    edges = [0, 1, 15, 16, 17, 255, 256, 257, 767, 768, 769]
+    lens = [int(rng.choice(edges)) if rng.random() < 0.4 else int(rng.integers(1, 3001)) for _ in range(N)]
+    bt, nb = paged_tables(rng, lens, 16)
+    if rng.random() < 0.5:  # spare columns past every sequence's pages
+        bt = np.concatenate([bt, -np.ones((N, int(rng.integers(1, 9))), np.int32)], axis=1)
+    ref_lens = list(lens)
+    for i in range(N):
+        pages = (lens[i] + 15) // 16
+        if pages > 1 and rng.random() < 0.2:
+            j = int(rng.integers(0, pages))
+            bt[i, j] = -1 if rng.random() < 0.5 else nb + int(rng.integers(0, 100))
+            ref_lens[i] = min(lens[i], 16 * j)
+    kp = normal(rng, (nb, Hkv, 16, D), dt)
+    vp = normal(rng, (nb, Hkv, 16, D), dt)
+    q = normal(rng, (N, H, D), dt)
+    announce(f"decode random case {seed}: H{H}/Hkv{Hkv}/D{D} dt={dt} {mapping} N={N} lens={lens}")
+    got = _run(q, kp, vp, bt, lens, dt, mapping)
+    ref = _oracle(q, kp, vp, bt, ref_lens, dt, dt, mapping)
+    for i in range(N):
+        if ref_lens[i] == 0:
+            assert np.all(got[i] == 0), i
+    assert max_abs_err(got, ref) <= TOL[dt]
+
+
 def test_decode_is_deterministic():
     lens = [700, 4000]
     q, kp, vp, bt, nb = decode_case(25, 32, 8, 128, lens, oracle.BF16)
