@@ -335,6 +335,88 @@ def test_forked_prefix_decode_shares_pages(G, D, qdt, mapping):
     assert bm.free_blocks == NB
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_fork_trees_decode_append_against_oracle(seed):
+    """Seeded random prefix trees through the KVCache: prefixes of random
+    length (some too short to share), forks of them and forks of forks
+    (taken after the parent wrote a few tokens of its own), decoded in a
+    random order by decode_append (the new token stored and attended in one
+    launch) over two layers for three steps, with blocks allocated as
+    sequences cross block edges and first writes into shared tails copied.
+    Every layer of every step against the fp32 oracle over each sequence's
+    pages as they are (src/kv_cache.rs:281-356, src/attention/mod.rs:64-98)."""
+    import zealot_amd as ze
+    from zealot_amd import KVCache
+    rng = np.random.default_rng(3000 + seed)
+    G = (1, 2, 4, 8)[seed % 4]
+    D = (128, 64)[seed // 4]
+    Hkv = int(rng.choice([1, 2]))
+    H, L, BS, MB, NB = G * Hkv, 2, 16, 64, 2048
+    bm = ze.BlockManager(NB, BS)
+    cache = KVCache(NB, BS, L, Hkv, D, dtype=torch.bfloat16, max_seqs=128, max_blocks_per_seq=MB)
+
+    def grow(sid, n):  # n more tokens at every layer, allocating as needed
+        st = cache.seq_state(sid)
+        start = st.cached_tokens
+        while len(cache.seq_state(sid).block_ids) * BS < start + n:
+            cache.alloc_block(sid, bm)
+        for layer in range(L):
+            k = normal(rng, (n, Hkv, D), oracle.BF16)
+            v = normal(rng, (n, Hkv, D), oracle.BF16)
+            cache.store_kv(layer, sid, to_dev(k), to_dev(v), start, n)
+
+    ids = []
+    can_share = False  # some prefix has 16 full pages and a fork: a subgroup must form
+    for pi in range(int(rng.integers(1, 5))):
+        pid = f"p{pi}"
+        cache.register_seq(pid, MB)
+        plen = int(rng.integers(1, 700)) if pi else int(rng.integers(16 * BS, 700))  # the first can share
+        grow(pid, plen)
+        ids.append(pid)
+        nf = int(rng.integers(0, 13)) if pi else int(rng.integers(1, 13))
+        can_share |= plen >= 16 * BS and nf > 0
+        for fi in range(nf):
+            cid = f"{pid}.{fi}"
+            cache.fork_seq(pid, cid)
+            ids.append(cid)
+            if rng.random() < 0.6:
+                grow(cid, int(rng.integers(1, 40)))
+            if rng.random() < 0.3:  # a fork of the fork, after its own tokens
+                gid = f"{cid}.g"
+                cache.fork_seq(cid, gid)
+                ids.append(gid)
+    order = [ids[i] for i in rng.permutation(len(ids))]
+    n = len(order)
+    announce(f"random fork tree {seed}: G={G} Hkv={Hkv} D={D} seqs={n}")
+    scale = np.float32(1 / math.sqrt(D))
+    for step in range(3):
+        for sid in order:
+            st = cache.seq_state(sid)
+            if st.cached_tokens == len(st.block_ids) * BS:
+                cache.alloc_block(sid, bm)
+        lens = [cache.seq_state(sid).cached_tokens + 1 for sid in order]
+        for layer in range(L):
+            k = normal(rng, (n, Hkv, D), oracle.BF16)
+            v = normal(rng, (n, Hkv, D), oracle.BF16)
+            q = normal(rng, (n, H, D), oracle.BF16)
+            out = to_host(cache.decode_append(layer, order, to_dev(k), to_dev(v), to_dev(q)))
+            kp, vp = to_host(cache.k_pool(layer)), to_host(cache.v_pool(layer))
+            bt = -np.ones((n, MB), np.int32)
+            for i, sid in enumerate(order):
+                b = cache.seq_state(sid).block_ids
+                bt[i, :len(b)] = b
+                pos = lens[i] - 1  # the appended row sits where its sequence's table says
+                blk, off = b[pos // BS], pos % BS
+                assert np.array_equal(kp[blk, :, off], k[i]) and np.array_equal(vp[blk, :, off], v[i]), (sid, layer)
+            ref = oracle.paged_decode(as_f32(q, oracle.BF16), kp, vp, oracle.BF16, bt, lens, Hkv, D, BS, scale)
+            assert max_abs_err(as_f32(out, oracle.BF16), ref) <= 2e-2, (step, layer)
+            sg, _ = cache.decode_sharing()
+            assert (sg > 0) == can_share, (sg, can_share)
+    for sid in order:
+        cache.release_seq(sid)
+    assert bm.free_blocks == NB
+
+
 def test_decode_plan_reuse_across_layers_and_batches():
     """The cache plans a decode once and reuses the plan while the shapes,
     lengths, prefix groups and tables stay the same (the layers of a step);
