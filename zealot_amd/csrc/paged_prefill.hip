@@ -481,7 +481,7 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         };
         // raw scores of the pair being turned into weights (the scale sits in
         // the exponent); -inf past a row's limit
-        float sc[T][8];
+        float scb[2][T][8];  // double buffer: pair j's scores and pair j + 1's
         // masks of pair pj's raw scores (pairs from open on): keys at or past a
         // row's limit get -inf
         auto mask_scores = [&](int pj, const f32x4 (&sacc)[2][T], float (&out)[T][8]) {
@@ -520,10 +520,10 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                     for (int kk = 0; kk < KK; ++kk)
                         sacc[h][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[h][kk], qf[t][kk], sacc[h][t], 0, 0, 0);
                 }
-            mask_scores(0, sacc, sc);
+            mask_scores(0, sacc, scb[0]);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                float cm = lane_max(sc[t]) * sl2;
+                float cm = lane_max(scb[0][t]) * sl2;
                 cm = fmaxf(cm, xor16(cm));
                 m[t] = fmaxf(cm, xor32(cm));
             }
@@ -533,8 +533,13 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         // issue between the score MFMAs of the next, the next pair's maxima
         // between this pair's PV MFMAs.  A rescale, when a maximum grew, is
         // applied after PV and before the next pair's weights.  IN: pairs j
-        // and j + 1 are open and pair j + 3 exists (no masks, no tests).
-        auto iter = [&]<bool IN>(int j) {
+        // and j + 1 are open and pair j + 3 exists (no masks, no tests).  P:
+        // the buffer of scb holding pair j's scores; IN iterations run in
+        // pairs that alternate it, so pair j + 1's scores are produced in the
+        // other buffer, not copied over the one being read.
+        auto iter = [&]<bool IN, int P>(int j) {
+            float (&sc)[T][8] = scb[P];
+            float (&sn)[T][8] = scb[IN ? 1 - P : P];
             const bool nxt = IN || j + 1 < npair;
             if (nxt) {
                 // this wave's part of pair j + 1 is in once only pair j + 2's
@@ -586,15 +591,15 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                     for (int t = 0; t < T; ++t)
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            sc[t][i] = sacc[0][t][i];
-                            sc[t][4 + i] = sacc[1][t][i];
+                            sn[t][i] = sacc[0][t][i];
+                            sn[t][4 + i] = sacc[1][t][i];
                         }
                 } else {
-                    mask_scores(j + 1, sacc, sc);
+                    mask_scores(j + 1, sacc, sn);
                 }
 #pragma unroll
                 for (int t = 0; t < T; ++t) {
-                    mx[t] = lane_max(sc[t]) * sl2;
+                    mx[t] = lane_max(sn[t]) * sl2;
                     grow |= mx[t] > m[t] + kRescaleSlack;
                 }
             }
@@ -616,8 +621,18 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         };
         const int in_end = min(open - 1, npair - (kStages - 1));  // iterations j < in_end are IN
         int j = 0;
-        for (; j < in_end; ++j) iter.template operator()<true>(j);
-        for (; j < npair; ++j) iter.template operator()<false>(j);
+        for (; j + 1 < in_end; j += 2) {  // two iterations a trip: the score buffers swap roles, no copies
+            iter.template operator()<true, 0>(j);
+            iter.template operator()<true, 1>(j + 1);
+        }
+        if (j < in_end) {
+            iter.template operator()<true, 0>(j++);
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) scb[0][t][i] = scb[1][t][i];
+        }
+        for (; j < npair; ++j) iter.template operator()<false, 0>(j);
 
         // rows of this lane: item row 64 w + 16 t + col, dims 16 dt + 4 grp + i
         // (bf16 pools, transposed V reads) or DT (4 grp + i) + dt (fp8 pools)
