@@ -357,16 +357,20 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         // page (odd page count) is loaded as a copy of the first, so both
         // waves issue the same loads per pair; its keys lie past every row's
         // limit and its V rows are zeroed below.
-        auto issue = [&](int pj) {
+        // this wave's page of pair pj (its K and V parts are one page's)
+        static_assert(PARTS == 2, "a wave loads the K and V of one page of each pair");
+        auto page_of = [&](int pj) { return trow[min(2 * pj + w, np - 1)]; };
+        // blk = page_of(pj), read one pair ahead: waiting for a scalar load
+        // also waits for every LDS read issued before it
+        auto issue = [&](int pj, int blk) {
             const int stg = pj & (kStages - 1);
 #pragma unroll
             for (int q = 0; q < PARTS; ++q) {
-                const int part = PARTS * w + q, h = part >> 1, kind = part & 1;  // page of the pair, K or V
-                const int blk = trow[min(2 * pj + h, np - 1)];
+                const int part = PARTS * w + q, kind = part & 1;  // K or V of this wave's page
                 const char *src = (kind ? vbase : kbase) + (size_t)blk * block_bytes;
 #pragma unroll
                 for (int j = 0; j < LPK; ++j)
-                    g2l16(src + (kind ? vg[j] : kg[j]), (lds_void *)(lds[stg][h][kind] + 1024 * j));
+                    g2l16(src + (kind ? vg[j] : kg[j]), (lds_void *)(lds[stg][w][kind] + 1024 * j));
             }
         };
         f32x4 o[DT][T];
@@ -413,7 +417,6 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                         w4 = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
                     }
                     kop[h][kk] = __builtin_bit_cast(bf16x8, w4);
-                    asm volatile("" : "+a"(kop[h][kk]));
                 }
             }
         };
@@ -476,8 +479,6 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                     }
                 }
             }
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) asm volatile("" : "+a"(va[dt]));
         };
         // raw scores of the pair being turned into weights (the scale sits in
         // the exponent); -inf past a row's limit
@@ -497,9 +498,10 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         auto lane_max = [&](const float (&v)[8]) {
             return fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
         };
-        if (npair > 0) issue(0);
+        if (npair > 0) issue(0, page_of(0));
         if (threadIdx.x == 0) next = claim();  // overlaps the first pairs' round trip
-        for (int i = 1; i < min(npair, kStages - 1); ++i) issue(i);
+        for (int i = 1; i < min(npair, kStages - 1); ++i) issue(i, page_of(i));
+        int nblk = npair > 0 ? page_of(kStages - 1) : 0;  // the next refill's page
         // pair 0's scores set the rows' reference maxima (key 0 is visible to
         // every row, so they are finite)
         if (npair > 0) {
@@ -549,15 +551,26 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                 else wait_vmcnt<0>();
                 wg_barrier();
             }
+            // K of pair j + 1 first (the score MFMAs need it first), then V of
+            // pair j; both are pinned to AGPRs only where the MFMAs take them,
+            // so the LDS reads all issue before the first wait
+            bf16x8 kop[2][KK];
+            if (nxt) read_k(j + 1, kop);
             u32x4 va[DT];
             if (IN || 2 * (j + 1) * BS <= vlim) read_v.template operator()<false>(j, va);
             else read_v.template operator()<true>(j, va);
-            bf16x8 kop[2][KK];
-            if (nxt) read_k(j + 1, kop);
-            if (IN || j + kStages - 1 < npair) issue(j + kStages - 1);
+            if (IN || j + kStages - 1 < npair) {
+                issue(j + kStages - 1, nblk);
+                nblk = page_of(j + kStages);
+            }
 
             f32x4 sacc[2][T];  // pair j + 1's scores
             bf16x8 pb[T];      // pair j's weights
+            if (nxt)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+a"(kop[h][kk]));
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 if (nxt)
@@ -577,6 +590,8 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
             }
             float mx[T];
             bool grow = false;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) asm volatile("" : "+a"(va[dt]));
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 lsum[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[t], lsum[t], 0, 0, 0);
