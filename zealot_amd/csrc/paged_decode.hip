@@ -258,7 +258,7 @@ __device__ __forceinline__ int shared_pair_pages(const Params &p, int g, int k) 
 
 __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
     __shared__ int hist[2048];  // bin j = kMaxItemPages - pages (longest first)
-    __shared__ int sums[1024];
+    __shared__ int wsum[16];
     const int t = threadIdx.x;
     hist[2 * t] = 0;
     hist[2 * t + 1] = 0;
@@ -277,21 +277,13 @@ __global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
         for (int k = 0; k < np; ++k) atomicAdd(&hist[kMaxItemPages - shared_pair_pages(p, g, k)], 1);
     }
     __syncthreads();
-    // exclusive scan of the bins, two per thread (block scan of the pair sums)
+    // exclusive scan of the bins, two per thread (each thread rewrites only
+    // its own two, so no barrier between reading and writing them)
     const int a = hist[2 * t], b = hist[2 * t + 1];
-    sums[t] = a + b;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int v = t >= o ? sums[t - o] : 0;
-        __syncthreads();
-        sums[t] += v;
-        __syncthreads();
-    }
-    const int base = sums[t] - (a + b);
-    __syncthreads();
+    int total_pairs;
+    const int base = zk::block_exclusive_scan_1024(a + b, wsum, &total_pairs);
     hist[2 * t] = base;
     hist[2 * t + 1] = base + a;
-    const int total_pairs = sums[1023];
     __syncthreads();
     // an item's descriptor carries the block ids of its first pages, so the
     // decode issues them without waiting for the item's table entries

@@ -101,33 +101,52 @@ __device__ __forceinline__ int tile_pages(const PParams &p, int n, int qt) {
 
 __global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
     __shared__ int hist[kMaxBins];
-    __shared__ int sums[1024];
+    __shared__ int wsum[16];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     hist[2 * t] = 0;
     hist[2 * t + 1] = 0;
-    // effective contexts: one wave per sequence, eight loads in flight per lane
-    for (int n = wave; n < p.num_seqs; n += 16) {
-        const int want = p.start[n] + chunk_len(p, n);
-        const int cap = p.max_blocks * p.block_size;
-        const int len = max(0, min(want, cap));
-        const int pages = (len + p.block_size - 1) / p.block_size;
-        const int32_t *row = p.bt + (size_t)n * p.max_blocks;
-        int first_bad = pages;
-        for (int i0 = 0; i0 < pages && first_bad == pages; i0 += 8 * kWave) {
-            int32_t b[8];
+    // effective contexts: one wave per sequence, the first 512 table entries
+    // of four sequences in flight at once (eight unconditional loads a lane
+    // each, the index clamped into the row), longer walks in further rounds
+    constexpr int kSeqsAtOnce = 4;
+    const int cap = p.max_blocks * p.block_size;
+    for (int n0 = wave; n0 < p.num_seqs; n0 += 16 * kSeqsAtOnce) {
+        int32_t b[kSeqsAtOnce][8];
+        int len[kSeqsAtOnce], pages[kSeqsAtOnce];
+#pragma unroll
+        for (int q = 0; q < kSeqsAtOnce; ++q) {
+            const int n = min(n0 + 16 * q, p.num_seqs - 1);
+            len[q] = max(0, min(p.start[n] + chunk_len(p, n), cap));
+            pages[q] = (len[q] + p.block_size - 1) / p.block_size;
+            const int32_t *row = p.bt + (size_t)n * p.max_blocks;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) b[q][j] = row[min(j * kWave + lane, max(pages[q] - 1, 0))];
+        }
+#pragma unroll
+        for (int q = 0; q < kSeqsAtOnce; ++q) {
+            const int n = n0 + 16 * q;
+            if (n >= p.num_seqs) break;
+            int first_bad = pages[q];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int i = i0 + j * kWave + lane;
-                b[j] = i < pages ? row[i] : 0;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + j * kWave + lane;
-                if (i < pages && (b[j] < 0 || (int64_t)b[j] >= p.num_blocks)) first_bad = min(first_bad, i);
+                const int i = j * kWave + lane;
+                if (i < pages[q] && (b[q][j] < 0 || (int64_t)b[q][j] >= p.num_blocks)) first_bad = min(first_bad, i);
             }
             for (int o = 32; o > 0; o >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, o));
+            const int32_t *row = p.bt + (size_t)n * p.max_blocks;
+            for (int i0 = 8 * kWave; i0 < pages[q] && first_bad == pages[q]; i0 += 8 * kWave) {
+                int32_t c[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) c[j] = row[min(i0 + j * kWave + lane, pages[q] - 1)];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int i = i0 + j * kWave + lane;
+                    if (i < pages[q] && (c[j] < 0 || (int64_t)c[j] >= p.num_blocks)) first_bad = min(first_bad, i);
+                }
+                for (int o = 32; o > 0; o >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, o));
+            }
+            if (lane == 0) p.eff[n] = min(len[q], first_bad * p.block_size);
         }
-        if (lane == 0) p.eff[n] = min(len, first_bad * p.block_size);
     }
     __threadfence_block();
     __syncthreads();
@@ -145,20 +164,13 @@ __global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
         if (tiles > 0) atomicAdd(&hist[key(n, kvh, tiles)], tiles);
     }
     __syncthreads();
+    // exclusive scan of the bins, two per thread (each thread rewrites only
+    // its own two, so no barrier between reading and writing them)
     const int a = hist[2 * t], b = hist[2 * t + 1];
-    sums[t] = a + b;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int v = t >= o ? sums[t - o] : 0;
-        __syncthreads();
-        sums[t] += v;
-        __syncthreads();
-    }
-    const int base = sums[t] - (a + b);
-    __syncthreads();
+    int total;
+    const int base = zk::block_exclusive_scan_1024(a + b, wsum, &total);
     hist[2 * t] = base;
     hist[2 * t + 1] = base + a;
-    const int total = sums[1023];
     __syncthreads();
     if (t < kXcds) {  // segment of each XCD queue; its first waves take items statically
         const int start = hist[t * kXcdBins], end = t + 1 < kXcds ? hist[(t + 1) * kXcdBins] : total;

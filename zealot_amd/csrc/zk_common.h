@@ -206,6 +206,32 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
+// Exclusive prefix sum of one int per thread over a 1024-thread workgroup:
+// a shuffle scan inside each of the 16 waves, then the wave totals through
+// `wsum` (16 ints of LDS) after one barrier.  Every thread must call it.
+// Returns the sum of the values of the threads before this one; *total gets
+// the sum over the workgroup.
+__device__ __forceinline__ int block_exclusive_scan_1024(int v, int *wsum, int *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o);
+        if (lane >= o) incl += u;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const int s = wsum[w];
+        before += w < wave ? s : 0;
+        all += s;
+    }
+    *total = all;
+    return before + incl - v;
+}
+
 // Sum of N consecutive f32x4 over the k ranges of a split-k product:
 // acc[q] = p[q] + p[plane + q] + ... in range order (the order every reduce
 // of these sums uses, so results do not depend on which kernel adds them).
