@@ -256,7 +256,10 @@ __device__ __forceinline__ int shared_pair_pages(const Params &p, int g, int k) 
     return max(0, min(p.shared_part_pages, p.sg_pages[g] - k * p.shared_part_pages));
 }
 
-__global__ void __launch_bounds__(1024) plan_kernel(Params p, int num_seqs) {
+// At most 64 VGPRs a lane, so that its 16 waves fit beside attention waves
+// already resident (four a SIMD beside one decode or prefill wave).
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8)))
+plan_kernel(Params p, int num_seqs) {
     __shared__ int hist[2048];  // bin j = kMaxItemPages - pages (longest first)
     __shared__ int wsum[16];
     const int t = threadIdx.x;

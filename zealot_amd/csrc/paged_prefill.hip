@@ -99,16 +99,22 @@ __device__ __forceinline__ int tile_pages(const PParams &p, int n, int qt) {
     return (vis + p.block_size - 1) / p.block_size;
 }
 
-__global__ void __launch_bounds__(1024) prefill_plan_kernel(PParams p) {
+// At most 64 VGPRs a lane (eight waves a SIMD): in a mixed step this kernel
+// starts while the decode's waves (about 200 VGPRs) hold half of every CU,
+// and its 16 waves need four per SIMD beside them; with more registers it
+// could not be placed until the decode ended, and the chunks' attention would
+// run after the decode instead of beside it.
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8)))
+prefill_plan_kernel(PParams p) {
     __shared__ int hist[kMaxBins];
     __shared__ int wsum[16];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     hist[2 * t] = 0;
     hist[2 * t + 1] = 0;
     // effective contexts: one wave per sequence, the first 512 table entries
-    // of four sequences in flight at once (eight unconditional loads a lane
+    // of two sequences in flight at once (eight unconditional loads a lane
     // each, the index clamped into the row), longer walks in further rounds
-    constexpr int kSeqsAtOnce = 4;
+    constexpr int kSeqsAtOnce = 2;
     const int cap = p.max_blocks * p.block_size;
     for (int n0 = wave; n0 < p.num_seqs; n0 += 16 * kSeqsAtOnce) {
         int32_t b[kSeqsAtOnce][8];
