@@ -1114,6 +1114,85 @@ __global__ void __launch_bounds__(kWave) decode_reduce_vec_kernel(Params p) {
         for (int c = 0; c < 4; ++c) store_out(p, (qrow(p, n) * p.num_heads + h) * D + 4 * j + c, acc[c] * inv);
 }
 
+// One wave per (kv-head, sequence): the G query heads of the kv-head at once
+// (LPH = 64 / G lanes a head, F = G * D / 64 floats a lane), so a launch has
+// Hkv / H of the waves of decode_reduce_vec_kernel.  Each lane reads its
+// head's (m, l) of every partition itself (no cross-lane reductions) and the
+// first C partitions' partials with them, one memory round trip; partitions
+// are added in slot order.
+template <int D, int G>
+__global__ void __launch_bounds__(kWave) decode_reduce_kv_kernel(Params p) {
+    constexpr int LPH = kWave / G, F = G * D / kWave, F4 = F / 4;
+    constexpr int C = 8;  // partitions loaded with the (m, l)
+    static_assert(F % 4 == 0 && kWave % G == 0, "lane layout");
+    const int kvh = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
+    const int ns = shared_parts_of(p, n);
+    const int nparts = ns + private_parts_of(p, n);
+    if (ns == 0 && nparts <= 1) return;  // written by the partition kernel
+    const int hh = lane / LPH, d0 = (lane % LPH) * F;
+    const int qh = qhead_of(p, kvh, hh, G);
+    const size_t base = ((size_t)n * p.num_heads + qh) * p.max_parts;
+    float2 ml[C];
+    f32x4 x[C][F4];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        if (i < nparts) {
+            ml[i] = p.ml[base + i];
+#pragma unroll
+            for (int k = 0; k < F4; ++k) x[i][k] = *reinterpret_cast<const f32x4 *>(p.po + (base + i) * D + d0 + 4 * k);
+        } else {
+            ml[i] = make_float2(-INFINITY, 0.0f);
+        }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < C; ++i) M = fmaxf(M, ml[i].x);
+    for (int i = C; i < nparts; ++i) M = fmaxf(M, p.ml[base + i].x);
+    auto weight = [&](float2 v) { return v.x == -INFINITY ? 0.0f : exp2f(v.x - M); };
+    float L = 0.0f;
+    f32x4 acc[F4];
+#pragma unroll
+    for (int k = 0; k < F4; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+        if (i < nparts) {
+            const float w = weight(ml[i]);
+            L += ml[i].y * w;
+#pragma unroll
+            for (int k = 0; k < F4; ++k)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[k][c] = fmaf(w, x[i][k][c], acc[k][c]);
+        }
+    for (int i = C; i < nparts; ++i) {
+        const float2 v = p.ml[base + i];
+        const float w = weight(v);
+        L += v.y * w;
+#pragma unroll
+        for (int k = 0; k < F4; ++k) {
+            const f32x4 y = *reinterpret_cast<const f32x4 *>(p.po + (base + i) * D + d0 + 4 * k);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[k][c] = fmaf(w, y[c], acc[k][c]);
+        }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const size_t ob = (qrow(p, n) * p.num_heads + qh) * D + d0;
+    if (p.q_f32) {
+#pragma unroll
+        for (int k = 0; k < F4; ++k) {
+            const f32x4 y = acc[k] * inv;
+            __builtin_memcpy((float *)p.out + ob + 4 * k, &y, sizeof(y));
+        }
+    } else {
+        uint32_t v[F / 2];
+#pragma unroll
+        for (int k = 0; k < F4; ++k) {
+            v[2 * k] = bf16x2_rne(acc[k][0] * inv, acc[k][1] * inv);
+            v[2 * k + 1] = bf16x2_rne(acc[k][2] * inv, acc[k][3] * inv);
+        }
+        __builtin_memcpy((uint16_t *)p.out + ob, v, sizeof(v));
+    }
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
@@ -1417,7 +1496,11 @@ int zk::paged_decode(const void *q, zk_dtype q_dtype, const void *k_pool, const 
     if (reduce) {
         dim3 rgrid(num_heads, num_seqs);
         KernelTimer timer("decode_reduce", s);
-        if (head_dim == 128) decode_reduce_vec_kernel<128><<<rgrid, kWave, 0, s>>>(p);
+        const dim3 kgrid(num_kv_heads, num_seqs);
+        if (head_dim == 128 && G == 4) decode_reduce_kv_kernel<128, 4><<<kgrid, kWave, 0, s>>>(p);
+        else if (head_dim == 128 && G == 8) decode_reduce_kv_kernel<128, 8><<<kgrid, kWave, 0, s>>>(p);
+        else if (head_dim == 128 && G == 2) decode_reduce_kv_kernel<128, 2><<<kgrid, kWave, 0, s>>>(p);
+        else if (head_dim == 128) decode_reduce_vec_kernel<128><<<rgrid, kWave, 0, s>>>(p);
         else if (head_dim == 64) decode_reduce_vec_kernel<64><<<rgrid, kWave, 0, s>>>(p);
         else if (head_dim == 256) decode_reduce_vec_kernel<256><<<rgrid, kWave, 0, s>>>(p);
         else decode_reduce_kernel<<<rgrid, kWave, 0, s>>>(p);
