@@ -1424,10 +1424,10 @@ int zk_cache_attention_batch(zk_kv_cache *c, size_t layer, const char *const *id
     if (mfma_prefill) {
         // chunks first, on the side stream when decodes share the step, so
         // the two kernels overlap; the cache stream waits for both at the end.
-        // Neither kernel fits beside the other on one SIMD (their registers
-        // add up to more than a SIMD holds), so each gets half of every CU:
-        // one two-wave prefill workgroup and two decode waves (the HBM-bound
-        // decode streams as fast on two waves a CU as on four)
+        // Each gets part of every CU: one four-wave prefill workgroup (a wave
+        // on each SIMD) and two decode waves (the HBM-bound decode streams as
+        // fast on two waves a CU as on four; four, one beside each prefill
+        // wave, measured 0.78 against 0.73 ms a mixed step)
         hipStream_t ps = c->stream;
         int pre_groups = 0, dec_waves = 0;
         if (!dec.empty()) {

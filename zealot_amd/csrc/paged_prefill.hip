@@ -19,7 +19,8 @@
 //       sort on their last tile's pages) and a group's tiles back to back,
 //       longest first.
 //   prefill_mfma_kernel<KV, D, G>  bf16 / fp8 pools, D in {64, 128}, G in
-//       {1, 2, 4, 8}, block_size 16: persistent two-wave workgroups take items
+//       {1, 2, 4, 8}, block_size 16: persistent four-wave workgroups (one wave
+//       a SIMD, two workgroups a CU, so two waves share each SIMD) take items
 //       from their XCD's queue (workgroups are dispatched round-robin over the
 //       8 XCDs), then from the others' when it runs dry.  An item holds 128
 //       query rows -- TQ = 128/G chunk tokens x the G heads of one kv-head,
@@ -47,8 +48,9 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWave = 64;
-constexpr int kWaves = 2;             // waves per workgroup, one per SIMD
-constexpr int kWaveRows = 64;         // query rows per wave (4 MFMA tiles)
+constexpr int kWaves = 4;             // waves per workgroup, one per SIMD
+constexpr int kWavesPerSimd = 2;      // workgroups per CU: two waves share each SIMD
+constexpr int kWaveRows = 32;         // query rows per wave (2 MFMA tiles)
 constexpr int kRows = kWaves * kWaveRows;  // query rows per item
 constexpr int kTiles = kWaveRows / 16;
 constexpr int kStages = 4;            // page pairs in LDS: the one computed on, the rest in flight
@@ -235,7 +237,10 @@ template <>
 struct LdsVec<4> { typedef uint32_t T; };
 
 template <int KV, int D, int G>
-__global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p) {
+// At most 256 registers a lane (two waves a SIMD): the operands stay in
+// VGPRs, so the kernel uses no AGPRs.
+__global__ void __launch_bounds__(kWave * kWaves) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd)))
+prefill_mfma_kernel(PParams p) {
     constexpr int BS = 16;
     constexpr int ELT = KV == ZK_BF16 ? 2 : 1;
     constexpr int DG = D / 4;         // head dims per lane group in QK
@@ -256,8 +261,8 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
     __shared__ __attribute__((aligned(16))) char lds[kStages][2][2][PAGE];  // [stage][page of the pair][K|V]
     __shared__ int item_bcast;
 
-    // wave w computes rows 64 w .. 64 w + 63 of every item and loads page w
-    // of every pair; both waves read both pages
+    // wave w computes rows 32 w .. 32 w + 31 of every item and loads one
+    // (page, K|V) part of every pair; every wave reads both pages
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave, col = lane & 15, grp = lane >> 4;
     const int H = p.num_heads, Hkv = p.num_kv_heads;
@@ -351,12 +356,12 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                 for (int kk = 0; kk < KK; ++kk) qf[t][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
             }
         }
-        // Q fragments live in AGPRs (MFMA reads its A/B operands from either
-        // file): VGPRs hold the accumulators and the page temporaries
+        // the Q fragments are ready here (their loads' wait stays out of the
+        // page loop)
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+a"(qf[t][kk]));
+            for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+v"(qf[t][kk]));
         float sl2 = p.scale_log2, vscale = 1.0f;
         if constexpr (KV == ZK_FP8_E4M3) {
             sl2 *= p.k_scales[(size_t)n * Hkv + kvh];
@@ -371,24 +376,26 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         const size_t block_bytes = (size_t)PAGE * Hkv;
         // Pages go through LDS in pairs: 32 keys per PV step feed the
         // 16x16x32 MFMA (the 16x16x16 form runs at half its rate).  Wave w
-        // loads page w of every pair into the pair's stage.  A missing second
-        // page (odd page count) is loaded as a copy of the first, so both
-        // waves issue the same loads per pair; its keys lie past every row's
+        // loads the K (w even) or V (w odd) of page w / 2 of every pair into
+        // the pair's stage.  A missing second
+        // page (odd page count) is loaded as a copy of the first, so every
+        // wave issues the same loads per pair; its keys lie past every row's
         // limit and its V rows are zeroed below.
-        // this wave's page of pair pj (its K and V parts are one page's)
-        static_assert(PARTS == 2, "a wave loads the K and V of one page of each pair");
-        auto page_of = [&](int pj) { return trow[min(2 * pj + w, np - 1)]; };
+        // this wave's page of pair pj (waves 2 h and 2 h + 1 load page h's K
+        // and V)
+        static_assert(PARTS == 1, "a wave loads one (page, K|V) part of each pair");
+        auto page_of = [&](int pj) { return trow[min(2 * pj + (w >> 1), np - 1)]; };
         // blk = page_of(pj), read one pair ahead: waiting for a scalar load
         // also waits for every LDS read issued before it
         auto issue = [&](int pj, int blk) {
             const int stg = pj & (kStages - 1);
 #pragma unroll
             for (int q = 0; q < PARTS; ++q) {
-                const int part = PARTS * w + q, kind = part & 1;  // K or V of this wave's page
+                const int part = PARTS * w + q, kind = part & 1, pg = part >> 1;  // this wave's page, K or V
                 const char *src = (kind ? vbase : kbase) + (size_t)blk * block_bytes;
 #pragma unroll
                 for (int j = 0; j < LPK; ++j)
-                    g2l16(src + (kind ? vg[j] : kg[j]), (lds_void *)(lds[stg][w][kind] + 1024 * j));
+                    g2l16(src + (kind ? vg[j] : kg[j]), (lds_void *)(lds[stg][pg][kind] + 1024 * j));
             }
         };
         f32x4 o[DT][T];
@@ -413,7 +420,7 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
         // limit (rows are token-major, limits grow with the row)
         const int open = min(p.causal ? st + qt * p.tq + 1 : st + len, eff) / BS / 2;
 
-        // K of pair pj as MFMA A operands (AGPRs: the MFMAs read them there)
+        // K of pair pj as MFMA A operands
         auto read_k = [&](int pj, bf16x8 (&kop)[2][KK]) {
             const int stg = pj & (kStages - 1);
 #pragma unroll
@@ -570,8 +577,8 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
                 wg_barrier();
             }
             // K of pair j + 1 first (the score MFMAs need it first), then V of
-            // pair j; both are pinned to AGPRs only where the MFMAs take them,
-            // so the LDS reads all issue before the first wait
+            // pair j; both are pinned only where the MFMAs take them, so the
+            // LDS reads all issue before the first wait
             bf16x8 kop[2][KK];
             if (nxt) read_k(j + 1, kop);
             u32x4 va[DT];
@@ -588,7 +595,7 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
-                    for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+a"(kop[h][kk]));
+                    for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+v"(kop[h][kk]));
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 if (nxt)
@@ -609,7 +616,7 @@ __global__ void __launch_bounds__(kWave * kWaves) prefill_mfma_kernel(PParams p)
             float mx[T];
             bool grow = false;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) asm volatile("" : "+a"(va[dt]));
+            for (int dt = 0; dt < DT; ++dt) asm volatile("" : "+v"(va[dt]));
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 lsum[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[t], lsum[t], 0, 0, 0);
@@ -722,13 +729,13 @@ bool launch_g(const PParams &p, hipStream_t s, int G) {
     }
 }
 
-// persistent workgroups: one wave per SIMD
+// persistent workgroups: kWavesPerSimd waves a SIMD
 int persistent_groups() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    return cus * (4 / kWaves);
+    return cus * kWavesPerSimd * 4 / kWaves;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
