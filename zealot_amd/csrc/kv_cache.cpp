@@ -130,6 +130,13 @@ struct DeviceGuard {
 
 }  // namespace
 
+// Prefix subgroups of a decode batch (plan_sharing): each sequence's shared
+// pages, the members of every subgroup ([nsg][32], -1 padded) and its pages.
+struct SharePlan {
+    std::vector<int32_t> seq_pb, sg_members, sg_pages;
+    long total_pages = 0;
+};
+
 struct zk_kv_cache {
     size_t num_blocks = 0, block_size = 0, num_layers = 0, num_kv_heads = 0, head_dim = 0;
     int dtype = ZK_F32;
@@ -165,6 +172,13 @@ struct zk_kv_cache {
     uint64_t dec_epoch = ~0ull;
     size_t dec_stride = 0;
     std::vector<const SeqState *> dec_ids;
+    // Prefix-sharing cache: the last grouping and what it was made from
+    // (epoch, batch, member cap, each sequence's fully written pages).
+    SharePlan sh_plan;
+    uint64_t sh_epoch = ~0ull;
+    int sh_cap = 0;
+    std::vector<const SeqState *> sh_ids;
+    std::vector<size_t> sh_full;
     // Second stream for the chunk half of a mixed attention batch, so the
     // MFMA-bound prefill runs beside the HBM-bound decode (default priority).
     hipStream_t side = nullptr;
@@ -289,7 +303,7 @@ int cow_blocks(zk_kv_cache *c, const std::vector<std::pair<SeqState *, size_t>> 
     std::vector<int32_t> pairs(2 * n);
     for (size_t i = 0; i < n; ++i) {
         SeqState &s = *tg[i].first;
-        if (int rc = zk_bm_allocate(s.bm, &fresh[i])) {
+        if (zk_bm_allocate(s.bm, &fresh[i]) != ZK_OK) {
             const zk::ErrorSnapshot saved = zk::save_error();
             for (size_t j = 0; j < i; ++j) (void)zk_bm_free(tg[j].first->bm, fresh[j]);
             return zk::restore_error(saved);
@@ -454,23 +468,17 @@ constexpr size_t kMinSharedPages = 16;
 
 constexpr int kSgStride = 32;  // member slots per subgroup (the kernel's layout)
 
-struct SharePlan {
-    std::vector<int32_t> seq_pb, sg_members, sg_pages;  // sg_members: [nsg][kSgStride], -1 padded
-    long total_pages = 0;
-};
-
-void plan_sharing(const std::vector<const SeqState *> &seqs, size_t layer, size_t bs, int cap, SharePlan &out) {
+// full[i]: the pages of sequence i fully written at the layer
+void plan_sharing(const std::vector<const SeqState *> &seqs, const std::vector<size_t> &full, int cap,
+                  SharePlan &out) {
     const int n = (int)seqs.size();
     out.seq_pb.assign(n, 0);
     out.sg_members.clear();
     out.sg_pages.clear();
     out.total_pages = 0;
-    std::vector<size_t> full(n);
     std::vector<std::pair<uint64_t, int>> keyed;
-    for (int i = 0; i < n; ++i) {
-        full[i] = std::min(seqs[i]->handles.size(), seqs[i]->layer_len[layer] / bs);
+    for (int i = 0; i < n; ++i)
         if (full[i] >= kMinSharedPages) keyed.emplace_back(seqs[i]->handles[0].block_id, i);
-    }
     std::sort(keyed.begin(), keyed.end());
     for (size_t a = 0; a < keyed.size();) {
         size_t b = a;
@@ -751,7 +759,7 @@ int zk_cache_fork_seq(zk_kv_cache *c, const char *parent, const char *child) {
         for (size_t i = 0; i < done; ++i) (void)zk_bm_free(p->bm, p->handles[i]);
         return zk::restore_error(saved);
     }
-    if (int rc = flush_tables(c)) {  // the parent's row is copied below
+    if (flush_tables(c) != ZK_OK) {  // the parent's row is copied below
         const zk::ErrorSnapshot saved = zk::save_error();
         for (const auto &h : p->handles) (void)zk_bm_free(p->bm, h);
         return zk::restore_error(saved);
@@ -1032,7 +1040,6 @@ int zk_cache_swap_in(zk_kv_cache *c, const char *const *ids, int n, zk_block_man
     if (!c || (n > 0 && !ids)) return set_error(ZK_ERR_INVALID_ARGUMENT, "Internal error: KVCache swap_in: NULL argument");
     if (n <= 0) return ZK_OK;
     std::vector<SeqState *> seqs((size_t)n);
-    size_t need = 0;
     for (int i = 0; i < n; ++i) {
         if (int rc = find_seq(c, ids[i], &seqs[i])) return rc;
         for (int j = 0; j < i; ++j)
@@ -1052,7 +1059,6 @@ int zk_cache_swap_in(zk_kv_cache *c, const char *const *ids, int n, zk_block_man
             if (bm && s.bm && bm != s.bm)
                 return set_error(ZK_ERR_FAILED_PRECONDITION,
                                  "Failed precondition: KVCache swap_in: sequence uses another BlockManager");
-            need += s.host_slots.size();
         }
     }
     DeviceGuard g(c->device);
@@ -1064,7 +1070,7 @@ int zk_cache_swap_in(zk_kv_cache *c, const char *const *ids, int n, zk_block_man
         zk_block_manager *m = s.bm ? s.bm : bm;
         for (size_t b = 0; b < s.host_slots.size(); ++b) {
             zk_block_handle h;
-            if (int rc = zk_bm_allocate(m, &h)) {
+            if (zk_bm_allocate(m, &h) != ZK_OK) {
                 const zk::ErrorSnapshot saved = zk::save_error();
                 for (int j = 0; j <= i; ++j)
                     for (const auto &x : fresh[j]) (void)zk_bm_free(seqs[j]->bm ? seqs[j]->bm : bm, x);
@@ -1184,11 +1190,29 @@ int decode_batch(zk_kv_cache *c, size_t layer, const std::vector<const SeqState 
         c->dec_ids = seqs;
         c->dec_stride = stride;
     }
-    // Shared prefixes of forked sequences (bf16 MFMA shapes only).
-    SharePlan sp;
+    // Shared prefixes of forked sequences (bf16 MFMA shapes only).  The
+    // grouping depends on the tables (epoch), the batch and the pages each
+    // sequence has fully written at the layer; the layers of one step
+    // usually agree on all three, so the last grouping is kept and reused.
+    static const SharePlan no_sharing;
+    const SharePlan *spp = &no_sharing;
     if (share && !lens_in && num_heads > 0 && num_heads % (int)H == 0 &&
-        zk::paged_decode_shares_prefixes(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads, (int)H))
-        plan_sharing(seqs, layer, c->block_size, 32 / (num_heads / (int)H), sp);
+        zk::paged_decode_shares_prefixes(c->dtype, (int)c->head_dim, (int)c->block_size, num_heads, (int)H)) {
+        const int cap = 32 / (num_heads / (int)H);
+        std::vector<size_t> full(n);
+        for (int i = 0; i < n; ++i)
+            full[i] = std::min(seqs[i]->handles.size(), seqs[i]->layer_len[layer] / c->block_size);
+        if (c->sh_epoch != c->epoch || c->sh_cap != cap || c->sh_ids != seqs || c->sh_full != full) {
+            c->sh_epoch = ~0ull;
+            plan_sharing(seqs, full, cap, c->sh_plan);
+            c->sh_epoch = c->epoch;
+            c->sh_cap = cap;
+            c->sh_ids = seqs;
+            c->sh_full = std::move(full);
+        }
+        spp = &c->sh_plan;
+    }
+    const SharePlan &sp = *spp;
     const int nsg = (int)sp.sg_pages.size();
     if (append && nsg)  // the appended token's page is written by its sequence's own item, never a shared one
         for (int i = 0; i < n; ++i)
