@@ -93,8 +93,10 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 // PART: the input row is not read from x but is the projection output a
 // split-k skinny product leaves as f32 sums [splits][rows][dim] in `partial`:
 // x = T(sum over ranges, in range order), the value its reduce kernel would
-// have stored (VEC > 1 only).
-template <typename T, int VEC, int MAXV, bool PART = false>
+// have stored (VEC > 1 only).  FOLD: the ranges loaded up front (at least
+// `splits` where the register budget allows: a range past `splits` is a
+// wasted load instruction).
+template <typename T, int VEC, int MAXV, bool PART = false, int FOLD = kFoldLoads>
 __global__ void __launch_bounds__(kThreads)
 rms_norm_kernel(const T *x, const T *residual, const T *__restrict__ w, T *out, T *res_out,
                 const int64_t *__restrict__ rows, int dim, float eps,  // out may be x, res_out residual
@@ -110,7 +112,7 @@ rms_norm_kernel(const T *x, const T *residual, const T *__restrict__ w, T *out, 
         constexpr int N4 = VEC / 4;
         // ranges loaded up front, within a budget of 32 16-byte loads a thread
         constexpr int FB = 32 / (MAXV * N4);
-        constexpr int FL = FB < 1 ? 1 : FB > kFoldLoads ? kFoldLoads : FB;
+        constexpr int FL = FB < 1 ? 1 : FB > FOLD ? FOLD : FB;
         const size_t plane4 = (size_t)gridDim.x * dim / 4;
         f32x4 t[MAXV][FL][N4];
         float a[MAXV][VEC];
@@ -314,12 +316,21 @@ int norm_dispatch(int rows_n, const void *x, const void *res, const void *w, voi
     return 0;
 }
 
+template <int MAXV, int FOLD>
+void launch_norm_fold(int rows_n, const float *partial, int splits, const void *res, const void *w, void *out,
+                      void *res_out, int dim, float eps, hipStream_t s) {
+    rms_norm_kernel<uint16_t, 8, MAXV, true, FOLD><<<rows_n, kThreads, 0, s>>>(
+        nullptr, (const uint16_t *)res, (const uint16_t *)w, (uint16_t *)out, (uint16_t *)res_out, nullptr, dim, eps,
+        partial, splits);
+}
+
+// ranges loaded up front: splits rounded up to 2, 4 or 8
 template <int MAXV>
 void launch_norm_partials(int rows_n, const float *partial, int splits, const void *res, const void *w, void *out,
                           void *res_out, int dim, float eps, hipStream_t s) {
-    rms_norm_kernel<uint16_t, 8, MAXV, true><<<rows_n, kThreads, 0, s>>>(
-        nullptr, (const uint16_t *)res, (const uint16_t *)w, (uint16_t *)out, (uint16_t *)res_out, nullptr, dim, eps,
-        partial, splits);
+    if (splits <= 2) launch_norm_fold<MAXV, 2>(rows_n, partial, splits, res, w, out, res_out, dim, eps, s);
+    else if (splits <= 4) launch_norm_fold<MAXV, 4>(rows_n, partial, splits, res, w, out, res_out, dim, eps, s);
+    else launch_norm_fold<MAXV, kFoldLoads>(rows_n, partial, splits, res, w, out, res_out, dim, eps, s);
 }
 
 }  // namespace

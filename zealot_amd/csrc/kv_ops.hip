@@ -70,6 +70,8 @@ append_copy_kernel(const char *__restrict__ k, const char *__restrict__ v, char 
 // row; q columns [0, qcols) go to q_out (row stride ldq), the K and V
 // columns (Hkv * D each, after them) to the bf16 pools at slot_mapping[t],
 // bit for bit the reduce kernel followed by the append of its K / V columns.
+// FOLD: ranges loaded up front (splits rounded up to 2, 4 or 8).
+template <int FOLD>
 __global__ void __launch_bounds__(kThreads)
 append_split_sums_kernel(const float *__restrict__ partial, int splits, uint32_t rows, uint32_t cols8,
                          uint16_t *__restrict__ q_out, uint64_t ldq, uint32_t qcols, char *__restrict__ k_pool,
@@ -82,7 +84,7 @@ append_split_sums_kernel(const float *__restrict__ partial, int splits, uint32_t
     const f32x4 *p = reinterpret_cast<const f32x4 *>(partial + (size_t)t * cols8 * 8 + c);
     const int64_t slot = c < qcols ? 0 : slots[t];  // loaded beside the sums
     f32x4 ab[2];
-    sum_ranges(p, plane / 4, splits, ab);
+    sum_ranges<2, FOLD>(p, plane / 4, splits, ab);
     const f32x4 a = ab[0], b = ab[1];
     const uint4 v = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])};
     if (c < qcols) {
@@ -542,7 +544,10 @@ int zk::append_split_sums(void *k_pool, void *v_pool, const float *partial, int 
     hipStream_t s = (hipStream_t)stream;
     const uint32_t cols8 = (uint32_t)(cols / 8), total = (uint32_t)(rows * cols8);
     KernelTimer timer("append", s);
-    append_split_sums_kernel<<<(total + kThreads - 1) / kThreads, kThreads, 0, s>>>(
+    auto kernel = splits <= 2 ? append_split_sums_kernel<2>
+                  : splits <= 4 ? append_split_sums_kernel<4>
+                                : append_split_sums_kernel<kFoldLoads>;
+    kernel<<<(total + kThreads - 1) / kThreads, kThreads, 0, s>>>(
         partial, splits, (uint32_t)rows, cols8, (uint16_t *)q_out, (uint64_t)ldq, (uint32_t)qcols, (char *)k_pool,
         (char *)v_pool, slot_mapping, (uint32_t)num_kv_heads, (uint32_t)head_dim, (uint32_t)block_size,
         num_blocks * block_size);

@@ -240,25 +240,26 @@ __device__ __forceinline__ int block_exclusive_scan_1024(int v, int *wsum, int *
 // loads are unconditional (a range past `splits` re-reads range 0, a cache
 // hit whose value is not used): guarded loads make the compiler wait for each
 // group before the next.  The sum selects instead of adding zero, which keeps
-// a -0 sum's sign.
+// a -0 sum's sign.  FOLD (at most kFoldLoads) lowers the up-front loads for a
+// caller that knows `splits` is small: loads past `splits` are wasted issue.
 constexpr int kFoldLoads = 8;
 __device__ __forceinline__ size_t fold_offset(int r, int splits, size_t plane) {
     return r < splits ? (size_t)r * plane : 0;
 }
-template <int N>
+template <int N, int FOLD = kFoldLoads>
 __device__ __forceinline__ void sum_ranges(const f32x4 *p, size_t plane, int splits, f32x4 (&acc)[N]) {
-    f32x4 t[kFoldLoads][N];
+    f32x4 t[FOLD][N];
 #pragma unroll
-    for (int r = 0; r < kFoldLoads; ++r)
+    for (int r = 0; r < FOLD; ++r)
 #pragma unroll
         for (int q = 0; q < N; ++q) t[r][q] = p[fold_offset(r, splits, plane) + q];
 #pragma unroll
     for (int q = 0; q < N; ++q) acc[q] = t[0][q];
 #pragma unroll
-    for (int r = 1; r < kFoldLoads; ++r)
+    for (int r = 1; r < FOLD; ++r)
 #pragma unroll
         for (int q = 0; q < N; ++q) acc[q] = r < splits ? acc[q] + t[r][q] : acc[q];
-    for (int r = kFoldLoads; r < splits; ++r)
+    for (int r = FOLD; r < splits; ++r)
 #pragma unroll
         for (int q = 0; q < N; ++q) acc[q] += p[(size_t)r * plane + q];
 }
